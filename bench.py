@@ -1,0 +1,248 @@
+"""Benchmark of the GDN decode and prefill operators on one MI355X.
+
+Prints ONE JSON line.  The headline ``value`` is the decode step at batch
+256 (qk4 / v8 / d128): algorithmic state-stream bytes per second with every
+input already resident in HBM.  The prefill at 32 768 packed tokens
+(8 varlen sequences, qk16 / v32) is reported in the ``prefill`` object of
+the same line.
+
+Work accounting (per v-head and per step):
+* decode bytes: 2 * 128 * 128 * 4 (state read + write) + 2 * 256 (v, o)
+  + 4 (a, b), plus 2 * 256 (q, k) per qk-head;
+* prefill flops per token: 10 * C * d + 6 * d^2 = 180 224 (C = 64, d = 128,
+  dense chunk tiles) -- the conservative qk-shared count 8 C d + 6 d^2 is
+  printed beside it.
+
+Timing: ``--warmup`` untimed steps, then ``--steps`` timed steps bracketed by
+``torch.cuda.synchronize()``; every launch inside the timed region is also
+bracketed by its own pair of HIP events on the launch stream, whose mean is
+the kernel duration the roofline uses.  Decode rotates 4 (state, new_state)
+buffer sets (1 GiB) so the 256 MB Infinity Cache cannot serve the state.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+__graft_entry__.load_package()
+from track_c_gdn_amd import decode as gdec  # noqa: E402
+from track_c_gdn_amd import inputs as ginp  # noqa: E402
+from track_c_gdn_amd import prefill as gpre  # noqa: E402
+
+METRIC = "decode state GB/s (%HBM peak) at B=256; prefill tokens/s (%MFMA) at 32k tok"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+D = 128
+C = 64
+
+
+def decode_bytes(B: int, HQ: int, HV: int) -> int:
+    per_vhead = 2 * D * D * 4 + 2 * D * 2 + 4
+    per_qkhead = 2 * D * 2
+    return B * (HV * per_vhead + HQ * per_qkhead)
+
+
+def prefill_flops(T: int, HV: int, qk_shared: bool = False) -> int:
+    per_tok = (8 if qk_shared else 10) * C * D + 6 * D * D
+    return T * HV * per_tok
+
+
+def _to(x, dev):
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in x.items()}
+
+
+def _traffic(name: str):
+    p = ROOT / "profiles" / f"{name}_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def timed_launches(launch, n_steps: int, warmup: int):
+    """Run ``launch(i)`` warmup + n_steps times; return (total_ms, mean_kernel_ms)."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(n_steps):
+        evs[i][0].record()
+        launch(warmup + i)
+        evs[i][1].record()
+    t1.record()
+    torch.cuda.synchronize()
+    total = t0.elapsed_time(t1)
+    per = [a.elapsed_time(b) for a, b in evs]
+    return total, sum(per) / len(per)
+
+
+def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4):
+    x = ginp.decode_inputs(B, HQ, HV, seed=1001)
+    g = _to(x, dev)
+    states = [g["state"]] + [g["state"].clone() for _ in range(sets - 1)]
+    outs = [torch.empty_like(g["state"]) for _ in range(sets)]
+    o = torch.empty(B, 1, HV, D, dtype=torch.bfloat16, device=dev)
+
+    def launch(i):
+        j = i % sets
+        gdec.gdn_decode(g["q"], g["k"], g["v"], states[j], g["A_log"], g["a"], g["dt_bias"],
+                        g["b"], g["scale"], output=o, new_state=outs[j])
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    nbytes = decode_bytes(B, HQ, HV)
+    return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=nbytes)
+
+
+def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
+    w = ginp.WORKLOADS[name]
+    lens = ginp.workload_lengths(name)
+    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
+    g = _to(x, dev)
+    T = sum(lens)
+    N = len(lens)
+    out = torch.empty(T, w["HV"], D, dtype=torch.bfloat16, device=dev)
+    fs = torch.empty(N, w["HV"], D, D, dtype=torch.float32, device=dev)
+
+    def launch(i):
+        gpre.gdn_prefill(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"], g["dt_bias"],
+                         g["b"], g["cu_seqlens"], g["scale"], output=out, final_state=fs,
+                         validate=False)
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    return dict(total_ms=total_ms, kernel_ms=kern_ms, T=T, N=N, lens=lens, HQ=w["HQ"],
+                HV=w["HV"], flops=prefill_flops(T, w["HV"]),
+                flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True))
+
+
+def cpu_baseline_decode(budget_s=12.0, B=256):
+    """Oracle decode step in fp32 on the host cores (bounded sample of B=256)."""
+    from oracle import gdn_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = ginp.decode_inputs(B, 4, 8, seed=1001)
+    args = [x[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b")]
+    O.decode_step(*args, x["scale"], dtype=torch.float32)          # warmup
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.decode_step(*args, x["scale"], dtype=torch.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    gbs = decode_bytes(B, 4, 8) * n / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{n} fp32 oracle decode steps at B=256 qk4/v8 ({el:.1f} s)"}
+
+
+def cpu_baseline_prefill(budget_s=12.0):
+    """Per-token fp32 oracle recurrence (definition-reference style) on a prefix sample."""
+    from oracle import gdn_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = ginp.prefill_inputs([512], 16, 32, seed=1004, with_state=True)
+    args = [x[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
+    t0 = time.perf_counter()
+    O.prefill_recurrent(*args, x["scale"], dtype=torch.float32)
+    el = time.perf_counter() - t0
+    toks = 512
+    return {"value": round(toks / el, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"512-token sequence, qk16/v32, fp32 per-token oracle recurrence ({el:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the GDN operators shard with no communication "
+              "(per sequence / per head), so a multi-GPU figure is not measured here.",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "decode_b256_qk4_v8", "batch": 256, "qk_heads": 4,
+                       "v_heads": 8, "head_dim": 128, "state": "fp32 [256,8,128,128] k-last",
+                       "state_buffer_sets": 4}}
+
+    if args.only in ("all", "decode"):
+        r = bench_decode(dev, args.steps, args.warmup)
+        ms = r["total_ms"] / args.steps
+        gbs = r["bytes"] / (ms * 1e-3) / 1e9
+        kgbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+        line.update(value=round(gbs, 1), ms_per_step=round(ms, 5))
+        line["roofline"] = {"bound": "hbm", "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
+                            "traffic": _traffic("gdn_decode_kernel_b256"),
+                            "kernel": "gdn_decode_kernel", "bytes_per_launch": r["bytes"],
+                            "kernel_us": round(r["kernel_ms"] * 1e3, 2)}
+        print(f"# decode B=256: {ms*1e3:.2f} us/step, kernel {r['kernel_ms']*1e3:.2f} us, "
+              f"{kgbs:.0f} GB/s ({kgbs/HBM_PEAK_GBS*100:.1f}% of HBM peak)",
+              file=sys.stderr, flush=True)
+
+    if args.only in ("all", "prefill"):
+        try:
+            r = bench_prefill(dev, args.prefill_steps, max(2, args.warmup // 5))
+            ms = r["total_ms"] / args.prefill_steps
+            tfl = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+            line["prefill"] = {
+                "workload": "prefill_varlen8_t32768_qk16_v32", "tokens": r["T"],
+                "seq_lens": r["lens"], "qk_heads": r["HQ"], "v_heads": r["HV"],
+                "tokens_per_s": round(r["T"] / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+                "steps": args.prefill_steps, "dtype": "fp16 MFMA operands, fp32 accumulate",
+                "roofline": {"bound": "mfma", "achieved": round(tfl, 2),
+                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "flops_per_launch": r["flops"],
+                             "frac_qk_shared_count": round(
+                                 r["flops_qk_shared"] / (r["kernel_ms"] * 1e-3) / 1e12
+                                 / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "traffic": _traffic("gdn_prefill_t32768_qk16_v32"),
+                             "kernel_us": round(r["kernel_ms"] * 1e3, 2)},
+            }
+            print(f"# prefill 32k qk16/v32: {ms*1e3:.1f} us/step, {tfl:.1f} TFLOP/s "
+                  f"({tfl/MFMA_BF16_PEAK_TFLOPS*100:.1f}% of bf16 MFMA peak)",
+                  file=sys.stderr, flush=True)
+        except Exception as e:  # prefill not available: say so in the line
+            line["prefill"] = {"error": f"{type(e).__name__}: {e}"}
+            print(f"# prefill failed: {e}", file=sys.stderr, flush=True)
+
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_decode()
+        if args.only in ("all", "prefill") and "error" not in line.get("prefill", {"error": 1}):
+            line["prefill"]["cpu_baseline"] = cpu_baseline_prefill()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,109 @@
+/*
+ * gdn_hip.h -- C ABI of libgdn_hip.so, the MI355X (gfx950) Gated DeltaNet
+ * decode and prefill operators.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers to contiguous row-major tensors; bf16 tensors are
+ *     passed as uint16_t (raw bf16 bits), fp32 as float;
+ *   - the caller owns every buffer; nothing here allocates device memory;
+ *   - work is enqueued on `stream` (a hipStream_t, NULL = default stream),
+ *     asynchronously, with no host synchronisation;
+ *   - return 0 on success, a negative GDN_ERR_* code for an argument error
+ *     (nothing launched), or -(hipError_t) if a launch failed;
+ *   - no C++ exception crosses the ABI.
+ *
+ * Layouts (D = 128 = K = V; qk-head of v-head h is h / (HV/HQ)):
+ *   decode : q, k [B, HQ, D] bf16; v [B, HV, D] bf16; a, b [B, HV] bf16;
+ *            A_log, dt_bias [HV] fp32; state [B, HV, V, K] fp32 (k-last);
+ *            out [B, HV, D] bf16.
+ *   prefill: q, k [T, HQ, D] bf16; v [T, HV, D] bf16; a, b [T, HV] bf16;
+ *            cu_seqlens [N+1] (int64, or int32 when cu_is_int32 != 0);
+ *            state / final_state [N, HV, V, K] fp32; out [T, HV, D] bf16.
+ */
+#ifndef GDN_HIP_H_
+#define GDN_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+
+#define GDN_OK 0
+#define GDN_ERR_NULL (-1001)      /* a required pointer is NULL */
+#define GDN_ERR_SHAPE (-1002)     /* an unsupported size or head configuration */
+#define GDN_ERR_WORKSPACE (-1003) /* workspace missing or too small */
+
+/* ABI version of the loaded library (GDN_ABI_VERSION). */
+int gdn_abi_version(void);
+
+/* Human-readable text for a return code of this library. */
+const char* gdn_error_string(int code);
+
+/*
+ * One decode step for B sequences.
+ * Replaces the reference decode entry `run(q, k, v, state, A_log, a, dt_bias,
+ * b, scale)` (gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py:100-146)
+ * and its kernel (same file :26-79).
+ *   state      : [B, HV, V, K] fp32, or NULL for a zero state (kernel.py:86-94).
+ *   new_state  : [B, HV, V, K] fp32 output; may equal `state` (in-place update).
+ *   scale      : applied to q; the caller resolves None/0 to 1/sqrt(D)
+ *                (kernel.py:112-115).
+ * HV must be a multiple of HQ and HV/HQ <= 4.
+ */
+int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                   const float* state, float* new_state,
+                   const float* A_log, const uint16_t* a, const float* dt_bias,
+                   const uint16_t* b, uint16_t* out,
+                   int B, int HQ, int HV, float scale, void* stream);
+
+/*
+ * One decode step against a state pool, updated in place:
+ * state_pool[slot_ids[n]] is read and overwritten for every n < B.
+ * No reference counterpart: the reference decode takes one dense state per
+ * sequence (kernel.py:100-146).  This serves callers that keep recurrent
+ * states in a slot pool (serving engines).  slot_ids must be distinct; a
+ * slot outside [0, pool_size) leaves the pool untouched and yields a zero
+ * output row.
+ */
+int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        float* state_pool, int pool_size, const int32_t* slot_ids,
+                        const float* A_log, const uint16_t* a, const float* dt_bias,
+                        const uint16_t* b, uint16_t* out,
+                        int B, int HQ, int HV, float scale, void* stream);
+
+/*
+ * Workspace bytes gdn_prefill_fwd needs for this problem (may be 0).
+ */
+size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV);
+
+/*
+ * Chunked (64-token) varlen prefill.
+ * Replaces the reference prefill entry `run(q, k, v, state, A_log, a,
+ * dt_bias, b, cu_seqlens, scale)`
+ * (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:1762-1802) and
+ * the five kernels it launches (kernel.py:1570-1633, 1728-1759).
+ *   state       : [N, HV, V, K] fp32 initial states, or NULL for zeros.
+ *   final_state : [N, HV, V, K] fp32 output.
+ *   cu_seqlens  : device array, N+1 entries, cu_seqlens[0] == 0,
+ *                 cu_seqlens[N] == T, non-decreasing (empty sequences allowed).
+ *   scale       : the caller resolves None/0 to 1/sqrt(D) (kernel.py:1777-1778).
+ *   workspace   : device buffer of at least gdn_prefill_workspace_bytes(...)
+ *                 bytes (may be NULL when that is 0).
+ */
+int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                    const float* state, const float* A_log, const uint16_t* a,
+                    const float* dt_bias, const uint16_t* b,
+                    const void* cu_seqlens, int cu_is_int32, int N, int T,
+                    int HQ, int HV, float scale,
+                    uint16_t* out, float* final_state,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_HIP_H_ */

@@ -1,0 +1,332 @@
+"""CPU oracle for the Gated DeltaNet (GDN) decode and prefill operators.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker the HIP kernels are held
+against: only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU
+baseline leg may import it.  No product code path routes through it.
+
+It restates, in plain PyTorch on the CPU (float64 by default, float32 for the
+timed CPU baseline), the arithmetic of the two reference operators:
+
+* decode  -- ``gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py`` (DEC)
+* prefill -- ``gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py`` (PRE)
+
+Every function cites the reference lines it follows.  Head counts are
+generic: v-head ``h`` reads qk-head ``h // (HV // HQ)`` (DEC:47, PRE:495, the
+reference hard-codes ratio 2).  The recurrent state is "k-last":
+``state[n, h, v, k]`` fp32 with K contiguous (DEC:53,70; PRE:1129).
+
+How each function is pinned (tests/test_oracle.py):
+
+* gating           -- torch.nn.functional.softplus / sigmoid closed forms and
+                      special cases (A_log -> -inf gives g = 1, b = 0 gives 0.5).
+* decode_step      -- closed forms at state = 0 and beta = 0, the delta-rule
+                      write invariant (g = beta = 1, |k| = 1 gives S' k = v),
+                      linearity in v, and an elementwise brute-force loop.
+* chunk metadata   -- brute-force enumeration over random cu_seqlens including
+                      empty sequences and exact multiples of the chunk size.
+* unit_lower_inverse_blocked -- (I + A) Tm = I and torch.linalg.solve_triangular.
+* prefill_recurrent -- equals repeated decode_step with the prefill softplus,
+                      closed forms at T = 1, split / varlen invariances.
+* prefill_chunked  -- equals prefill_recurrent in float64 at chunk sizes
+                      1, 16, 32, 64, 128 including ragged tails.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+__all__ = [
+    "softplus_thresh20",
+    "softplus_stable",
+    "decode_gates",
+    "prefill_log_decay_beta",
+    "decode_step",
+    "chunk_indices",
+    "chunk_offsets",
+    "unit_lower_inverse_blocked",
+    "prefill_recurrent",
+    "prefill_chunked",
+    "default_scale",
+]
+
+
+def default_scale(scale: Optional[float], head_dim: int) -> float:
+    """``None`` or ``0.0`` means ``1/sqrt(D)`` (DEC:112-115, PRE:1777-1778)."""
+    if scale is None or float(scale) == 0.0:
+        return 1.0 / math.sqrt(head_dim)
+    return float(scale)
+
+
+# ----------------------------------------------------------------------------
+# gating
+# ----------------------------------------------------------------------------
+
+def softplus_thresh20(x: torch.Tensor) -> torch.Tensor:
+    """Decode softplus: ``x <= 20 ? log(1 + e^x) : x`` (DEC:21-23)."""
+    return torch.where(x <= 20.0, torch.log1p(torch.exp(torch.clamp(x, max=20.0))), x)
+
+
+def softplus_stable(x: torch.Tensor) -> torch.Tensor:
+    """Prefill softplus: ``x > 0 ? x + log(1 + e^-x) : log(1 + e^x)`` (PRE:1711-1720)."""
+    pos = x + torch.log1p(torch.exp(-torch.clamp(x, min=0.0)))
+    neg = torch.log1p(torch.exp(torch.clamp(x, max=0.0)))
+    return torch.where(x > 0, pos, neg)
+
+
+def decode_gates(A_log, a, dt_bias, b, dtype=torch.float64) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Decode decay ``g`` and write strength ``beta`` per (batch, v-head).
+
+    ``g = exp(-exp(A_log[h]) * softplus20(a[n,h] + dt_bias[h]))`` and
+    ``beta = 1 / (1 + exp(-b[n,h]))`` (DEC:59-65).  ``a``/``b`` may be
+    ``[B, HV]`` or ``[B, 1, HV]``.
+    """
+    HV = A_log.shape[-1]
+    a = a.reshape(-1, HV).to(dtype)
+    b = b.reshape(-1, HV).to(dtype)
+    log_g = -torch.exp(A_log.to(dtype))[None, :] * softplus_thresh20(a + dt_bias.to(dtype)[None, :])
+    g = torch.exp(log_g)
+    beta = 1.0 / (1.0 + torch.exp(-b))
+    return g, beta
+
+
+def prefill_log_decay_beta(a, b, A_log, dt_bias, dtype=torch.float64):
+    """Per-token log-decay and beta for prefill, ``[T, HV]`` each.
+
+    ``log_decay = -exp(A_log) * softplus_stable(a + dt_bias)`` and
+    ``beta = sigmoid(b)`` (PRE:1706-1722).  The reference then cumsums the
+    log-decay inside each 64-token chunk (PRE:1721); :func:`prefill_chunked`
+    does that step itself so that the per-token form stays available.
+    """
+    ld = -torch.exp(A_log.to(dtype))[None, :] * softplus_stable(a.to(dtype) + dt_bias.to(dtype)[None, :])
+    beta = torch.sigmoid(b.to(dtype))
+    return ld, beta
+
+
+# ----------------------------------------------------------------------------
+# decode
+# ----------------------------------------------------------------------------
+
+def _expand_heads(x: torch.Tensor, HV: int) -> torch.Tensor:
+    """qk-head -> v-head map ``h -> h // (HV//HQ)`` (repeat_interleave; DEC:47)."""
+    HQ = x.shape[-2]
+    assert HV % HQ == 0
+    return x.repeat_interleave(HV // HQ, dim=-2)
+
+
+def decode_step(q, k, v, state, A_log, a, dt_bias, b, scale=None, dtype=torch.float64):
+    """One GDN decode step for every (batch, v-head) (DEC:67-79).
+
+    Shapes: ``q, k [B, 1, HQ, D]``, ``v [B, 1, HV, D]``, ``state [B, HV, V, K]``
+    or ``None`` (zeros, DEC:86-94).  Per (n, h), in ``dtype``::
+
+        S'    = g * S                      (DEC:72)
+        delta = beta * (v - S' k)          (DEC:73-74, decayed state)
+        S_new = S' + delta k^T             (DEC:75)
+        o     = scale * S_new q            (DEC:56, 76)
+
+    Returns ``(o [B, 1, HV, D], S_new [B, HV, V, K])`` in ``dtype``; the
+    caller casts ``o`` to bf16 as DEC:78 does.
+    """
+    B, _, HQ, D = q.shape
+    HV = v.shape[2]
+    scale = default_scale(scale, D)
+    qh = _expand_heads(q.reshape(B, HQ, D).to(dtype), HV)
+    kh = _expand_heads(k.reshape(B, HQ, D).to(dtype), HV)
+    vh = v.reshape(B, HV, D).to(dtype)
+    if state is None:
+        S = torch.zeros(B, HV, D, D, dtype=dtype)
+    else:
+        S = state.to(dtype)
+    g, beta = decode_gates(A_log, a, dt_bias, b, dtype)
+    S1 = g[:, :, None, None] * S
+    sk = torch.einsum("nhvk,nhk->nhv", S1, kh)
+    delta = beta[:, :, None] * (vh - sk)
+    S_new = S1 + delta[:, :, :, None] * kh[:, :, None, :]
+    o = scale * torch.einsum("nhvk,nhk->nhv", S_new, qh)
+    return o.reshape(B, 1, HV, D), S_new
+
+
+# ----------------------------------------------------------------------------
+# varlen chunk metadata
+# ----------------------------------------------------------------------------
+
+def chunk_indices(cu_seqlens: torch.Tensor, chunk_size: int) -> torch.Tensor:
+    """``[(seq_id, local_chunk_id)]`` int32 ``[NT, 2]`` (PRE:175-202).
+
+    Sequences of length 0 contribute no chunks; a ragged tail is one chunk.
+    """
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    rows = []
+    for n in range(len(cu) - 1):
+        length = cu[n + 1] - cu[n]
+        for c in range((length + chunk_size - 1) // chunk_size):
+            rows.append((n, c))
+    if not rows:
+        return torch.empty((0, 2), dtype=torch.int32)
+    return torch.tensor(rows, dtype=torch.int32)
+
+
+def chunk_offsets(cu_seqlens: torch.Tensor, chunk_size: int) -> torch.Tensor:
+    """Exclusive prefix sum of per-sequence chunk counts, int64 ``[N+1]`` (PRE:204-209)."""
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    out = [0]
+    for n in range(len(cu) - 1):
+        out.append(out[-1] + (cu[n + 1] - cu[n] + chunk_size - 1) // chunk_size)
+    return torch.tensor(out, dtype=torch.int64)
+
+
+# ----------------------------------------------------------------------------
+# (I + A)^-1 for a strictly lower-triangular A
+# ----------------------------------------------------------------------------
+
+def unit_lower_inverse_blocked(A: torch.Tensor, block: int = 16) -> torch.Tensor:
+    """``(I + A)^-1`` for strictly lower-triangular ``A [..., C, C]``.
+
+    Follows the reference's blocked scheme (PRE:661-737): each ``block x
+    block`` diagonal block is inverted by row-wise forward substitution
+    (PRE:680-703) and the off-diagonal blocks are merged with block products
+    ``Ti_ij = -Ti_ii * sum_{j<=m<i} A_im Ti_mj`` (PRE:718-737), generalised
+    here from 4 blocks to ``C / block``.
+    """
+    C = A.shape[-1]
+    assert C % block == 0
+    nb = C // block
+    L = torch.tril(A, diagonal=-1)
+    Ti = torch.zeros_like(L)
+    eye = torch.eye(block, dtype=A.dtype)
+    for bi in range(nb):
+        s = bi * block
+        blk = L[..., s:s + block, s:s + block]
+        inv = torch.zeros_like(blk)
+        inv[...] = eye
+        for i in range(1, block):
+            # row i of (I + blk)^-1 = e_i - sum_{j<i} blk[i, j] * inv[j, :]
+            inv[..., i, :] = eye[i] - torch.einsum("...j,...jc->...c", blk[..., i, :i], inv[..., :i, :])
+        Ti[..., s:s + block, s:s + block] = inv
+    for bi in range(1, nb):
+        for bj in range(bi - 1, -1, -1):
+            si, sj = bi * block, bj * block
+            acc = torch.zeros_like(Ti[..., si:si + block, sj:sj + block])
+            for bm in range(bj, bi):
+                sm = bm * block
+                acc = acc + L[..., si:si + block, sm:sm + block] @ Ti[..., sm:sm + block, sj:sj + block]
+            Ti[..., si:si + block, sj:sj + block] = -Ti[..., si:si + block, si:si + block] @ acc
+    return Ti
+
+
+# ----------------------------------------------------------------------------
+# prefill
+# ----------------------------------------------------------------------------
+
+def _check_prefill_shapes(q, k, v, state, a, b, cu_seqlens):
+    T, HQ, D = q.shape
+    HV = v.shape[1]
+    assert k.shape == (T, HQ, D) and v.shape == (T, HV, D)
+    assert a.shape == (T, HV) and b.shape == (T, HV)
+    N = cu_seqlens.numel() - 1
+    assert int(cu_seqlens[-1]) == T and int(cu_seqlens[0]) == 0
+    if state is not None:
+        assert state.shape == (N, HV, D, D)
+    return T, HQ, HV, D, N
+
+
+def prefill_recurrent(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None,
+                      dtype=torch.float64):
+    """Token-by-token GDN prefill: the definition of what the chunked form computes.
+
+    For each sequence ``[cu[n], cu[n+1])`` starting from ``state[n]`` (zeros if
+    ``state`` is ``None``, PRE:1049, 1121), every token applies the decode
+    step of DEC:72-76 with ``g_t = exp(log_decay_t)`` from the prefill gating
+    (PRE:1711-1722).  Returns ``(o [T, HV, D], final_state [N, HV, V, K])``.
+    """
+    T, HQ, HV, D, N = _check_prefill_shapes(q, k, v, state, a, b, cu_seqlens)
+    scale = default_scale(scale, D)
+    ld, beta = prefill_log_decay_beta(a, b, A_log, dt_bias, dtype)
+    qh = _expand_heads(q.to(dtype), HV)
+    kh = _expand_heads(k.to(dtype), HV)
+    vh = v.to(dtype)
+    o = torch.zeros(T, HV, D, dtype=dtype)
+    final = torch.zeros(N, HV, D, D, dtype=dtype)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    for n in range(N):
+        S = torch.zeros(HV, D, D, dtype=dtype) if state is None else state[n].to(dtype).clone()
+        for t in range(cu[n], cu[n + 1]):
+            S = torch.exp(ld[t])[:, None, None] * S
+            sk = torch.einsum("hvk,hk->hv", S, kh[t])
+            delta = beta[t][:, None] * (vh[t] - sk)
+            S = S + delta[:, :, None] * kh[t][:, None, :]
+            o[t] = scale * torch.einsum("hvk,hk->hv", S, qh[t])
+        final[n] = S
+    return o, final
+
+
+def _round_bf16(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+def prefill_chunked(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None,
+                    chunk_size: int = 64, dtype=torch.float64,
+                    reference_storage: bool = False):
+    """Chunked (WY / UT transform) GDN prefill, the reference's algorithm.
+
+    Per sequence and per chunk of ``C`` tokens (ragged tail allowed), with
+    ``gam`` the chunk-local cumsum of the log-decay (PRE:1721) and ``S`` the
+    state at chunk start (``[HV, V, K]``):
+
+    1. ``A_ij = beta_i e^{gam_i - gam_j} k_i . k_j`` for ``i > j`` (PRE:509-525)
+    2. ``Tm = (I + A)^-1`` (PRE:661-737)
+    3. ``U = Tm diag(beta) V``, ``W = Tm diag(beta e^gam) K`` (PRE:739-796)
+    4. ``Vn = U - W S^T`` (PRE:1179-1211)
+    5. ``O = scale [e^gam (Q S^T) + tril_incl(Q K^T e^{gam_i-gam_j}) Vn]`` (PRE:1447-1496)
+    6. ``S <- e^{gam_L} S + (e^{gam_L - gam} Vn)^T K`` (PRE:1213-1225, 1286-1314)
+
+    ``reference_storage=True`` additionally rounds to bf16 where the
+    reference stores or casts bf16: ``W``, ``U`` (PRE:1002-1003), the chunk
+    state used by steps 4-5 (PRE:1159, 1182, 1365), ``Vn`` (PRE:1368) and the
+    intra-chunk attention weights before their product with ``Vn``
+    (PRE:1494).  It is used to measure the reference's own rounding error,
+    not as a parity target.
+    """
+    T, HQ, HV, D, N = _check_prefill_shapes(q, k, v, state, a, b, cu_seqlens)
+    scale = default_scale(scale, D)
+    C = int(chunk_size)
+    ld, beta = prefill_log_decay_beta(a, b, A_log, dtype=dtype, dt_bias=dt_bias)
+    qh = _expand_heads(q.to(dtype), HV)
+    kh = _expand_heads(k.to(dtype), HV)
+    vh = v.to(dtype)
+    rnd = _round_bf16 if reference_storage else (lambda x: x)
+    o = torch.zeros(T, HV, D, dtype=dtype)
+    final = torch.zeros(N, HV, D, D, dtype=dtype)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    for n in range(N):
+        S = torch.zeros(HV, D, D, dtype=dtype) if state is None else state[n].to(dtype).clone()
+        for s in range(cu[n], cu[n + 1], C):
+            e = min(s + C, cu[n + 1])
+            L = e - s
+            gam = torch.cumsum(ld[s:e], dim=0).transpose(0, 1)          # [HV, L]
+            bet = beta[s:e].transpose(0, 1)                             # [HV, L]
+            Kc = kh[s:e].transpose(0, 1)                                # [HV, L, D]
+            Qc = qh[s:e].transpose(0, 1)
+            Vc = vh[s:e].transpose(0, 1)
+            dec = torch.exp(gam[:, :, None] - gam[:, None, :])          # [HV, L, L]
+            strict = torch.tril(torch.ones(L, L, dtype=torch.bool), diagonal=-1)
+            incl = torch.tril(torch.ones(L, L, dtype=torch.bool), diagonal=0)
+            A = torch.where(strict, bet[:, :, None] * dec * (Kc @ Kc.transpose(1, 2)),
+                            torch.zeros((), dtype=dtype))
+            eye = torch.eye(L, dtype=dtype).expand(HV, L, L)
+            Tm = torch.linalg.solve_triangular(eye + A, eye, upper=False, unitriangular=True)
+            U = rnd(Tm @ (bet[:, :, None] * Vc))
+            W = rnd(Tm @ ((bet * torch.exp(gam))[:, :, None] * Kc))
+            Sx = rnd(S)
+            Vn = U - W @ Sx.transpose(1, 2)                             # [HV, L, V]
+            P = torch.where(incl, (Qc @ Kc.transpose(1, 2)) * dec, torch.zeros((), dtype=dtype))
+            Oc = torch.exp(gam)[:, :, None] * (Qc @ Sx.transpose(1, 2)) + rnd(P) @ rnd(Vn)
+            o[s:e] = (scale * Oc).transpose(0, 1)
+            gl = gam[:, L - 1]                                          # [HV]
+            Vd = torch.exp(gl[:, None] - gam)[:, :, None] * Vn          # [HV, L, V]
+            S = torch.exp(gl)[:, None, None] * S + rnd(Vd).transpose(1, 2) @ Kc
+        final[n] = S
+    return o, final

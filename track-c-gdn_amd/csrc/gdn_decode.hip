@@ -1,0 +1,210 @@
+// GDN decode: one recurrent step per (sequence, v-head), single pass over the
+// fp32 k-last state.  Replaces the reference's Triton decode kernel
+// (gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py:26-79).
+//
+// Per (n, h), with S = state[n, h] in [V=128, K=128] (K contiguous):
+//   S'    = g * S
+//   delta = beta * (v - S' k)
+//   S_new = S' + delta k^T
+//   o     = scale * S_new q = scale * (S' q + delta (k . q))
+//
+// Mapping (gfx950, wave64):
+//   * one workgroup per (n, qk-head) owns all HV/HQ v-heads that read that
+//     qk-head, so q/k are fetched once; 4 waves per v-head, 32 rows per wave.
+//   * a DPP row (16 lanes) owns one state row; lane c holds k = 4c..4c+3 and
+//     64+4c..64+4c+3, so each dwordx4 load covers four 256-byte row segments.
+//   * each lane keeps 8 rows (16 x float4 = 256 B) in registers: all loads are
+//     issued before any arithmetic, the row reductions are 4 DPP adds each,
+//     and the updated row is written straight back (no LDS, no second pass).
+//   * in-place update (state_in == state_out) is safe: every element is read
+//     and written by the same lane.
+
+#include "gdn_common.h"
+#include "../../include/gdn_hip.h"
+
+namespace {
+
+using namespace gdn;
+
+constexpr int D = kHeadDim;
+constexpr int kWavesPerHead = 4;
+constexpr int kRowsPerWave = D / kWavesPerHead;   // 32
+constexpr int kRowsPerLane = kRowsPerWave / 4;    // 8 (4 DPP rows per wave)
+
+template <bool kNonTemporal>
+__device__ __forceinline__ f32x4 load_state(const f32x4* p) {
+  if constexpr (kNonTemporal) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <bool kNonTemporal>
+__device__ __forceinline__ void store_state(f32x4* p, f32x4 x) {
+  if constexpr (kNonTemporal) __builtin_nontemporal_store(x, p);
+  else *p = x;
+}
+
+__device__ __forceinline__ void load_bf16x8_split(const uint16_t* base, int c, float (&x)[8]) {
+  // elements 4c..4c+3 and 64+4c..64+4c+3
+  const uint2 lo = *reinterpret_cast<const uint2*>(base + 4 * c);
+  const uint2 hi = *reinterpret_cast<const uint2*>(base + 64 + 4 * c);
+  unpack_bf16x2(lo.x, x[0], x[1]);
+  unpack_bf16x2(lo.y, x[2], x[3]);
+  unpack_bf16x2(hi.x, x[4], x[5]);
+  unpack_bf16x2(hi.y, x[6], x[7]);
+}
+
+template <bool kNonTemporal>
+__global__ __launch_bounds__(1024) void gdn_decode_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* state_in, float* state_out,
+    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
+    uint16_t* __restrict__ out, const int32_t* __restrict__ slot_ids,
+    int HQ, int HV, int pool_size, float scale) {
+  const int ratio = HV / HQ;
+  const int n = blockIdx.x / HQ;
+  const int hq = blockIdx.x - n * HQ;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int hv = hq * ratio + wave / kWavesPerHead;
+  const int row0 = (wave % kWavesPerHead) * kRowsPerWave;
+  const int rsub = lane >> 4;     // DPP row within the wave
+  const int c = lane & 15;        // lane within the DPP row
+  const int rbase = row0 + rsub * kRowsPerLane;   // this lane's 8 consecutive rows
+
+  const size_t nh = size_t(n) * HV + hv;
+  uint16_t* o_ptr = out + nh * D + rbase;
+
+  int slot = n;
+  if (slot_ids != nullptr) {
+    slot = slot_ids[n];
+    if (slot < 0 || slot >= pool_size) {
+      // Unmapped sequence: no state access, zero output.
+      if (c == 0) *reinterpret_cast<uint4*>(o_ptr) = make_uint4(0, 0, 0, 0);
+      return;
+    }
+  }
+  const size_t sbase = (size_t(slot) * HV + hv) * size_t(D) * D;
+
+  // Issue the state loads first: 16 x 16 B in flight per lane.
+  f32x4 s[kRowsPerLane][2];
+  if (state_in != nullptr) {
+    const float* sp = state_in + sbase + size_t(rbase) * D;
+#pragma unroll
+    for (int j = 0; j < kRowsPerLane; ++j) {
+      s[j][0] = load_state<kNonTemporal>(reinterpret_cast<const f32x4*>(sp + j * D + 4 * c));
+      s[j][1] = load_state<kNonTemporal>(reinterpret_cast<const f32x4*>(sp + j * D + 64 + 4 * c));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowsPerLane; ++j) {
+      s[j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  const size_t qk_off = (size_t(n) * HQ + hq) * D;
+  float kk[8], qq[8];
+  load_bf16x8_split(k + qk_off, c, kk);
+  load_bf16x8_split(q + qk_off, c, qq);
+  float vv[8];
+  {
+    const uint4 vw = *reinterpret_cast<const uint4*>(v + nh * D + rbase);
+    unpack_bf16x2(vw.x, vv[0], vv[1]);
+    unpack_bf16x2(vw.y, vv[2], vv[3]);
+    unpack_bf16x2(vw.z, vv[4], vv[5]);
+    unpack_bf16x2(vw.w, vv[6], vv[7]);
+  }
+
+  // Gates (reference DEC:59-65), uniform per wave.
+  const float a_val = bf16_bits_to_f32(a[nh]);
+  const float b_val = bf16_bits_to_f32(b[nh]);
+  const float g = expf(-expf(A_log[hv]) * softplus_thresh20(a_val + dt_bias[hv]));
+  const float beta = 1.0f / (1.0f + expf(-b_val));
+
+  float kq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) kq = fmaf(kk[e], qq[e], kq);
+  kq = row16_sum(kq);
+
+  float o_out[kRowsPerLane];
+  float* dst = state_out + sbase + size_t(rbase) * D;
+#pragma unroll
+  for (int j = 0; j < kRowsPerLane; ++j) {
+    float x[8] = {s[j][0].x, s[j][0].y, s[j][0].z, s[j][0].w,
+                  s[j][1].x, s[j][1].y, s[j][1].z, s[j][1].w};
+    float pk = 0.f, pq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] *= g;
+      pk = fmaf(x[e], kk[e], pk);
+      pq = fmaf(x[e], qq[e], pq);
+    }
+    pk = row16_sum(pk);
+    pq = row16_sum(pq);
+    const float delta = beta * (vv[j] - pk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = fmaf(delta, kk[e], x[e]);
+    o_out[j] = scale * fmaf(delta, kq, pq);
+    store_state<kNonTemporal>(reinterpret_cast<f32x4*>(dst + j * D + 4 * c),
+                              f32x4{x[0], x[1], x[2], x[3]});
+    store_state<kNonTemporal>(reinterpret_cast<f32x4*>(dst + j * D + 64 + 4 * c),
+                              f32x4{x[4], x[5], x[6], x[7]});
+  }
+  if (c == 0) {
+    uint4 w;
+    w.x = pack_bf16x2(o_out[0], o_out[1]);
+    w.y = pack_bf16x2(o_out[2], o_out[3]);
+    w.z = pack_bf16x2(o_out[4], o_out[5]);
+    w.w = pack_bf16x2(o_out[6], o_out[7]);
+    *reinterpret_cast<uint4*>(o_ptr) = w;
+  }
+}
+
+int check_decode_args(const void* q, const void* k, const void* v, const void* state_out,
+                      const void* A_log, const void* a, const void* dt_bias, const void* b,
+                      const void* out, int B, int HQ, int HV) {
+  if (!q || !k || !v || !state_out || !A_log || !a || !dt_bias || !b || !out) return GDN_ERR_NULL;
+  if (B < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return GDN_ERR_SHAPE;
+  if ((HV / HQ) * kWavesPerHead * kWave > 1024) return GDN_ERR_SHAPE;
+  return GDN_OK;
+}
+
+int launch_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state_in,
+                  float* state_out, const float* A_log, const uint16_t* a, const float* dt_bias,
+                  const uint16_t* b, uint16_t* out, const int32_t* slot_ids, int B, int HQ, int HV,
+                  int pool_size, float scale, void* stream) {
+  if (B == 0) return GDN_OK;
+  const dim3 grid(unsigned(B) * unsigned(HQ));
+  const dim3 block(unsigned(HV / HQ) * kWavesPerHead * kWave);
+  hipLaunchKernelGGL(gdn_decode_kernel<true>, grid, block, 0, static_cast<hipStream_t>(stream),
+                     q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, slot_ids, HQ, HV,
+                     pool_size, scale);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? GDN_OK : -int(err);
+}
+
+}  // namespace
+
+extern "C" int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const float* state, float* new_state, const float* A_log,
+                              const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                              uint16_t* out, int B, int HQ, int HV, float scale, void* stream) {
+  const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  return launch_decode(q, k, v, state, new_state, A_log, a, dt_bias, b, out, nullptr, B, HQ, HV,
+                       B, scale, stream);
+}
+
+extern "C" int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                   float* state_pool, int pool_size, const int32_t* slot_ids,
+                                   const float* A_log, const uint16_t* a, const float* dt_bias,
+                                   const uint16_t* b, uint16_t* out, int B, int HQ, int HV,
+                                   float scale, void* stream) {
+  const int rc = check_decode_args(q, k, v, state_pool, A_log, a, dt_bias, b, out, B, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (!slot_ids) return GDN_ERR_NULL;
+  if (pool_size < 0) return GDN_ERR_SHAPE;
+  return launch_decode(q, k, v, state_pool, state_pool, A_log, a, dt_bias, b, out, slot_ids, B,
+                       HQ, HV, pool_size, scale, stream);
+}

@@ -1,0 +1,149 @@
+"""GDN decode operator: one recurrent step per sequence on the GPU.
+
+Host-side mirror of the reference decode entry point
+``gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py`` (DEC):
+
+* :func:`run` -- same positional signature, defaults, asserts and return
+  tuple as ``run`` at DEC:100-146 (value-returning, qk4/v8/d128).
+* :func:`run_dps` -- destination-passing variant: ``output`` and
+  ``new_state`` are appended as trailing parameters and written in place.
+* :func:`gdn_decode` -- the same step for any head layout with
+  ``HV % HQ == 0`` (e.g. 16 qk-heads / 32 v-heads).
+* :func:`decode_pool_` -- in-place step against a slot-indexed state pool.
+
+All compute runs in the HIP kernel of libgdn_hip.so on torch's current
+stream; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _capi
+
+HQ = 4
+HV = 8
+D = 128
+
+
+def _resolve_scale(scale, head_dim: int) -> float:
+    # DEC:112-115
+    if scale is None or float(scale) == 0.0:
+        return 1.0 / math.sqrt(head_dim)
+    return float(scale)
+
+
+def _check_common(q, k, v, A_log, a, dt_bias, b):
+    assert q.is_cuda and k.is_cuda and v.is_cuda, "decode inputs must be GPU tensors"
+    assert q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+    assert a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
+    B, T1, nq, d = q.shape
+    assert T1 == 1 and d == D
+    assert k.shape == q.shape
+    assert v.dim() == 4 and v.shape[0] == B and v.shape[1] == 1 and v.shape[3] == D
+    nv = v.shape[2]
+    assert nv % nq == 0 and nv // nq <= 4, "v-heads must be a multiple (<=4x) of qk-heads"
+    assert A_log.numel() == nv and dt_bias.numel() == nv
+    assert a.numel() == B * nv and b.numel() == B * nv
+    return B, nq, nv
+
+
+def _gates(A_log, dt_bias):
+    # DEC:131-133 (A_log.float(), dt_bias.float())
+    return A_log.float().contiguous(), dt_bias.float().contiguous()
+
+
+def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, nq, nv):
+    A_log, dt_bias = _gates(A_log, dt_bias)
+    q = q.contiguous()
+    k = k.contiguous()
+    v = v.contiguous()
+    a = a.contiguous()
+    b = b.contiguous()
+    rc = _capi.lib().gdn_decode_fwd(
+        _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
+        _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
+        B, nq, nv, float(scale), _capi.stream_handle(q.device))
+    _capi.check(rc, "gdn_decode_fwd")
+
+
+@torch.no_grad()
+def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
+               new_state=None):
+    """One decode step for any ``HV % HQ == 0`` head layout.
+
+    ``q, k [B, 1, HQ, 128]``, ``v [B, 1, HV, 128]`` bf16; ``state
+    [B, HV, 128, 128]`` fp32 or ``None``; ``a, b [B, 1, HV]`` bf16; ``A_log,
+    dt_bias [HV]``.  Returns ``(output [B, 1, HV, 128] bf16, new_state)``.
+    ``new_state`` may be the ``state`` tensor itself (in-place update).
+    """
+    B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
+    scale = _resolve_scale(scale, q.shape[-1])
+    if state is not None:
+        assert state.is_cuda and state.dtype == torch.float32
+        assert state.shape == (B, nv, D, D)
+        if not state.is_contiguous():   # DEC:95-96
+            state = state.contiguous()
+    if output is None:
+        output = torch.empty(B, 1, nv, D, dtype=q.dtype, device=q.device)
+    if new_state is None:
+        new_state = torch.empty(B, nv, D, D, dtype=torch.float32, device=q.device)
+    assert output.dtype == torch.bfloat16 and output.is_contiguous() and output.numel() == B * nv * D
+    assert new_state.dtype == torch.float32 and new_state.is_contiguous()
+    assert new_state.shape == (B, nv, D, D)
+    _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, nq, nv)
+    return output, new_state
+
+
+@torch.no_grad()
+def run(q, k, v, state, A_log, a, dt_bias, b, scale):
+    """Reference-compatible decode entry (DEC:100-146), qk4 / v8 / d128.
+
+    Returns ``(output [B, 1, 8, 128] bf16, new_state [B, 8, 128, 128] fp32)``;
+    the input state is not modified.
+    """
+    assert q.shape[1:] == (1, HQ, D)    # DEC:117-120
+    assert k.shape[1:] == (1, HQ, D)
+    assert v.shape[1:] == (1, HV, D)
+    assert q.shape[0] == v.shape[0]
+    return gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale)
+
+
+@torch.no_grad()
+def run_dps(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
+    """Destination-passing decode: writes ``output`` and ``new_state``, returns None."""
+    assert q.shape[1:] == (1, HQ, D)
+    assert k.shape[1:] == (1, HQ, D)
+    assert v.shape[1:] == (1, HV, D)
+    assert q.shape[0] == v.shape[0]
+    gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale, output=output, new_state=new_state)
+
+
+@torch.no_grad()
+def decode_pool_(q, k, v, state_pool, slot_ids, A_log, a, dt_bias, b, scale=None, *,
+                 output=None):
+    """One decode step against ``state_pool[slot_ids[n]]``, updated in place.
+
+    ``state_pool [P, HV, 128, 128]`` fp32, ``slot_ids [B]`` int32 (distinct).
+    A slot outside ``[0, P)`` leaves the pool untouched and gives a zero
+    output row.  Returns ``output [B, 1, HV, 128]`` bf16.
+    """
+    B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
+    scale = _resolve_scale(scale, q.shape[-1])
+    assert state_pool.is_cuda and state_pool.dtype == torch.float32 and state_pool.is_contiguous()
+    assert state_pool.dim() == 4 and state_pool.shape[1:] == (nv, D, D)
+    assert slot_ids.is_cuda and slot_ids.dtype == torch.int32 and slot_ids.numel() == B
+    slot_ids = slot_ids.contiguous()
+    if output is None:
+        output = torch.empty(B, 1, nv, D, dtype=q.dtype, device=q.device)
+    A_log, dt_bias = _gates(A_log, dt_bias)
+    q, k, v, a, b = (t.contiguous() for t in (q, k, v, a, b))
+    rc = _capi.lib().gdn_decode_pool_fwd(
+        _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state_pool), state_pool.shape[0],
+        _capi.ptr(slot_ids), _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b),
+        _capi.ptr(output), B, nq, nv, float(scale), _capi.stream_handle(q.device))
+    _capi.check(rc, "gdn_decode_pool_fwd")
+    return output

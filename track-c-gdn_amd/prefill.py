@@ -1,0 +1,140 @@
+"""GDN chunked varlen prefill operator on the GPU.
+
+Host-side mirror of the reference prefill entry point
+``gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py`` (PRE):
+
+* :func:`run` -- same positional signature, validation (``_validate_inputs``,
+  PRE:1635-1667), scale default (PRE:1777-1778) and return tuple
+  ``(output [T, 8, 128] bf16, final_state [N, 8, 128, 128] fp32)`` as
+  PRE:1762-1802.  ``cu_seqlens`` may be int64 (as the reference asserts) or
+  int32.
+* :func:`run_dps` -- destination-passing variant (``output``,
+  ``final_state`` appended).
+* :func:`gdn_prefill` -- any ``HV % HQ == 0`` head layout, optional
+  validation, caller-provided outputs.
+
+All compute runs in the HIP kernels of libgdn_hip.so on torch's current
+stream.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _capi
+
+NUM_Q_HEADS = 4
+NUM_K_HEADS = 4
+NUM_V_HEADS = 8
+HEAD_SIZE = 128
+CHUNK_SIZE = 64
+
+
+def _resolve_scale(scale) -> float:
+    # PRE:1777-1778
+    if scale is None or scale == 0.0:
+        return 1.0 / math.sqrt(HEAD_SIZE)
+    return float(scale)
+
+
+def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                    num_q_heads: int = NUM_Q_HEADS, num_v_heads: int = NUM_V_HEADS,
+                    check_total: bool = True) -> None:
+    """The checks of PRE:1635-1667, raising AssertionError before any launch.
+
+    ``check_total`` keeps the reference's ``cu_seqlens[-1] == T`` check
+    (PRE:1665), which reads one value back to the host.
+    """
+    assert q.is_cuda and k.is_cuda and v.is_cuda
+    assert A_log.is_cuda and a.is_cuda and dt_bias.is_cuda and b.is_cuda and cu_seqlens.is_cuda
+    assert q.dtype == torch.bfloat16
+    assert k.dtype == torch.bfloat16
+    assert v.dtype == torch.bfloat16
+    assert A_log.dtype == torch.float32
+    assert dt_bias.dtype == torch.float32
+    assert a.dtype == torch.bfloat16
+    assert b.dtype == torch.bfloat16
+    if state is not None:
+        assert state.is_cuda and state.dtype == torch.float32
+    assert q.shape[1:] == (num_q_heads, HEAD_SIZE)
+    assert k.shape[1:] == (num_q_heads, HEAD_SIZE)
+    assert v.shape[1:] == (num_v_heads, HEAD_SIZE)
+    assert A_log.shape == (num_v_heads,)
+    assert dt_bias.shape == (num_v_heads,)
+    assert a.shape == (q.shape[0], num_v_heads)
+    assert b.shape == (q.shape[0], num_v_heads)
+    assert cu_seqlens.dtype in (torch.int64, torch.int32)
+    assert cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 1
+    if check_total:
+        assert int(cu_seqlens[-1].item()) == q.shape[0]
+    if state is not None:
+        assert state.shape == (cu_seqlens.numel() - 1, num_v_heads, HEAD_SIZE, HEAD_SIZE)
+
+
+def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
+    return int(_capi.lib().gdn_prefill_workspace_bytes(N, T, HQ, HV))
+
+
+@torch.no_grad()
+def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
+                output=None, final_state=None, workspace=None, validate: bool = True):
+    """Chunked GDN prefill over packed varlen sequences, any ``HV % HQ == 0``.
+
+    ``q, k [T, HQ, 128]``, ``v [T, HV, 128]``, ``a, b [T, HV]`` bf16;
+    ``state [N, HV, 128, 128]`` fp32 or ``None`` (zeros); ``cu_seqlens [N+1]``
+    int64/int32.  Returns ``(output [T, HV, 128] bf16, final_state)``.
+    ``validate=False`` skips the host read-back of ``cu_seqlens[-1]``; the
+    caller then guarantees ``cu_seqlens[N] == T``.
+    """
+    T, nq, d = q.shape
+    nv = v.shape[1]
+    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv,
+                    check_total=validate)
+    assert nv % nq == 0
+    scale = _resolve_scale(scale)
+    N = cu_seqlens.numel() - 1
+    if state is not None and not state.is_contiguous():
+        state = state.contiguous()
+    q, k, v, a, b = (t.contiguous() for t in (q, k, v, a, b))
+    cu = cu_seqlens.contiguous()
+    A_log = A_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    if output is None:
+        output = torch.empty(T, nv, HEAD_SIZE, dtype=torch.bfloat16, device=q.device)
+    if final_state is None:
+        final_state = torch.empty(N, nv, HEAD_SIZE, HEAD_SIZE, dtype=torch.float32,
+                                  device=q.device)
+    assert output.dtype == torch.bfloat16 and output.is_contiguous()
+    assert output.shape == (T, nv, HEAD_SIZE)
+    assert final_state.dtype == torch.float32 and final_state.is_contiguous()
+    assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
+    ws_need = workspace_bytes(N, T, nq, nv)
+    if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
+        workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = _capi.lib().gdn_prefill_fwd(
+        _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
+        _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
+        1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
+        _capi.ptr(output), _capi.ptr(final_state), _capi.ptr(workspace), ws_bytes,
+        _capi.stream_handle(q.device))
+    _capi.check(rc, "gdn_prefill_fwd")
+    return output, final_state
+
+
+@torch.no_grad()
+def run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale):
+    """Reference-compatible prefill entry (PRE:1762-1802), qk4 / v8 / d128."""
+    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, check_total=False)
+    return gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale)
+
+
+@torch.no_grad()
+def run_dps(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, final_state):
+    """Destination-passing prefill: writes ``output`` / ``final_state``, returns None."""
+    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, check_total=False)
+    gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
+                final_state=final_state)
