@@ -14,9 +14,9 @@ Work accounting (per v-head and per step):
   printed beside it.
 
 Timing: ``--warmup`` untimed steps, then ``--steps`` timed steps bracketed by
-``torch.cuda.synchronize()``; every launch inside the timed region is also
-bracketed by its own pair of HIP events on the launch stream, whose mean is
-the kernel duration the roofline uses.  Decode rotates 4 (state, new_state)
+``torch.cuda.synchronize()`` and one pair of HIP events on the launch
+stream; a step is one kernel launch, so the mean launch duration (the
+roofline's kernel time) is the elapsed time over the step count.  Decode rotates 4 (state, new_state)
 buffer sets (1 GiB) so the 256 MB Infinity Cache cannot serve the state.
 """
 
@@ -75,25 +75,26 @@ def _traffic(name: str):
 
 
 def timed_launches(launch, n_steps: int, warmup: int):
-    """Run ``launch(i)`` warmup + n_steps times; return (total_ms, mean_kernel_ms)."""
+    """Run ``launch(i)`` warmup + n_steps times; return (total_ms, mean_launch_ms).
+
+    The timed launches run back to back on the launch stream between one
+    pair of HIP events; every launch is one kernel, so the mean launch
+    duration is the elapsed time over the launch count (event markers between
+    launches would insert gaps of their own).
+    """
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n_steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0.record()
     for i in range(n_steps):
-        evs[i][0].record()
         launch(warmup + i)
-        evs[i][1].record()
     t1.record()
     torch.cuda.synchronize()
     total = t0.elapsed_time(t1)
-    per = [a.elapsed_time(b) for a, b in evs]
-    return total, sum(per) / len(per)
+    return total, total / n_steps
 
 
 def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4):
@@ -102,11 +103,12 @@ def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4):
     states = [g["state"]] + [g["state"].clone() for _ in range(sets - 1)]
     outs = [torch.empty_like(g["state"]) for _ in range(sets)]
     o = torch.empty(B, 1, HV, D, dtype=torch.bfloat16, device=dev)
+    steps_ = [gdec.PreparedDecode(g["q"], g["k"], g["v"], states[j], g["A_log"], g["a"],
+                                  g["dt_bias"], g["b"], g["scale"], o, outs[j])
+              for j in range(sets)]
 
     def launch(i):
-        j = i % sets
-        gdec.gdn_decode(g["q"], g["k"], g["v"], states[j], g["A_log"], g["a"], g["dt_bias"],
-                        g["b"], g["scale"], output=o, new_state=outs[j])
+        steps_[i % sets]()
 
     total_ms, kern_ms = timed_launches(launch, steps, warmup)
     nbytes = decode_bytes(B, HQ, HV)
@@ -123,10 +125,11 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     out = torch.empty(T, w["HV"], D, dtype=torch.bfloat16, device=dev)
     fs = torch.empty(N, w["HV"], D, D, dtype=torch.float32, device=dev)
 
+    call = gpre.PreparedPrefill(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
+                                g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"], out, fs)
+
     def launch(i):
-        gpre.gdn_prefill(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"], g["dt_bias"],
-                         g["b"], g["cu_seqlens"], g["scale"], output=out, final_state=fs,
-                         validate=False)
+        call()
 
     total_ms, kern_ms = timed_launches(launch, steps, warmup)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, T=T, N=N, lens=lens, HQ=w["HQ"],
@@ -147,7 +150,7 @@ def cpu_baseline_decode(budget_s=12.0, B=256):
         O.decode_step(*args, x["scale"], dtype=torch.float32)
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
+        if el >= budget_s or n >= 400:
             break
     gbs = decode_bytes(B, 4, 8) * n / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
@@ -155,20 +158,25 @@ def cpu_baseline_decode(budget_s=12.0, B=256):
             "sample": f"{n} fp32 oracle decode steps at B=256 qk4/v8 ({el:.1f} s)"}
 
 
-def cpu_baseline_prefill(budget_s=12.0):
-    """Per-token fp32 oracle recurrence (definition-reference style) on a prefix sample."""
+def cpu_baseline_prefill():
+    """Per-token fp32 oracle recurrence (definition-reference style) over the whole
+    32 768-token qk16 / v32 workload, once."""
     from oracle import gdn_oracle as O
 
     torch.set_num_threads(os.cpu_count() or 1)
-    x = ginp.prefill_inputs([512], 16, 32, seed=1004, with_state=True)
+    name = "prefill_varlen8_t32768_qk16_v32"
+    w = ginp.WORKLOADS[name]
+    lens = ginp.workload_lengths(name)
+    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
     args = [x[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
     t0 = time.perf_counter()
     O.prefill_recurrent(*args, x["scale"], dtype=torch.float32)
     el = time.perf_counter() - t0
-    toks = 512
+    toks = sum(lens)
     return {"value": round(toks / el, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"512-token sequence, qk16/v32, fp32 per-token oracle recurrence ({el:.1f} s)"}
+            "sample": f"the full {toks}-token qk16/v32 workload once, fp32 per-token oracle "
+                      f"recurrence ({el:.1f} s)"}
 
 
 def main():
@@ -179,6 +187,9 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 5 plain 256 MiB device copies (the reference kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE counter readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GDN operators shard with no communication "
@@ -236,6 +247,14 @@ def main():
         except Exception as e:  # prefill not available: say so in the line
             line["prefill"] = {"error": f"{type(e).__name__}: {e}"}
             print(f"# prefill failed: {e}", file=sys.stderr, flush=True)
+
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_calibration_bytes"] = src.numel() * 4
 
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode()

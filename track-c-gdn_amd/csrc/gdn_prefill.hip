@@ -13,7 +13,7 @@
 // are never formed:
 //   A   = tril_strict(beta_i e^{gam_i-gam_j} K K^T)      (MFMA 16x16x32)
 //   P   = tril_incl(e^{gam_i-gam_j} Q K^T)                (MFMA 16x16x32)
-//   Tm  = (I + A)^-1                                       (fp32, blocked 16x16)
+//   Tm  = (I + A)^-1      (fp32 16x16 diagonal blocks, MFMA block merges)
 //   X   = diag(beta) (V - diag(e^gam) K S^T)               (MFMA 32x32x16)
 //   Vn  = Tm X          ( = U - W S^T of the reference )   (MFMA 32x32x16)
 //   O   = scale (diag(e^gam) Q S^T + P Vn)                 (MFMA 32x32x16)
@@ -39,38 +39,43 @@ using namespace gdn;
 
 constexpr int D = kHeadDim;   // 128
 constexpr int C = 64;         // chunk
-constexpr int KLD = D + 4;    // sK / sQ row stride (halves): 264 B rows
-constexpr int TLD = C + 4;    // sKT / sTm / sP row stride (halves): 136 B rows
-constexpr int FLD = C + 1;    // sA / sTF row stride (floats)
-constexpr int kThreads = 256;
+constexpr int KLD = D + 8;    // sK / sQ row stride (halves): 272 B rows
+constexpr int TLD = C + 8;    // sKT / sTm / sP row stride (halves): 144 B rows
+constexpr int ALD = C + 4;    // sA row stride (floats): 272 B rows
+constexpr int kThreads = 256; // 4 waves, one per SIMD
+
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
+// Column order inside every 16-column group of the fp16 operand tiles: the
+// two middle quads are swapped (bits 2 and 3 of the index), so that the 8
+// k-slots lane half h feeds an MFMA -- rows {0-3, 8-11} (h = 0) or
+// {4-7, 12-15} (h = 1) of a 16-row accumulator block -- are 16 contiguous
+// bytes.  The map is its own inverse.
+__device__ __forceinline__ int perm16(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
 
 struct __align__(16) Smem {
-  _Float16 K[C * KLD];        // K chunk, [t][k]
-  _Float16 Q[C * KLD];        // Q chunk, [t][k]
-  _Float16 KT[D * TLD];       // K chunk transposed, [k][t]
-  _Float16 Tm[C * TLD];       // (I + A)^-1, [t][t']
-  _Float16 P[C * TLD];        // decayed causal Q K^T, [t][t']
-  float A[C * FLD];           // beta-scaled decayed strict K K^T (fp32)
-  float TF[C * FLD];          // (I + A)^-1 in fp32
-  float Y[3 * 16 * 17];       // per-wave 16x16 scratch of the inverse
-  float gam[C];               // chunk-local cumsum of the log-decay
+  uint16_t rawK[C * D];        // next chunk's K rows as loaded (bf16), filled by DMA
+  uint16_t rawQ[C * D];        // next chunk's Q rows as loaded (bf16), filled by DMA
+  uint16_t rawV[2][C * D];     // V chunks (bf16) [t][v], filled by DMA, double-buffered
+  _Float16 K[C * KLD];         // K chunk [t][perm(k)]
+  _Float16 Q[C * KLD];         // Q chunk [t][perm(k)]
+  _Float16 KT[D * TLD];        // K chunk transposed [k][perm(t)]
+  _Float16 Tm[C * TLD];        // (I + A)^-1 [t][perm(t')]
+  _Float16 P[C * TLD];         // decayed causal Q K^T [t][perm(t')]
+  float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32)
+  float gam[C];                // chunk-local cumsum of the log-decay
   float beta[C];
-  float eg[C];                // e^{gam_t}
-  float ed[C];                // e^{gam_{L-1} - gam_t}
+  float eg[C];                 // e^{gam_t}
+  float ed[C];                 // e^{gam_{L-1} - gam_t}
 };
 
-__device__ __forceinline__ f16x8 ld_frag_split(const _Float16* row, int col) {
-  // halves [col, col+4) and [col+8, col+12) of one row (two 8-byte LDS reads)
-  const f16x4 lo = *reinterpret_cast<const f16x4*>(row + col);
-  const f16x4 hi = *reinterpret_cast<const f16x4*>(row + col + 8);
-  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
+__device__ __forceinline__ f16x8 ld16(const _Float16* p) { return *reinterpret_cast<const f16x8*>(p); }
 
-__device__ __forceinline__ f16x8 ld_frag_contig(const _Float16* row, int col) {
-  // halves [col, col+8) of one row (two 8-byte LDS reads)
-  const f16x4 lo = *reinterpret_cast<const f16x4*>(row + col);
-  const f16x4 hi = *reinterpret_cast<const f16x4*>(row + col + 4);
-  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+__device__ __forceinline__ f16x8 ld_f32x8_as_f16(const float* p) {
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
+  return f16x8{(_Float16)lo[0], (_Float16)lo[1], (_Float16)lo[2], (_Float16)lo[3],
+               (_Float16)hi[0], (_Float16)hi[1], (_Float16)hi[2], (_Float16)hi[3]};
 }
 
 __device__ __forceinline__ f16x8 pack8(const f32x16& x, int s) {
@@ -88,8 +93,18 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Row t of an accumulator tile element i for lane half h (32x32 layout).
+__device__ __forceinline__ f32x4 mfma16k16(f16x4_t a, f16x4_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Row of accumulator element i for lane half h (32x32 layout).
 __device__ __forceinline__ int acc_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
 
 template <typename CuT>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
@@ -109,6 +124,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   const int lane = tid & 63;
   const int h = lane >> 5;        // lane half (32x32 MFMA layouts)
   const int col = lane & 31;
+  const int g4 = lane >> 4;       // lane group (16x16 MFMA layouts)
+  const int c16 = lane & 15;
   const int vrow = 32 * wave + col;   // state row v owned by this lane
 
   long long bos_l = (long long)cu_seqlens[n];
@@ -120,6 +137,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 
   const float a_log_exp = expf(A_log[hv]);
   const float dtb = dt_bias[hv];
+  const size_t qk_stride = size_t(HQ) * D;   // elements per token in q / k
+  const size_t v_stride = size_t(HV) * D;    // elements per token in v / out
+  const int n_chunks = (len + C - 1) / C;
 
   // Upper 16x16 tiles inside the diagonal 32x32 blocks of Tm / P are read by
   // the 32x32 products and must be zero; they are never written afterwards.
@@ -129,6 +149,32 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     sm.Tm[R * TLD + Cc] = (_Float16)0.f;
     sm.P[R * TLD + Cc] = (_Float16)0.f;
   }
+
+  // Wave w owns chunk rows [16w, 16w+16) of the staging: it DMAs them from
+  // HBM into rawK / rawQ / rawV one chunk ahead and converts the same K / Q
+  // rows, so no other wave touches its raw rows in between.  Lane l of DMA
+  // instruction r carries row 16w + 4r + l/16, columns 8(l%16)..+7; rows past
+  // the chunk end are clamped to its last row (zeroed at conversion).
+  uint16_t ra = 0, rb = 0;            // gate inputs of row `lane` (wave 0)
+  auto issue_chunk = [&](int ch) {
+    const int t0 = bos + ch * C;
+    const int L = min(C, len - ch * C);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row0 = 16 * wave + 4 * r;
+      const int row = min(row0 + (lane >> 4), L - 1);
+      const size_t off = size_t(t0 + row) * qk_stride + size_t(hq) * D + (lane & 15) * 8;
+      lds_dma16(k + off, &sm.rawK[row0 * D]);
+      lds_dma16(q + off, &sm.rawQ[row0 * D]);
+      lds_dma16(v + size_t(t0 + row) * v_stride + size_t(hv) * D + (lane & 15) * 8,
+                &sm.rawV[ch & 1][row0 * D]);
+    }
+    if (wave == 0) {
+      const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
+      ra = a[gi];
+      rb = b[gi];
+    }
+  };
 
   // ---- initial state: S^T tiles, Sacc[j][i] = S[vrow][32j + acc_row(i, h)]
   f32x16 Sacc[4];
@@ -146,272 +192,234 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     }
   }
 
-  const size_t qk_stride = size_t(HQ) * D;   // elements per token in q / k
-  const size_t v_stride = size_t(HV) * D;    // elements per token in v / out
-  const int n_chunks = (len + C - 1) / C;
+  if (n_chunks > 0) issue_chunk(0);
 
   for (int ch = 0; ch < n_chunks; ++ch) {
     const int t0 = bos + ch * C;
     const int L = min(C, len - ch * C);
+    const uint16_t* sV = sm.rawV[ch & 1];
 
-    // ---------------- phase 0: K, Q -> LDS (fp16), K^T, gates
+    // ================= P0: convert this wave's raw rows; gates; prefetch ch+1
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's DMA and gate loads landed
+    {
+      const int r0 = 16 * wave + 4 * g4;          // this lane's quad of rows
+      const int cc = c16 * 8;                     // and its 8 columns
+      const int pc_lo = (cc & ~15) + ((cc & 8) ? 4 : 0);
+      float kf[4][8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int seg = tid + kThreads * r;     // 1024 segments of 8 halves
-      const int row = seg >> 4;
-      const int c8 = (seg & 15) * 8;
-      uint4 kw = make_uint4(0, 0, 0, 0), qw = make_uint4(0, 0, 0, 0);
-      if (row < L) {
-        const size_t off = size_t(t0 + row) * qk_stride + size_t(hq) * D + c8;
-        kw = *reinterpret_cast<const uint4*>(k + off);
-        qw = *reinterpret_cast<const uint4*>(q + off);
+      for (int r = 0; r < 4; ++r) {
+        const bool valid = r0 + r < L;
+        uint4 kw = *reinterpret_cast<const uint4*>(&sm.rawK[(r0 + r) * D + cc]);
+        uint4 qw = *reinterpret_cast<const uint4*>(&sm.rawQ[(r0 + r) * D + cc]);
+        if (!valid) { kw = make_uint4(0, 0, 0, 0); qw = make_uint4(0, 0, 0, 0); }
+        float qf[8];
+        unpack_bf16x2(kw.x, kf[r][0], kf[r][1]); unpack_bf16x2(kw.y, kf[r][2], kf[r][3]);
+        unpack_bf16x2(kw.z, kf[r][4], kf[r][5]); unpack_bf16x2(kw.w, kf[r][6], kf[r][7]);
+        unpack_bf16x2(qw.x, qf[0], qf[1]); unpack_bf16x2(qw.y, qf[2], qf[3]);
+        unpack_bf16x2(qw.z, qf[4], qf[5]); unpack_bf16x2(qw.w, qf[6], qf[7]);
+        const int row = r0 + r;
+        *reinterpret_cast<f16x4_t*>(&sm.K[row * KLD + pc_lo]) =
+            f16x4_t{(_Float16)kf[r][0], (_Float16)kf[r][1], (_Float16)kf[r][2], (_Float16)kf[r][3]};
+        *reinterpret_cast<f16x4_t*>(&sm.K[row * KLD + pc_lo + 8]) =
+            f16x4_t{(_Float16)kf[r][4], (_Float16)kf[r][5], (_Float16)kf[r][6], (_Float16)kf[r][7]};
+        *reinterpret_cast<f16x4_t*>(&sm.Q[row * KLD + pc_lo]) =
+            f16x4_t{(_Float16)qf[0], (_Float16)qf[1], (_Float16)qf[2], (_Float16)qf[3]};
+        *reinterpret_cast<f16x4_t*>(&sm.Q[row * KLD + pc_lo + 8]) =
+            f16x4_t{(_Float16)qf[4], (_Float16)qf[5], (_Float16)qf[6], (_Float16)qf[7]};
       }
-      float kf[8], qf[8];
-      unpack_bf16x2(kw.x, kf[0], kf[1]); unpack_bf16x2(kw.y, kf[2], kf[3]);
-      unpack_bf16x2(kw.z, kf[4], kf[5]); unpack_bf16x2(kw.w, kf[6], kf[7]);
-      unpack_bf16x2(qw.x, qf[0], qf[1]); unpack_bf16x2(qw.y, qf[2], qf[3]);
-      unpack_bf16x2(qw.z, qf[4], qf[5]); unpack_bf16x2(qw.w, qf[6], qf[7]);
-      f16x4 k0, k1, q0, q1;
+      const int pt = perm16(r0);   // a quad of rows stays contiguous under the permutation
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        k0[e] = (_Float16)kf[e]; k1[e] = (_Float16)kf[4 + e];
-        q0[e] = (_Float16)qf[e]; q1[e] = (_Float16)qf[4 + e];
-      }
-      *reinterpret_cast<f16x4*>(&sm.K[row * KLD + c8]) = k0;
-      *reinterpret_cast<f16x4*>(&sm.K[row * KLD + c8 + 4]) = k1;
-      *reinterpret_cast<f16x4*>(&sm.Q[row * KLD + c8]) = q0;
-      *reinterpret_cast<f16x4*>(&sm.Q[row * KLD + c8 + 4]) = q1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.KT[(c8 + e) * TLD + row] = (_Float16)kf[e];
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<f16x4_t*>(&sm.KT[(cc + e) * TLD + pt]) =
+            f16x4_t{(_Float16)kf[0][e], (_Float16)kf[1][e], (_Float16)kf[2][e], (_Float16)kf[3][e]};
     }
     if (wave == 0) {
-      const int t = lane;
+      // gates: log-decay, its inclusive scan over the chunk, beta
       float ld = 0.f, bt = 0.f;
-      if (t < L) {
-        const size_t gi = size_t(t0 + t) * HV + hv;
-        const float x = bf16_bits_to_f32(a[gi]) + dtb;
-        ld = -a_log_exp * softplus_stable(x);
-        bt = sigmoidf_(bf16_bits_to_f32(b[gi]));
+      if (lane < L) {
+        ld = -a_log_exp * softplus_stable(bf16_bits_to_f32(ra) + dtb);
+        bt = sigmoidf_(bf16_bits_to_f32(rb));
       }
-      // inclusive scan over the 64 lanes
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const float y = __shfl_up(ld, off, 64);
         if (lane >= off) ld += y;
       }
       const float gl = __shfl(ld, L - 1, 64);
-      sm.gam[t] = ld;
-      sm.beta[t] = bt;
-      sm.eg[t] = expf(ld);
-      sm.ed[t] = expf(gl - ld);
+      sm.gam[lane] = ld;
+      sm.beta[lane] = bt;
+      sm.eg[lane] = expf(ld);
+      sm.ed[lane] = expf(gl - ld);
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): raw rows read, they may be refilled
+    if (ch + 1 < n_chunks) issue_chunk(ch + 1);
     __syncthreads();
 
-    // ---------------- phase 1: A (strict, beta-scaled) and P (inclusive) tiles
-    {
-      const int g4 = lane >> 4;    // 16x16 layouts: lane group
-      const int c16 = lane & 15;
+    // ================= P1: A (K K^T, fp32) and P (Q K^T, fp16) tiles, 5 per wave
 #pragma unroll
-      for (int r = 0; r < 5; ++r) {
-        const int task = wave + 4 * r;          // 0..9: K K^T tiles, 10..19: Q K^T tiles
-        const bool is_qk = task >= 10;
-        const int tile = is_qk ? task - 10 : task;
-        // lower tiles (ti >= tj) of the 4x4 grid of 16x16 tiles
-        const int ti = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
-        const int tj = tile - (ti * (ti + 1)) / 2;
-        const _Float16* X = is_qk ? sm.Q : sm.K;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < 5; ++r) {
+      const int task = wave + 4 * r;          // 0..9: K K^T tiles, 10..19: Q K^T tiles
+      const bool is_qk = task >= 10;
+      const int tile = is_qk ? task - 10 : task;
+      const int ti = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
+      const int tj = tile - (ti * (ti + 1)) / 2;
+      const _Float16* X = is_qk ? sm.Q : sm.K;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const f16x8 fa = ld_frag_contig(&X[(16 * ti + c16) * KLD], 32 * ks + 8 * g4);
-          const f16x8 fb = ld_frag_contig(&sm.K[(16 * tj + c16) * KLD], 32 * ks + 8 * g4);
-          acc = mfma16(fa, fb, acc);
-        }
-        const int cc = 16 * tj + c16;
-        const float gc = sm.gam[cc];
+      for (int ks = 0; ks < 4; ++ks)
+        acc = mfma16(ld16(&X[(16 * ti + c16) * KLD + 32 * ks + 8 * g4]),
+                     ld16(&sm.K[(16 * tj + c16) * KLD + 32 * ks + 8 * g4]), acc);
+      const int cc = 16 * tj + c16;
+      const float gc = sm.gam[cc];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rr = 16 * ti + 4 * g4 + i;
-          const float dec = expf(fminf(sm.gam[rr] - gc, 0.f));
-          if (!is_qk) {
-            sm.A[rr * FLD + cc] = rr > cc ? sm.beta[rr] * dec * acc[i] : 0.f;
-          } else {
-            sm.P[rr * TLD + cc] = (_Float16)(rr >= cc ? dec * acc[i] : 0.f);
-          }
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 16 * ti + 4 * g4 + i;
+        const float dec = exp_fast(fminf(sm.gam[rr] - gc, 0.f));
+        if (!is_qk) sm.A[rr * ALD + cc] = rr > cc ? sm.beta[rr] * dec * acc[i] : 0.f;
+        else sm.P[rr * TLD + perm16(cc)] = (_Float16)(rr >= cc ? dec * acc[i] : 0.f);
       }
     }
     __syncthreads();
 
-    // ---------------- phase 2: Tm = (I + A)^-1, blocked 16x16, fp32
-    if (wave == 0) {
-      // diagonal blocks by forward substitution; lane = (block, column)
-      const int bb = lane >> 4, c = lane & 15;
-      const float* Ab = &sm.A[(16 * bb) * FLD + 16 * bb];
+    // ================= P2: diagonal block `wave` of Tm  ||  K S^T, Q S^T, X
+    {
+      // forward substitution in fp32: column c of (I + A_bb)^-1, bb = wave
+      // (the four 16-lane groups compute the same column; all write it)
+      const int bb = wave, c = c16;
+      const float* Ab = &sm.A[(16 * bb) * ALD + 16 * bb];
       float x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float s = (i == c) ? 1.f : 0.f;
 #pragma unroll
-        for (int j = 0; j < i; ++j) s = fmaf(-Ab[i * FLD + j], x[j], s);
+        for (int j4 = 0; j4 < i; j4 += 4) {
+          const f32x4 arow = *reinterpret_cast<const f32x4*>(&Ab[i * ALD + j4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j4 + e < i) s = fmaf(-arow[e], x[j4 + e], s);
+        }
         x[i] = s;
       }
+      const int pc = perm16(16 * bb + c);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sm.TF[(16 * bb + i) * FLD + 16 * bb + c] = x[i];
+      for (int i = 0; i < 16; ++i) sm.Tm[(16 * bb + i) * TLD + pc] = (_Float16)x[i];
     }
-    __syncthreads();
+    f32x16 KS[2], QS[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) { KS[tt] = f32x16{}; QS[tt] = f32x16{}; }
     {
-      // off-diagonal blocks, level by level:  T_ij = -T_ii * sum_{j<=m<i} A_im T_mj
-      const int g4 = lane >> 4, c = lane & 15;
-      float* Yw = &sm.Y[(wave < 3 ? wave : 0) * 16 * 17];
-#pragma unroll 1
-      for (int lvl = 1; lvl <= 3; ++lvl) {
-        const bool active = wave < 4 - lvl;
-        const int bj = wave, bi = wave + lvl;
-        if (active) {
-          float y[4];
+      const _Float16* krow0 = &sm.K[col * KLD + 8 * h];
+      const _Float16* qrow0 = &sm.Q[col * KLD + 8 * h];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int rr = 4 * g4 + i;
-            float s = 0.f;
-            for (int bm = bj; bm < bi; ++bm) {
-              const float* Arow = &sm.A[(16 * bi + rr) * FLD + 16 * bm];
-              const float* Tcol = &sm.TF[(16 * bm) * FLD + 16 * bj + c];
+      for (int j = 0; j < 4; ++j) {
 #pragma unroll
-              for (int m = 0; m < 16; ++m) s = fmaf(Arow[m], Tcol[m * FLD], s);
-            }
-            y[i] = s;
-          }
+        for (int s = 0; s < 2; ++s) {
+          const f16x8 sb = pack8(Sacc[j], s);
+          const int kc = 32 * j + 16 * s;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Yw[(4 * g4 + i) * 17 + c] = y[i];
-        }
-        __syncthreads();
-        if (active) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int rr = 4 * g4 + i;
-            const float* Trow = &sm.TF[(16 * bi + rr) * FLD + 16 * bi];
-            float s = 0.f;
-#pragma unroll
-            for (int m = 0; m < 16; ++m) s = fmaf(Trow[m], Yw[m * 17 + c], s);
-            sm.TF[(16 * bi + rr) * FLD + 16 * bj + c] = -s;
+          for (int tt = 0; tt < 2; ++tt) {
+            KS[tt] = mfma32(ld16(krow0 + 32 * tt * KLD + kc), sb, KS[tt]);
+            QS[tt] = mfma32(ld16(qrow0 + 32 * tt * KLD + kc), sb, QS[tt]);
           }
         }
-        __syncthreads();
       }
     }
-    for (int e = tid; e < C * C; e += kThreads) {
-      const int rr = e >> 6, cc = e & 63;
-      // the upper tiles of the diagonal 32-blocks stay zero from the prologue
-      if (rr >= cc) sm.Tm[rr * TLD + cc] = (_Float16)sm.TF[rr * FLD + cc];
-      else if ((rr >> 5) == (cc >> 5) && ((rr >> 4) & 1) == ((cc >> 4) & 1))
-        sm.Tm[rr * TLD + cc] = (_Float16)0.f;
+    // X = beta (V - e^gam K S^T) in place of KS; e^gam Q S^T in place of QS
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = 32 * tt + acc_row(i, h);
+        const float eg = sm.eg[t];
+        KS[tt][i] = sm.beta[t] * (bf16_bits_to_f32(sV[t * D + vrow]) - eg * KS[tt][i]);
+        QS[tt][i] *= eg;
+      }
     }
     __syncthreads();
 
-    // ---------------- phase 3: the state-dependent chain for rows [32w, 32w+32)
+    // ================= P3: block merges of Tm (wave 0)
+    if (wave == 0) {
+#pragma unroll
+      for (int a0 = 0; a0 < 64; a0 += 32) {
+        // 16-merges inside the diagonal 32-blocks: T21 = -T22 (A21 T11)
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sm.A[(a0 + 16 + c16) * ALD + a0 + 4 * g4]);
+        const f16x4_t fa = {(_Float16)a4[0], (_Float16)a4[1], (_Float16)a4[2], (_Float16)a4[3]};
+        f16x4_t fb;
+        const int pcb = perm16(a0 + c16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) fb[e] = sm.Tm[(a0 + 4 * g4 + e) * TLD + pcb];
+        const f32x4 y = mfma16k16(fa, fb, f32x4{0.f, 0.f, 0.f, 0.f});
+        const f16x4_t ft =
+            *reinterpret_cast<const f16x4_t*>(&sm.Tm[(a0 + 16 + c16) * TLD + perm16(a0 + 16 + 4 * g4)]);
+        const f16x4_t fy = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+        const f32x4 t21 = mfma16k16(ft, fy, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g4 + i) * TLD + pcb] = (_Float16)(-t21[i]);
+      }
+      // 32-merge: T_ba = -T_b (A_ba T_a), a = rows/cols 0..31, b = 32..63
+      f32x16 y = f32x16{};
+      const int pcol = perm16(col);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        f16x8 fb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fb[e] = sm.Tm[(16 * s + 8 * h + e) * TLD + pcol];
+        y = mfma32(ld_f32x8_as_f16(&sm.A[(32 + col) * ALD + 16 * s + 8 * h]), fb, y);
+      }
+      f32x16 tba = f32x16{};
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        tba = mfma32(ld16(&sm.Tm[(32 + col) * TLD + 32 + 16 * s + 8 * h]), pack8(y, s), tba);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
+    }
+    __syncthreads();
+
+    // ================= P4: Vn = Tm X, O = scale (e^gam Q S^T + P Vn), state update
     {
-      // V slice in accumulator layout (issued early)
-      float Vv[2][16];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int t = 32 * tt + acc_row(i, h);
-          Vv[tt][i] = t < L ? bf16_bits_to_f32(v[size_t(t0 + t) * v_stride + size_t(hv) * D + vrow]) : 0.f;
-        }
-      }
-
-      f16x8 Sb[4][2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { Sb[j][0] = pack8(Sacc[j], 0); Sb[j][1] = pack8(Sacc[j], 1); }
-
-      f32x16 KS[2], QS[2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        KS[tt] = f32x16{};
-        QS[tt] = f32x16{};
-        const _Float16* krow = &sm.K[(32 * tt + col) * KLD];
-        const _Float16* qrow = &sm.Q[(32 * tt + col) * KLD];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const int kc = 32 * j + 16 * s + 4 * h;
-            KS[tt] = mfma32(ld_frag_split(krow, kc), Sb[j][s], KS[tt]);
-            QS[tt] = mfma32(ld_frag_split(qrow, kc), Sb[j][s], QS[tt]);
-          }
-        }
-      }
-
-      // X = beta (V - e^gam K S^T)   (reuses KS)
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int t = 32 * tt + acc_row(i, h);
-          KS[tt][i] = sm.beta[t] * (Vv[tt][i] - sm.eg[t] * KS[tt][i]);
-        }
-      }
       f16x8 Xb[2][2];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) { Xb[tt][0] = pack8(KS[tt], 0); Xb[tt][1] = pack8(KS[tt], 1); }
-
-      // Vn = Tm X  (Tm lower triangular in 32-blocks)
-      f32x16 Vn[2] = {f32x16{}, f32x16{}};
+      f16x8 Vnb[2][2], Vdb[2][2];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const _Float16* trow = &sm.Tm[(32 * tt + col) * TLD];
+        f32x16 vn = f32x16{};
+        const _Float16* trow = &sm.Tm[(32 * tt + col) * TLD + 8 * h];
 #pragma unroll
         for (int tp = 0; tp <= tt; ++tp) {
 #pragma unroll
-          for (int s = 0; s < 2; ++s)
-            Vn[tt] = mfma32(ld_frag_split(trow, 32 * tp + 16 * s + 4 * h), Xb[tp][s], Vn[tt]);
+          for (int s = 0; s < 2; ++s) vn = mfma32(ld16(trow + 32 * tp + 16 * s), Xb[tp][s], vn);
         }
-      }
-      f16x8 Vnb[2][2];
+        Vnb[tt][0] = pack8(vn, 0);
+        Vnb[tt][1] = pack8(vn, 1);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) { Vnb[tt][0] = pack8(Vn[tt], 0); Vnb[tt][1] = pack8(Vn[tt], 1); }
-
-      // O = scale (e^gam Q S^T + P Vn)
+        for (int i = 0; i < 16; ++i) vn[i] *= sm.ed[32 * tt + acc_row(i, h)];
+        Vdb[tt][0] = pack8(vn, 0);
+        Vdb[tt][1] = pack8(vn, 1);
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) QS[tt][i] *= sm.eg[32 * tt + acc_row(i, h)];
-        const _Float16* prow = &sm.P[(32 * tt + col) * TLD];
+        const _Float16* prow = &sm.P[(32 * tt + col) * TLD + 8 * h];
 #pragma unroll
         for (int tp = 0; tp <= tt; ++tp) {
 #pragma unroll
-          for (int s = 0; s < 2; ++s)
-            QS[tt] = mfma32(ld_frag_split(prow, 32 * tp + 16 * s + 4 * h), Vnb[tp][s], QS[tt]);
+          for (int s = 0; s < 2; ++s) QS[tt] = mfma32(ld16(prow + 32 * tp + 16 * s), Vnb[tp][s], QS[tt]);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int t = 32 * tt + acc_row(i, h);
-          if (t < L)
-            out[size_t(t0 + t) * v_stride + size_t(hv) * D + vrow] = f32_to_bf16_bits(scale * QS[tt][i]);
+          if (t < L) out[size_t(t0 + t) * v_stride + size_t(hv) * D + vrow] = f32_to_bf16_bits(scale * QS[tt][i]);
         }
-      }
-
-      // S <- e^{gam_L} S + (e^{gam_L - gam} Vn)^T K
-      f16x8 Vdb[2][2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) Vn[tt][i] *= sm.ed[32 * tt + acc_row(i, h)];
-        Vdb[tt][0] = pack8(Vn[tt], 0);
-        Vdb[tt][1] = pack8(Vn[tt], 1);
       }
       const float egL = sm.eg[L - 1];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         Sacc[j] *= egL;
-        const _Float16* ktrow = &sm.KT[(32 * j + col) * TLD];
+        const _Float16* ktrow = &sm.KT[(32 * j + col) * TLD + 8 * h];
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
 #pragma unroll
-          for (int s = 0; s < 2; ++s)
-            Sacc[j] = mfma32(ld_frag_split(ktrow, 32 * tp + 16 * s + 4 * h), Vdb[tp][s], Sacc[j]);
+          for (int s = 0; s < 2; ++s) Sacc[j] = mfma32(ld16(ktrow + 32 * tp + 16 * s), Vdb[tp][s], Sacc[j]);
         }
       }
     }

@@ -147,3 +147,36 @@ def decode_pool_(q, k, v, state_pool, slot_ids, A_log, a, dt_bias, b, scale=None
         _capi.ptr(output), B, nq, nv, float(scale), _capi.stream_handle(q.device))
     _capi.check(rc, "gdn_decode_pool_fwd")
     return output
+
+
+class PreparedDecode:
+    """A decode step on fixed buffers, validated once and launched by one C call.
+
+    For serving loops (and the benchmark) that step the same buffers
+    repeatedly: arguments are checked and resolved to device pointers at
+    construction, the stream is torch's current stream at that time, and
+    ``__call__`` only enqueues the kernel.  ``new_state`` may be ``state``.
+    """
+
+    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
+        B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
+        assert state is None or (state.is_contiguous() and state.dtype == torch.float32
+                                 and state.shape == (B, nv, D, D))
+        assert output.dtype == torch.bfloat16 and output.is_contiguous()
+        assert output.numel() == B * nv * D
+        assert new_state.dtype == torch.float32 and new_state.is_contiguous()
+        assert new_state.shape == (B, nv, D, D)
+        for t in (q, k, v, a, b):
+            assert t.is_contiguous()
+        A_log, dt_bias = _gates(A_log, dt_bias)
+        self._keep = (q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+        self._fn = _capi.lib().gdn_decode_fwd
+        self._args = (
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
+            _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
+            B, nq, nv, float(_resolve_scale(scale, q.shape[-1])), _capi.stream_handle(q.device))
+
+    def __call__(self) -> None:
+        rc = self._fn(*self._args)
+        if rc:
+            _capi.check(rc, "gdn_decode_fwd")

@@ -138,3 +138,41 @@ def run_dps(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, fin
     validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, check_total=False)
     gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
                 final_state=final_state)
+
+
+class PreparedPrefill:
+    """A prefill call on fixed buffers, validated once and launched by one C call.
+
+    ``cu_seqlens`` is read back once here (the reference's ``cu_seqlens[-1]
+    == T`` check); ``__call__`` only enqueues the kernel on the stream that
+    was current at construction.
+    """
+
+    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                 final_state):
+        T, nq, _ = q.shape
+        nv = v.shape[1]
+        validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv)
+        N = cu_seqlens.numel() - 1
+        for t in (q, k, v, a, b, cu_seqlens, A_log, dt_bias):
+            assert t.is_contiguous()
+        assert state is None or state.is_contiguous()
+        assert output.dtype == torch.bfloat16 and output.is_contiguous()
+        assert output.shape == (T, nv, HEAD_SIZE)
+        assert final_state.dtype == torch.float32 and final_state.is_contiguous()
+        assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
+        ws = workspace_bytes(N, T, nq, nv)
+        self._ws = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
+        self._keep = (q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, final_state)
+        self._fn = _capi.lib().gdn_prefill_fwd
+        self._args = (
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
+            _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu_seqlens),
+            1 if cu_seqlens.dtype == torch.int32 else 0, N, T, nq, nv,
+            float(_resolve_scale(scale)), _capi.ptr(output), _capi.ptr(final_state),
+            _capi.ptr(self._ws), ws, _capi.stream_handle(q.device))
+
+    def __call__(self) -> None:
+        rc = self._fn(*self._args)
+        if rc:
+            _capi.check(rc, "gdn_prefill_fwd")
