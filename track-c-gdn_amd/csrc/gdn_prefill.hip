@@ -53,21 +53,33 @@ typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 // bytes.  The map is its own inverse.
 __device__ __forceinline__ int perm16(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
 
+// LDS written by DMA lives in objects of its own, so that the compiler can
+// tell the other LDS accesses from the in-flight DMA writes.
+struct __align__(16) SmemRaw {
+  uint16_t k[C * D];           // next chunk's K rows as loaded (bf16)
+  uint16_t q[C * D];           // next chunk's Q rows as loaded (bf16)
+};
+
 struct __align__(16) Smem {
-  uint16_t rawK[C * D];        // next chunk's K rows as loaded (bf16), filled by DMA
-  uint16_t rawQ[C * D];        // next chunk's Q rows as loaded (bf16), filled by DMA
-  uint16_t rawV[2][C * D];     // V chunks (bf16) [t][v], filled by DMA, double-buffered
   _Float16 K[C * KLD];         // K chunk [t][perm(k)]
   _Float16 Q[C * KLD];         // Q chunk [t][perm(k)]
   _Float16 KT[D * TLD];        // K chunk transposed [k][perm(t)]
   _Float16 Tm[C * TLD];        // (I + A)^-1 [t][perm(t')]
   _Float16 P[C * TLD];         // decayed causal Q K^T [t][perm(t')]
   float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32)
-  float gam[C];                // chunk-local cumsum of the log-decay
-  float beta[C];
-  float eg[C];                 // e^{gam_t}
-  float ed[C];                 // e^{gam_{L-1} - gam_t}
+  float gam[2][C];             // chunk-local cumsum of the log-decay (double-buffered)
+  float beta[2][C];
+  float eg[2][C];              // e^{gam_t}
+  float ed[2][C];              // e^{gam_{L-1} - gam_t}
 };
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its outstanding global loads or HBM->LDS DMA (those are
+// waited for explicitly where their data is consumed).  The asm statement is
+// a compiler memory barrier as well.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ f16x8 ld16(const _Float16* p) { return *reinterpret_cast<const f16x8*>(p); }
 
@@ -102,8 +114,16 @@ __device__ __forceinline__ int acc_row(int i, int h) { return 8 * (i >> 2) + 4 *
 
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
+// HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l's
+// bytes land at lds_dst + 16 l; lds_dst must be uniform across the wave.
+// Issued from asm so that the compiler does not wait for it at the next LDS
+// access it cannot disambiguate; every consumer of the copied data waits for
+// it explicitly (vmcnt) and then crosses a barrier.
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_addr), "v"(src) : "memory");
 }
 
 template <typename CuT>
@@ -115,6 +135,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const CuT* __restrict__ cu_seqlens, int T, int HQ, int HV, float scale,
     uint16_t* __restrict__ out, float* __restrict__ ht) {
   __shared__ Smem sm;
+  __shared__ SmemRaw raw;
+  __shared__ __align__(16) uint16_t rawV[C * D];    // V chunk (bf16) [t][v], filled by DMA
 
   const int n = blockIdx.x / HV;
   const int hv = blockIdx.x - n * HV;
@@ -155,25 +177,56 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // rows, so no other wave touches its raw rows in between.  Lane l of DMA
   // instruction r carries row 16w + 4r + l/16, columns 8(l%16)..+7; rows past
   // the chunk end are clamped to its last row (zeroed at conversion).
-  uint16_t ra = 0, rb = 0;            // gate inputs of row `lane` (wave 0)
-  auto issue_chunk = [&](int ch) {
+  uint16_t ra = 0, rb = 0;            // gate inputs of row `lane` (wave 1)
+  // K / Q rows of chunk ch (issued once this wave has converted the previous
+  // chunk's raw rows) and the gate inputs of chunk ch (wave 1).
+  auto issue_kq = [&](int ch) {
+    const int t0 = bos + ch * C;
+    const int L = min(C, len - ch * C);
+    if (wave == 1) {
+      const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
+      ra = a[gi];
+      rb = b[gi];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row0 = 16 * wave + 4 * r;
+      const int row = min(row0 + (lane >> 4), L - 1);
+      const size_t off = size_t(t0 + row) * qk_stride + size_t(hq) * D + (lane & 15) * 8;
+      lds_dma16(k + off, &raw.k[row0 * D]);
+      lds_dma16(q + off, &raw.q[row0 * D]);
+    }
+  };
+  // V rows of chunk ch (issued once every wave has read the previous chunk's V).
+  auto issue_v = [&](int ch) {
     const int t0 = bos + ch * C;
     const int L = min(C, len - ch * C);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row0 = 16 * wave + 4 * r;
       const int row = min(row0 + (lane >> 4), L - 1);
-      const size_t off = size_t(t0 + row) * qk_stride + size_t(hq) * D + (lane & 15) * 8;
-      lds_dma16(k + off, &sm.rawK[row0 * D]);
-      lds_dma16(q + off, &sm.rawQ[row0 * D]);
-      lds_dma16(v + size_t(t0 + row) * v_stride + size_t(hv) * D + (lane & 15) * 8,
-                &sm.rawV[ch & 1][row0 * D]);
+      lds_dma16(v + size_t(t0 + row) * v_stride + size_t(hv) * D + (lane & 15) * 8, &rawV[row0 * D]);
     }
-    if (wave == 0) {
-      const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
-      ra = a[gi];
-      rb = b[gi];
+  };
+  // Gates of chunk ch (wave 1): log-decay, its inclusive scan, beta, decays.
+  auto gates_chunk = [&](int ch) {
+    const int L = min(C, len - ch * C);
+    const int gb = ch & 1;
+    float ld = 0.f, bt = 0.f;
+    if (lane < L) {
+      ld = -a_log_exp * softplus_stable(bf16_bits_to_f32(ra) + dtb);
+      bt = sigmoidf_(bf16_bits_to_f32(rb));
     }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(ld, off, 64);
+      if (lane >= off) ld += y;
+    }
+    const float gl = __shfl(ld, L - 1, 64);
+    sm.gam[gb][lane] = ld;
+    sm.beta[gb][lane] = bt;
+    sm.eg[gb][lane] = expf(ld);
+    sm.ed[gb][lane] = expf(gl - ld);
   };
 
   // ---- initial state: S^T tiles, Sacc[j][i] = S[vrow][32j + acc_row(i, h)]
@@ -192,15 +245,46 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     }
   }
 
-  if (n_chunks > 0) issue_chunk(0);
+  if (n_chunks > 0) {
+    issue_kq(0);
+    if (wave == 1) gates_chunk(0);
+    issue_v(0);
+  }
+  // Output of the previous chunk, packed bf16 pairs in accumulator order: it
+  // is stored at the start of the next chunk, so that no recent store sits
+  // in front of the waits for the DMA.
+  uint32_t opack[2][8];
+  int o_t0 = 0;
 
   for (int ch = 0; ch < n_chunks; ++ch) {
     const int t0 = bos + ch * C;
     const int L = min(C, len - ch * C);
-    const uint16_t* sV = sm.rawV[ch & 1];
+    const uint16_t* sV = rawV;
+    const int gb = ch & 1;
+    const float* g_gam = sm.gam[gb];
+    const float* g_beta = sm.beta[gb];
+    const float* g_eg = sm.eg[gb];
+    const float* g_ed = sm.ed[gb];
 
     // ================= P0: convert this wave's raw rows; gates; prefetch ch+1
-    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's DMA and gate loads landed
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's DMA of chunk ch landed
+    if (ch > 0) {
+      // output of chunk ch-1 (a full chunk: only the last chunk can be ragged).
+      // Row 32tt + 8g + 4h + r: a uniform row pointer plus a per-lane offset.
+      const uint32_t loff = uint32_t(vrow) + uint32_t(4 * h) * uint32_t(v_stride);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = 4 * g + r;
+            uint16_t* rowp = out + size_t(o_t0 + 32 * tt + 8 * g + r) * v_stride + size_t(hv) * D;
+            rowp[loff] = uint16_t(opack[tt][i >> 1] >> (16 * (i & 1)));
+          }
+        }
+      }
+    }
     {
       const int r0 = 16 * wave + 4 * g4;          // this lane's quad of rows
       const int cc = c16 * 8;                     // and its 8 columns
@@ -209,8 +293,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool valid = r0 + r < L;
-        uint4 kw = *reinterpret_cast<const uint4*>(&sm.rawK[(r0 + r) * D + cc]);
-        uint4 qw = *reinterpret_cast<const uint4*>(&sm.rawQ[(r0 + r) * D + cc]);
+        uint4 kw = *reinterpret_cast<const uint4*>(&raw.k[(r0 + r) * D + cc]);
+        uint4 qw = *reinterpret_cast<const uint4*>(&raw.q[(r0 + r) * D + cc]);
         if (!valid) { kw = make_uint4(0, 0, 0, 0); qw = make_uint4(0, 0, 0, 0); }
         float qf[8];
         unpack_bf16x2(kw.x, kf[r][0], kf[r][1]); unpack_bf16x2(kw.y, kf[r][2], kf[r][3]);
@@ -233,27 +317,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         *reinterpret_cast<f16x4_t*>(&sm.KT[(cc + e) * TLD + pt]) =
             f16x4_t{(_Float16)kf[0][e], (_Float16)kf[1][e], (_Float16)kf[2][e], (_Float16)kf[3][e]};
     }
-    if (wave == 0) {
-      // gates: log-decay, its inclusive scan over the chunk, beta
-      float ld = 0.f, bt = 0.f;
-      if (lane < L) {
-        ld = -a_log_exp * softplus_stable(bf16_bits_to_f32(ra) + dtb);
-        bt = sigmoidf_(bf16_bits_to_f32(rb));
-      }
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(ld, off, 64);
-        if (lane >= off) ld += y;
-      }
-      const float gl = __shfl(ld, L - 1, 64);
-      sm.gam[lane] = ld;
-      sm.beta[lane] = bt;
-      sm.eg[lane] = expf(ld);
-      sm.ed[lane] = expf(gl - ld);
-    }
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): raw rows read, they may be refilled
-    if (ch + 1 < n_chunks) issue_chunk(ch + 1);
-    __syncthreads();
+    if (ch + 1 < n_chunks) issue_kq(ch + 1);
+    lds_barrier();
 
     // ================= P1: A (K K^T, fp32) and P (Q K^T, fp16) tiles, 5 per wave
 #pragma unroll
@@ -264,22 +330,26 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       const int ti = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
       const int tj = tile - (ti * (ti + 1)) / 2;
       const _Float16* X = is_qk ? sm.Q : sm.K;
+      f16x8 fa[4], fb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        fa[ks] = ld16(&X[(16 * ti + c16) * KLD + 32 * ks + 8 * g4]);
+        fb[ks] = ld16(&sm.K[(16 * tj + c16) * KLD + 32 * ks + 8 * g4]);
+      }
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        acc = mfma16(ld16(&X[(16 * ti + c16) * KLD + 32 * ks + 8 * g4]),
-                     ld16(&sm.K[(16 * tj + c16) * KLD + 32 * ks + 8 * g4]), acc);
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[ks], fb[ks], acc);
       const int cc = 16 * tj + c16;
-      const float gc = sm.gam[cc];
+      const float gc = g_gam[cc];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int rr = 16 * ti + 4 * g4 + i;
-        const float dec = exp_fast(fminf(sm.gam[rr] - gc, 0.f));
-        if (!is_qk) sm.A[rr * ALD + cc] = rr > cc ? sm.beta[rr] * dec * acc[i] : 0.f;
+        const float dec = exp_fast(fminf(g_gam[rr] - gc, 0.f));
+        if (!is_qk) sm.A[rr * ALD + cc] = rr > cc ? g_beta[rr] * dec * acc[i] : 0.f;
         else sm.P[rr * TLD + perm16(cc)] = (_Float16)(rr >= cc ? dec * acc[i] : 0.f);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ================= P2: diagonal block `wave` of Tm  ||  K S^T, Q S^T, X
     {
@@ -328,16 +398,26 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int t = 32 * tt + acc_row(i, h);
-        const float eg = sm.eg[t];
-        KS[tt][i] = sm.beta[t] * (bf16_bits_to_f32(sV[t * D + vrow]) - eg * KS[tt][i]);
-        QS[tt][i] *= eg;
+      for (int g = 0; g < 4; ++g) {
+        const int t4 = 32 * tt + 8 * g + 4 * h;     // rows of elements 4g..4g+3
+        const f32x4 eg = *reinterpret_cast<const f32x4*>(&g_eg[t4]);
+        const f32x4 bt = *reinterpret_cast<const f32x4*>(&g_beta[t4]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 4 * g + r;
+          KS[tt][i] = bt[r] * (bf16_bits_to_f32(sV[(t4 + r) * D + vrow]) - eg[r] * KS[tt][i]);
+          QS[tt][i] *= eg[r];
+        }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ================= P3: block merges of Tm (wave 0)
+    // ================= P3: block merges of Tm (wave 0); gates of chunk ch+1 (wave 1);
+    // V of chunk ch+1 (every wave has read V of chunk ch)
+    if (ch + 1 < n_chunks) {
+      if (wave == 1) gates_chunk(ch + 1);   // its loads were issued before the K/Q DMA
+      issue_v(ch + 1);
+    }
     if (wave == 0) {
 #pragma unroll
       for (int a0 = 0; a0 < 64; a0 += 32) {
@@ -373,7 +453,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ================= P4: Vn = Tm X, O = scale (e^gam Q S^T + P Vn), state update
     {
@@ -393,7 +473,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         Vnb[tt][0] = pack8(vn, 0);
         Vnb[tt][1] = pack8(vn, 1);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) vn[i] *= sm.ed[32 * tt + acc_row(i, h)];
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 ed = *reinterpret_cast<const f32x4*>(&g_ed[32 * tt + 8 * g + 4 * h]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vn[4 * g + r] *= ed[r];
+        }
         Vdb[tt][0] = pack8(vn, 0);
         Vdb[tt][1] = pack8(vn, 1);
       }
@@ -406,12 +490,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           for (int s = 0; s < 2; ++s) QS[tt] = mfma32(ld16(prow + 32 * tp + 16 * s), Vnb[tp][s], QS[tt]);
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int t = 32 * tt + acc_row(i, h);
-          if (t < L) out[size_t(t0 + t) * v_stride + size_t(hv) * D + vrow] = f32_to_bf16_bits(scale * QS[tt][i]);
-        }
+        for (int i = 0; i < 8; ++i)
+          opack[tt][i] = pack_bf16x2(scale * QS[tt][2 * i], scale * QS[tt][2 * i + 1]);
       }
-      const float egL = sm.eg[L - 1];
+      o_t0 = t0;
+      const float egL = g_eg[L - 1];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         Sacc[j] *= egL;
@@ -423,7 +506,25 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
+  }
+
+  // ---- output of the last chunk (rows past its end are not written)
+  if (n_chunks > 0) {
+    const int L = len - (n_chunks - 1) * C;
+    const uint32_t loff = uint32_t(vrow) + uint32_t(4 * h) * uint32_t(v_stride);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 4 * g + r;
+          uint16_t* rowp = out + size_t(o_t0 + 32 * tt + 8 * g + r) * v_stride + size_t(hv) * D;
+          if (32 * tt + acc_row(i, h) < L) rowp[loff] = uint16_t(opack[tt][i >> 1] >> (16 * (i & 1)));
+        }
+      }
+    }
   }
 
   // ---- final state
