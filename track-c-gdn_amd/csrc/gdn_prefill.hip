@@ -39,55 +39,86 @@ using namespace gdn;
 
 constexpr int D = kHeadDim;   // 128
 constexpr int C = 64;         // chunk
-constexpr int KLD = D + 8;    // sK / sQ row stride (halves): 272 B rows
-constexpr int TLD = C + 8;    // sKT / sTm / sP row stride (halves): 144 B rows
-constexpr int ALD = C + 4;    // sA row stride (floats): 272 B rows
-constexpr int kThreads = 256; // 4 waves, one per SIMD
+constexpr int KCLD = D + 8;   // Kc / Qc / Ost row stride (halves): 272 B rows
+constexpr int TLD = C + 8;    // Tm / P row stride (halves): 144 B rows
+constexpr int ALD = C + 4;    // A row stride (floats): 272 B rows
+constexpr int GSZ = 4 * C;    // floats of gate data per chunk: gam, beta, e^gam, e^(gam_L - gam)
+constexpr int kWaves = 8;     // two per SIMD
+constexpr int kThreads = kWaves * 64;
+constexpr int kRowsPerWave = D / kWaves;   // 16 state rows (v) per wave
+constexpr int kGateThreads = 256;          // gate pre-pass: one wave per chunk
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-// Column order inside every 16-column group of the fp16 operand tiles: the
-// two middle quads are swapped (bits 2 and 3 of the index), so that the 8
-// k-slots lane half h feeds an MFMA -- rows {0-3, 8-11} (h = 0) or
-// {4-7, 12-15} (h = 1) of a 16-row accumulator block -- are 16 contiguous
-// bytes.  The map is its own inverse.
-__device__ __forceinline__ int perm16(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
+// Column order inside every 32-column group of the fp16 operand tiles: column
+// 16 a + 4 q + r is stored at position 8 q + 4 a + r.  The 8 k-slots that
+// lane group q feeds a 16x16x32 MFMA from two stacked 16x16 accumulator tiles
+// -- rows 4q..4q+3 of each -- are then 16 contiguous bytes, and every quad
+// of 4 consecutive columns stays contiguous.
+__device__ __forceinline__ int p32(int c) {
+  return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
+}
 
-// LDS written by DMA lives in objects of its own, so that the compiler can
-// tell the other LDS accesses from the in-flight DMA writes.
+// Raw bf16 rows as copied from HBM: 16-byte chunk c of row t sits in slot
+// c ^ (t & 15) of that row (the copy picks which global chunk each lane
+// fetches), so column reads down 16 consecutive rows hit 16 distinct banks.
+__device__ __forceinline__ int raw_off(int t, int col) { return t * D + 8 * ((col >> 3) ^ (t & 15)) + (col & 7); }
+
 struct __align__(16) SmemRaw {
-  uint16_t k[C * D];           // next chunk's K rows as loaded (bf16)
-  uint16_t q[C * D];           // next chunk's Q rows as loaded (bf16)
+  uint16_t k[C * D];           // next chunk's K rows (bf16, swizzled), DMA target
+  uint16_t q[C * D];           // next chunk's Q rows (bf16, swizzled), DMA target
 };
 
 struct __align__(16) Smem {
-  _Float16 K[C * KLD];         // K chunk [t][perm(k)]
-  _Float16 Q[C * KLD];         // Q chunk [t][perm(k)]
-  _Float16 KT[D * TLD];        // K chunk transposed [k][perm(t)]
-  _Float16 Tm[C * TLD];        // (I + A)^-1 [t][perm(t')]
-  _Float16 P[C * TLD];         // decayed causal Q K^T [t][perm(t')]
+  _Float16 Kc[2][C * KCLD];    // K chunk in fp16 [t][p32(k)], double-buffered
+  _Float16 Qc[C * KCLD];       // Q chunk in fp16 [t][p32(k)]
+  _Float16 Tm[C * TLD];        // (I + A)^-1 [t][p32(t')]
+  _Float16 P[C * TLD];         // decayed causal Q K^T [t][p32(t')]
   float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32)
-  float gam[2][C];             // chunk-local cumsum of the log-decay (double-buffered)
-  float beta[2][C];
-  float eg[2][C];              // e^{gam_t}
-  float ed[2][C];              // e^{gam_{L-1} - gam_t}
+  uint16_t Ost[C * KCLD];      // output chunk staging (bf16) [t][v]
 };
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
-// operations, not for its outstanding global loads or HBM->LDS DMA (those are
-// waited for explicitly where their data is consumed).  The asm statement is
-// a compiler memory barrier as well.
+// operations, not for outstanding global stores or HBM->LDS copies.  The asm
+// statement is a compiler memory barrier as well.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Waits until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
 __device__ __forceinline__ f16x8 ld16(const _Float16* p) { return *reinterpret_cast<const f16x8*>(p); }
+
+__device__ __forceinline__ bf16x8_t ld16_bf(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16): inside each 16-lane group, lane i
+// receives element i % 4 of the 8-byte reads issued by lanes 4 m + i / 4,
+// m = 0..3, of the same group.
+__device__ __forceinline__ f16x4_t ld_tr16(const _Float16* p) {
+  return __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                         (__attribute__((address_space(3))) i16x4_t*)p));
+}
 
 __device__ __forceinline__ f16x8 ld_f32x8_as_f16(const float* p) {
   const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
   const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
   return f16x8{(_Float16)lo[0], (_Float16)lo[1], (_Float16)lo[2], (_Float16)lo[3],
                (_Float16)hi[0], (_Float16)hi[1], (_Float16)hi[2], (_Float16)hi[3]};
+}
+
+// Two stacked 16x16 accumulator tiles -> one 8-slot fp16 operand.
+__device__ __forceinline__ f16x8 pack2(const f32x4& a, const f32x4& b) {
+  return f16x8{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
+               (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
 }
 
 __device__ __forceinline__ f16x8 pack8(const f32x16& x, int s) {
@@ -105,6 +136,10 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ f32x4 mfma16_bf(bf16x8_t a, bf16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ f32x4 mfma16k16(f16x4_t a, f16x4_t b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
@@ -116,9 +151,9 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 
 // HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l's
 // bytes land at lds_dst + 16 l; lds_dst must be uniform across the wave.
-// Issued from asm so that the compiler does not wait for it at the next LDS
-// access it cannot disambiguate; every consumer of the copied data waits for
-// it explicitly (vmcnt) and then crosses a barrier.
+// Issued from asm so that the compiler does not wait for it at LDS accesses
+// it cannot tell apart from the destination; every consumer of the copied
+// data waits for it explicitly (wait_vm) and then crosses a barrier.
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
   const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
@@ -126,96 +161,48 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
                :: "s"(lds_addr), "v"(src) : "memory");
 }
 
+// Tokens [bos, bos + len) of sequence n, clamped into [0, T].
 template <typename CuT>
-__global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const float* __restrict__ h0,
+__device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {
+  long long b0 = (long long)cu[n], e0 = (long long)cu[n + 1];
+  b0 = b0 < 0 ? 0 : (b0 > T ? T : b0);
+  e0 = e0 < b0 ? b0 : (e0 > T ? T : e0);
+  bos = int(b0);
+  len = int(e0 - b0);
+}
+
+// Gate-data slot of chunk 0 of sequence n: floor(bos / C) + n.  For ordered
+// sequences the slot ranges are disjoint, and for any clamped bounds the last
+// slot is at most floor(T / C) + N - 1, which sizes the workspace.
+__device__ __forceinline__ int gate_slot0(int bos, int n) { return bos / C + n; }
+
+// Gates of every chunk (reference PRE:1706-1722 and the chunk-local cumsum of
+// PRE:1721): one block per (v-head, sequence), one wave per chunk, lane = token.
+// Writes, per chunk, gam (chunk-local cumsum of the log-decay), beta, e^gam and
+// e^(gam_last - gam) to gws[(chunk, hv)]; rows past the sequence end carry a
+// zero log-decay and beta = 0.
+template <typename CuT>
+__global__ __launch_bounds__(kGateThreads) void gdn_prefill_gates_kernel(
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
-    const CuT* __restrict__ cu_seqlens, int T, int HQ, int HV, float scale,
-    uint16_t* __restrict__ out, float* __restrict__ ht) {
-  __shared__ Smem sm;
-  __shared__ SmemRaw raw;
-  __shared__ __align__(16) uint16_t rawV[C * D];    // V chunk (bf16) [t][v], filled by DMA
-
-  const int n = blockIdx.x / HV;
-  const int hv = blockIdx.x - n * HV;
-  const int hq = hv / (HV / HQ);
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int h = lane >> 5;        // lane half (32x32 MFMA layouts)
-  const int col = lane & 31;
-  const int g4 = lane >> 4;       // lane group (16x16 MFMA layouts)
-  const int c16 = lane & 15;
-  const int vrow = 32 * wave + col;   // state row v owned by this lane
-
-  long long bos_l = (long long)cu_seqlens[n];
-  long long eos_l = (long long)cu_seqlens[n + 1];
-  bos_l = bos_l < 0 ? 0 : (bos_l > T ? T : bos_l);
-  eos_l = eos_l < bos_l ? bos_l : (eos_l > T ? T : eos_l);
-  const int bos = int(bos_l);
-  const int len = int(eos_l - bos_l);
-
+    const CuT* __restrict__ cu_seqlens, int T, int HV, float* __restrict__ gws) {
+  const int hv = blockIdx.x;
+  const int n = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int bos, len;
+  seq_bounds(cu_seqlens, n, T, bos, len);
+  const int slot0 = gate_slot0(bos, n);
+  const int n_chunks = (len + C - 1) / C;
   const float a_log_exp = expf(A_log[hv]);
   const float dtb = dt_bias[hv];
-  const size_t qk_stride = size_t(HQ) * D;   // elements per token in q / k
-  const size_t v_stride = size_t(HV) * D;    // elements per token in v / out
-  const int n_chunks = (len + C - 1) / C;
-
-  // Upper 16x16 tiles inside the diagonal 32x32 blocks of Tm / P are read by
-  // the 32x32 products and must be zero; they are never written afterwards.
-  for (int e = tid; e < 2 * 16 * 16; e += kThreads) {
-    const int blk = e >> 8, r = (e >> 4) & 15, c = e & 15;
-    const int R = 32 * blk + r, Cc = 32 * blk + 16 + c;
-    sm.Tm[R * TLD + Cc] = (_Float16)0.f;
-    sm.P[R * TLD + Cc] = (_Float16)0.f;
-  }
-
-  // Wave w owns chunk rows [16w, 16w+16) of the staging: it DMAs them from
-  // HBM into rawK / rawQ / rawV one chunk ahead and converts the same K / Q
-  // rows, so no other wave touches its raw rows in between.  Lane l of DMA
-  // instruction r carries row 16w + 4r + l/16, columns 8(l%16)..+7; rows past
-  // the chunk end are clamped to its last row (zeroed at conversion).
-  uint16_t ra = 0, rb = 0;            // gate inputs of row `lane` (wave 1)
-  // K / Q rows of chunk ch (issued once this wave has converted the previous
-  // chunk's raw rows) and the gate inputs of chunk ch (wave 1).
-  auto issue_kq = [&](int ch) {
-    const int t0 = bos + ch * C;
+  for (int ch = wave; ch < n_chunks; ch += kGateThreads / 64) {
     const int L = min(C, len - ch * C);
-    if (wave == 1) {
-      const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
-      ra = a[gi];
-      rb = b[gi];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row0 = 16 * wave + 4 * r;
-      const int row = min(row0 + (lane >> 4), L - 1);
-      const size_t off = size_t(t0 + row) * qk_stride + size_t(hq) * D + (lane & 15) * 8;
-      lds_dma16(k + off, &raw.k[row0 * D]);
-      lds_dma16(q + off, &raw.q[row0 * D]);
-    }
-  };
-  // V rows of chunk ch (issued once every wave has read the previous chunk's V).
-  auto issue_v = [&](int ch) {
-    const int t0 = bos + ch * C;
-    const int L = min(C, len - ch * C);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row0 = 16 * wave + 4 * r;
-      const int row = min(row0 + (lane >> 4), L - 1);
-      lds_dma16(v + size_t(t0 + row) * v_stride + size_t(hv) * D + (lane & 15) * 8, &rawV[row0 * D]);
-    }
-  };
-  // Gates of chunk ch (wave 1): log-decay, its inclusive scan, beta, decays.
-  auto gates_chunk = [&](int ch) {
-    const int L = min(C, len - ch * C);
-    const int gb = ch & 1;
     float ld = 0.f, bt = 0.f;
     if (lane < L) {
-      ld = -a_log_exp * softplus_stable(bf16_bits_to_f32(ra) + dtb);
-      bt = sigmoidf_(bf16_bits_to_f32(rb));
+      const size_t gi = size_t(bos + ch * C + lane) * HV + hv;
+      ld = -a_log_exp * softplus_stable(bf16_bits_to_f32(a[gi]) + dtb);
+      bt = sigmoidf_(bf16_bits_to_f32(b[gi]));
     }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -223,144 +210,196 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       if (lane >= off) ld += y;
     }
     const float gl = __shfl(ld, L - 1, 64);
-    sm.gam[gb][lane] = ld;
-    sm.beta[gb][lane] = bt;
-    sm.eg[gb][lane] = expf(ld);
-    sm.ed[gb][lane] = expf(gl - ld);
+    float* g = gws + (size_t(slot0 + ch) * HV + hv) * GSZ;
+    g[lane] = ld;
+    g[C + lane] = bt;
+    g[2 * C + lane] = expf(ld);
+    g[3 * C + lane] = expf(gl - ld);
+  }
+}
+
+// The state chain.  One workgroup (8 waves, two per SIMD) per (sequence,
+// v-head); wave w owns state rows v in [16w, 16w+16) and runs all of its
+// products as 16x16x32 MFMAs.  Software pipeline: in iteration i the waves run
+// the state-dependent work of chunk i and the state-independent preparation of
+// chunk i+1, in three phases separated by LDS barriers:
+//   P1  chain i : K S^T, Q S^T, X            prep : 32-row merge of Tm_i (wave 7)
+//   P2  chain i : Tm X, O -> Ost, Vd          prep : A_{i+1} = K K^T tiles, K/Q_{i+1} -> fp16
+//   P3  chain i : S update (K^T by            prep : diagonal blocks and 16-row merges of
+//                 transposing LDS reads)            Tm_{i+1} (waves 0-1), P_{i+1} tiles
+//                                                   (waves 2-7), stores of O_i, copies
+//                                                   of chunk i+2
+// Copies into LDS (K, Q, V rows, gate data) are issued two phases or more
+// before their first use and waited for with explicit vmcnt counts.
+template <typename CuT>
+__global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* __restrict__ h0,
+    const CuT* __restrict__ cu_seqlens, const float* __restrict__ gws, int T, int HQ, int HV,
+    float scale, uint16_t* __restrict__ out, float* __restrict__ ht) {
+  __shared__ Smem sm;
+  __shared__ SmemRaw raw;
+  __shared__ __align__(16) uint16_t rawV[C * D];     // V chunk (bf16, swizzled), DMA target
+  __shared__ __align__(16) float gbuf[2][GSZ];       // gate data, DMA target, double-buffered
+
+  const int n = blockIdx.x / HV;
+  const int hv = blockIdx.x - n * HV;
+  const int hq = hv / (HV / HQ);
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane >> 4;        // lane group (16x16 MFMA layouts)
+  const int c = lane & 15;
+  const int v0 = kRowsPerWave * wave;
+  const int vrow = v0 + c;        // state row v owned by this lane
+
+  int bos, len;
+  seq_bounds(cu_seqlens, n, T, bos, len);
+  const int slot0 = gate_slot0(bos, n);
+  const size_t qk_stride = size_t(HQ) * D;   // elements per token in q / k
+  const size_t v_stride = size_t(HV) * D;    // elements per token in v / out
+  const int n_chunks = (len + C - 1) / C;
+  auto chunk_len = [&](int ch) { return min(C, len - ch * C); };
+
+  // Upper 16x16 tiles inside the diagonal 32x32 blocks of Tm / P are read by
+  // the products and must be zero; they are never written afterwards.
+  for (int e = tid; e < 2 * 16 * 16; e += kThreads) {
+    const int blk = e >> 8, r = (e >> 4) & 15, cc = e & 15;
+    const int R = 32 * blk + r, pc = p32(32 * blk + 16 + cc);
+    sm.Tm[R * TLD + pc] = (_Float16)0.f;
+    sm.P[R * TLD + pc] = (_Float16)0.f;
+  }
+
+  // ---------------- copies into LDS.  An instruction covers 4 rows: lane l
+  // carries row row0 + l/16, swizzle slot l%16 (rows past the chunk end are
+  // clamped to its last row).  Wave w copies K/Q rows [8w, 8w+8) and V rows
+  // [8w, 8w+8).
+  auto copy_kq = [&](int ch) {      // 4 instructions per wave (+1 gate row on wave 0)
+    const int t0 = bos + ch * C;
+    const int L = chunk_len(ch);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row0 = 8 * wave + 4 * r;
+      const int row = row0 + (lane >> 4);
+      const int src_chunk = (lane & 15) ^ (row & 15);
+      const size_t off = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_chunk;
+      lds_dma16(k + off, &raw.k[row0 * D]);
+      lds_dma16(q + off, &raw.q[row0 * D]);
+    }
+    if (wave == 0) lds_dma16(gws + (size_t(slot0 + ch) * HV + hv) * GSZ + 4 * lane, &gbuf[ch & 1][0]);
+  };
+  auto copy_v = [&](int ch) {       // 2 instructions per wave
+    const int t0 = bos + ch * C;
+    const int L = chunk_len(ch);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row0 = 8 * wave + 4 * r;
+      const int row = row0 + (lane >> 4);
+      const int src_chunk = (lane & 15) ^ (row & 15);
+      lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + 8 * src_chunk,
+                &rawV[row0 * D]);
+    }
   };
 
-  // ---- initial state: S^T tiles, Sacc[j][i] = S[vrow][32j + acc_row(i, h)]
-  f32x16 Sacc[4];
-  const size_t state_off = (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
+  // ---------------- preparation steps (state-independent)
+  // K/Q rows (raw bf16) -> Kc[kb] / Qc in fp16, rows past the end -> 0.  Two
+  // 8-column pieces per lane.
+  auto convert_kq = [&](int ch, int kb) {
+    const int L = chunk_len(ch);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      f32x4 x = {0.f, 0.f, 0.f, 0.f};
-      if (h0 != nullptr) x = *reinterpret_cast<const f32x4*>(h0 + state_off + 32 * j + 8 * g + 4 * h);
-      Sacc[j][4 * g + 0] = x[0];
-      Sacc[j][4 * g + 1] = x[1];
-      Sacc[j][4 * g + 2] = x[2];
-      Sacc[j][4 * g + 3] = x[3];
+    for (int r = 0; r < 2; ++r) {
+      const int item = tid + kThreads * r;
+      const int row = item >> 4;
+      const int cc = (item & 15) * 8;                 // logical columns cc..cc+7
+      uint4 kw = *reinterpret_cast<const uint4*>(&raw.k[raw_off(row, cc)]);
+      uint4 qw = *reinterpret_cast<const uint4*>(&raw.q[raw_off(row, cc)]);
+      const uint32_t m = row < L ? 0xffffffffu : 0u;
+      kw.x &= m; kw.y &= m; kw.z &= m; kw.w &= m;
+      qw.x &= m; qw.y &= m; qw.z &= m; qw.w &= m;
+      float kf[8], qf[8];
+      unpack_bf16x2(kw.x, kf[0], kf[1]); unpack_bf16x2(kw.y, kf[2], kf[3]);
+      unpack_bf16x2(kw.z, kf[4], kf[5]); unpack_bf16x2(kw.w, kf[6], kf[7]);
+      unpack_bf16x2(qw.x, qf[0], qf[1]); unpack_bf16x2(qw.y, qf[2], qf[3]);
+      unpack_bf16x2(qw.z, qf[4], qf[5]); unpack_bf16x2(qw.w, qf[6], qf[7]);
+      _Float16* kd = &sm.Kc[kb][row * KCLD];
+      _Float16* qd = &sm.Qc[row * KCLD];
+      const int pa = p32(cc), pb = p32(cc + 4);
+      *reinterpret_cast<f16x4_t*>(kd + pa) = f16x4_t{(_Float16)kf[0], (_Float16)kf[1], (_Float16)kf[2], (_Float16)kf[3]};
+      *reinterpret_cast<f16x4_t*>(kd + pb) = f16x4_t{(_Float16)kf[4], (_Float16)kf[5], (_Float16)kf[6], (_Float16)kf[7]};
+      *reinterpret_cast<f16x4_t*>(qd + pa) = f16x4_t{(_Float16)qf[0], (_Float16)qf[1], (_Float16)qf[2], (_Float16)qf[3]};
+      *reinterpret_cast<f16x4_t*>(qd + pb) = f16x4_t{(_Float16)qf[4], (_Float16)qf[5], (_Float16)qf[6], (_Float16)qf[7]};
     }
-  }
-
-  if (n_chunks > 0) {
-    issue_kq(0);
-    if (wave == 1) gates_chunk(0);
-    issue_v(0);
-  }
-  // Output of the previous chunk, packed bf16 pairs in accumulator order: it
-  // is stored at the start of the next chunk, so that no recent store sits
-  // in front of the waits for the DMA.
-  uint32_t opack[2][8];
-  int o_t0 = 0;
-
-  for (int ch = 0; ch < n_chunks; ++ch) {
-    const int t0 = bos + ch * C;
-    const int L = min(C, len - ch * C);
-    const uint16_t* sV = rawV;
-    const int gb = ch & 1;
-    const float* g_gam = sm.gam[gb];
-    const float* g_beta = sm.beta[gb];
-    const float* g_eg = sm.eg[gb];
-    const float* g_ed = sm.ed[gb];
-
-    // ================= P0: convert this wave's raw rows; gates; prefetch ch+1
-    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's DMA of chunk ch landed
-    if (ch > 0) {
-      // output of chunk ch-1 (a full chunk: only the last chunk can be ragged).
-      // Row 32tt + 8g + 4h + r: a uniform row pointer plus a per-lane offset.
-      const uint32_t loff = uint32_t(vrow) + uint32_t(4 * h) * uint32_t(v_stride);
+  };
+  auto tile_coords = [](int tile, int& ti, int& tj) {
+    ti = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
+    tj = tile - (ti * (ti + 1)) / 2;
+  };
+  // A tile (ti, tj) = tril_strict(beta_i e^{gam_i - gam_j} K K^T) from the raw
+  // bf16 rows (bf16 MFMA: the inputs are exact).
+  auto tile_A = [&](int tile, const float* gd) {
+    int ti, tj;
+    tile_coords(tile, ti, tj);
+    const int ra = 16 * ti + c, rb = 16 * tj + c;
+    bf16x8_t fa[4], fb[4];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = 4 * g + r;
-            uint16_t* rowp = out + size_t(o_t0 + 32 * tt + 8 * g + r) * v_stride + size_t(hv) * D;
-            rowp[loff] = uint16_t(opack[tt][i >> 1] >> (16 * (i & 1)));
-          }
-        }
-      }
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = ld16_bf(&raw.k[raw_off(ra, 32 * ks + 8 * g)]);
+      fb[ks] = ld16_bf(&raw.k[raw_off(rb, 32 * ks + 8 * g)]);
     }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fa[ks], fb[ks], acc);
+    const int cc = 16 * tj + c;
+    const float gc = gd[cc];
+    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[16 * ti + 4 * g]);
+    const f32x4 br = *reinterpret_cast<const f32x4*>(&gd[C + 16 * ti + 4 * g]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 16 * ti + 4 * g + i;
+      const float dec = exp_fast(fminf(gr[i] - gc, 0.f));
+      sm.A[rr * ALD + cc] = rr > cc ? br[i] * dec * acc[i] : 0.f;
+    }
+  };
+  // P tile (ti, tj) = tril_incl(e^{gam_i - gam_j} Q K^T) from the fp16 copies.
+  auto tile_P = [&](int tile, const float* gd, int kb) {
+    int ti, tj;
+    tile_coords(tile, ti, tj);
+    f16x8 fa[4], fb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = ld16(&sm.Qc[(16 * ti + c) * KCLD + 32 * ks + 8 * g]);
+      fb[ks] = ld16(&sm.Kc[kb][(16 * tj + c) * KCLD + 32 * ks + 8 * g]);
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[ks], fb[ks], acc);
+    const int cc = 16 * tj + c;
+    const float gc = gd[cc];
+    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[16 * ti + 4 * g]);
+    const int pcc = p32(cc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 16 * ti + 4 * g + i;
+      const float dec = exp_fast(fminf(gr[i] - gc, 0.f));
+      sm.P[rr * TLD + pcc] = (_Float16)(rr >= cc ? dec * acc[i] : 0.f);
+    }
+  };
+  // Diagonal blocks 2w and 2w+1 of Tm (w = 0, 1) by forward substitution in
+  // fp32 -- lane groups 0-1 take block 2w, groups 2-3 block 2w+1 (the two
+  // groups of a block compute the same column and both write it) -- then the
+  // 16-row merge inside the 32-row block: T_{2w+1,2w} = -T_{2w+1} A T_{2w}.
+  auto diag_and_merge16 = [&](int w) {
     {
-      const int r0 = 16 * wave + 4 * g4;          // this lane's quad of rows
-      const int cc = c16 * 8;                     // and its 8 columns
-      const int pc_lo = (cc & ~15) + ((cc & 8) ? 4 : 0);
-      float kf[4][8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool valid = r0 + r < L;
-        uint4 kw = *reinterpret_cast<const uint4*>(&raw.k[(r0 + r) * D + cc]);
-        uint4 qw = *reinterpret_cast<const uint4*>(&raw.q[(r0 + r) * D + cc]);
-        if (!valid) { kw = make_uint4(0, 0, 0, 0); qw = make_uint4(0, 0, 0, 0); }
-        float qf[8];
-        unpack_bf16x2(kw.x, kf[r][0], kf[r][1]); unpack_bf16x2(kw.y, kf[r][2], kf[r][3]);
-        unpack_bf16x2(kw.z, kf[r][4], kf[r][5]); unpack_bf16x2(kw.w, kf[r][6], kf[r][7]);
-        unpack_bf16x2(qw.x, qf[0], qf[1]); unpack_bf16x2(qw.y, qf[2], qf[3]);
-        unpack_bf16x2(qw.z, qf[4], qf[5]); unpack_bf16x2(qw.w, qf[6], qf[7]);
-        const int row = r0 + r;
-        *reinterpret_cast<f16x4_t*>(&sm.K[row * KLD + pc_lo]) =
-            f16x4_t{(_Float16)kf[r][0], (_Float16)kf[r][1], (_Float16)kf[r][2], (_Float16)kf[r][3]};
-        *reinterpret_cast<f16x4_t*>(&sm.K[row * KLD + pc_lo + 8]) =
-            f16x4_t{(_Float16)kf[r][4], (_Float16)kf[r][5], (_Float16)kf[r][6], (_Float16)kf[r][7]};
-        *reinterpret_cast<f16x4_t*>(&sm.Q[row * KLD + pc_lo]) =
-            f16x4_t{(_Float16)qf[0], (_Float16)qf[1], (_Float16)qf[2], (_Float16)qf[3]};
-        *reinterpret_cast<f16x4_t*>(&sm.Q[row * KLD + pc_lo + 8]) =
-            f16x4_t{(_Float16)qf[4], (_Float16)qf[5], (_Float16)qf[6], (_Float16)qf[7]};
-      }
-      const int pt = perm16(r0);   // a quad of rows stays contiguous under the permutation
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<f16x4_t*>(&sm.KT[(cc + e) * TLD + pt]) =
-            f16x4_t{(_Float16)kf[0][e], (_Float16)kf[1][e], (_Float16)kf[2][e], (_Float16)kf[3][e]};
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): raw rows read, they may be refilled
-    if (ch + 1 < n_chunks) issue_kq(ch + 1);
-    lds_barrier();
-
-    // ================= P1: A (K K^T, fp32) and P (Q K^T, fp16) tiles, 5 per wave
-#pragma unroll
-    for (int r = 0; r < 5; ++r) {
-      const int task = wave + 4 * r;          // 0..9: K K^T tiles, 10..19: Q K^T tiles
-      const bool is_qk = task >= 10;
-      const int tile = is_qk ? task - 10 : task;
-      const int ti = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
-      const int tj = tile - (ti * (ti + 1)) / 2;
-      const _Float16* X = is_qk ? sm.Q : sm.K;
-      f16x8 fa[4], fb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        fa[ks] = ld16(&X[(16 * ti + c16) * KLD + 32 * ks + 8 * g4]);
-        fb[ks] = ld16(&sm.K[(16 * tj + c16) * KLD + 32 * ks + 8 * g4]);
-      }
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[ks], fb[ks], acc);
-      const int cc = 16 * tj + c16;
-      const float gc = g_gam[cc];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rr = 16 * ti + 4 * g4 + i;
-        const float dec = exp_fast(fminf(g_gam[rr] - gc, 0.f));
-        if (!is_qk) sm.A[rr * ALD + cc] = rr > cc ? g_beta[rr] * dec * acc[i] : 0.f;
-        else sm.P[rr * TLD + perm16(cc)] = (_Float16)(rr >= cc ? dec * acc[i] : 0.f);
-      }
-    }
-    lds_barrier();
-
-    // ================= P2: diagonal block `wave` of Tm  ||  K S^T, Q S^T, X
-    {
-      // forward substitution in fp32: column c of (I + A_bb)^-1, bb = wave
-      // (the four 16-lane groups compute the same column; all write it)
-      const int bb = wave, c = c16;
+      const int bb = 2 * w + (g >> 1);
       const float* Ab = &sm.A[(16 * bb) * ALD + 16 * bb];
+      // Opaque copy of the column index: keeps the 16 identity selects inside
+      // the chunk loop instead of being hoisted into registers.
+      int cid = c;
+      asm volatile("" : "+v"(cid));
       float x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float s = (i == c) ? 1.f : 0.f;
+        float s = (i == cid) ? 1.f : 0.f;
 #pragma unroll
         for (int j4 = 0; j4 < i; j4 += 4) {
           const f32x4 arow = *reinterpret_cast<const f32x4*>(&Ab[i * ALD + j4]);
@@ -370,173 +409,204 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         }
         x[i] = s;
       }
-      const int pc = perm16(16 * bb + c);
+      const int pc = p32(16 * bb + c);
 #pragma unroll
       for (int i = 0; i < 16; ++i) sm.Tm[(16 * bb + i) * TLD + pc] = (_Float16)x[i];
     }
-    f32x16 KS[2], QS[2];
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's diagonal writes done
+    const int a0 = 32 * w;
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sm.A[(a0 + 16 + c) * ALD + a0 + 4 * g]);
+    const f16x4_t fa = {(_Float16)a4[0], (_Float16)a4[1], (_Float16)a4[2], (_Float16)a4[3]};
+    f16x4_t fb;
+    const int pcb = p32(a0 + c);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) { KS[tt] = f32x16{}; QS[tt] = f32x16{}; }
-    {
-      const _Float16* krow0 = &sm.K[col * KLD + 8 * h];
-      const _Float16* qrow0 = &sm.Q[col * KLD + 8 * h];
+    for (int e = 0; e < 4; ++e) fb[e] = sm.Tm[(a0 + 4 * g + e) * TLD + pcb];
+    const f32x4 y = mfma16k16(fa, fb, f32x4{0.f, 0.f, 0.f, 0.f});
+    const f16x4_t ft = *reinterpret_cast<const f16x4_t*>(&sm.Tm[(a0 + 16 + c) * TLD + p32(a0 + 16 + 4 * g)]);
+    const f16x4_t fy = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+    const f32x4 t21 = mfma16k16(ft, fy, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g + i) * TLD + pcb] = (_Float16)(-t21[i]);
+  };
+  // 32-row merge of Tm: T_ba = -T_b (A_ba T_a) with 32x32x16 MFMAs
+  // (lane = column l % 32, half h = l / 32).
+  auto merge32 = [&]() {
+    const int col = lane & 31, h = lane >> 5;
+    f32x16 y = f32x16{};
+    const int pcol = p32(col);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const f16x8 sb = pack8(Sacc[j], s);
-          const int kc = 32 * j + 16 * s;
+    for (int s = 0; s < 2; ++s) {
+      f16x8 fb;
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            KS[tt] = mfma32(ld16(krow0 + 32 * tt * KLD + kc), sb, KS[tt]);
-            QS[tt] = mfma32(ld16(qrow0 + 32 * tt * KLD + kc), sb, QS[tt]);
-          }
-        }
-      }
+      for (int e = 0; e < 8; ++e) fb[e] = sm.Tm[(16 * s + 8 * h + e) * TLD + pcol];
+      y = mfma32(ld_f32x8_as_f16(&sm.A[(32 + col) * ALD + 16 * s + 8 * h]), fb, y);
     }
-    // X = beta (V - e^gam K S^T) in place of KS; e^gam Q S^T in place of QS
+    f32x16 tba = f32x16{};
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int t4 = 32 * tt + 8 * g + 4 * h;     // rows of elements 4g..4g+3
-        const f32x4 eg = *reinterpret_cast<const f32x4*>(&g_eg[t4]);
-        const f32x4 bt = *reinterpret_cast<const f32x4*>(&g_beta[t4]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 4 * g + r;
-          KS[tt][i] = bt[r] * (bf16_bits_to_f32(sV[(t4 + r) * D + vrow]) - eg[r] * KS[tt][i]);
-          QS[tt][i] *= eg[r];
-        }
-      }
+    for (int s = 0; s < 2; ++s) {
+      // k-slots of half h: rows 16 s + {4h..4h+3, 8+4h..8+4h+3} of Y
+      const _Float16* trow = &sm.Tm[(32 + col) * TLD + 32];
+      const f16x4_t lo = *reinterpret_cast<const f16x4_t*>(trow + p32(16 * s + 4 * h));
+      const f16x4_t hi = *reinterpret_cast<const f16x4_t*>(trow + p32(16 * s + 8 + 4 * h));
+      const f16x8 fa = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      tba = mfma32(fa, pack8(y, s), tba);
     }
-    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
+  };
 
-    // ================= P3: block merges of Tm (wave 0); gates of chunk ch+1 (wave 1);
-    // V of chunk ch+1 (every wave has read V of chunk ch)
-    if (ch + 1 < n_chunks) {
-      if (wave == 1) gates_chunk(ch + 1);   // its loads were issued before the K/Q DMA
-      issue_v(ch + 1);
-    }
-    if (wave == 0) {
+  // ---------------- initial state: Sacc[kb][i] = S[vrow][16 kb + 4 g + i]
+  f32x4 Sacc[8];
+  const size_t state_off = (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
-      for (int a0 = 0; a0 < 64; a0 += 32) {
-        // 16-merges inside the diagonal 32-blocks: T21 = -T22 (A21 T11)
-        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sm.A[(a0 + 16 + c16) * ALD + a0 + 4 * g4]);
-        const f16x4_t fa = {(_Float16)a4[0], (_Float16)a4[1], (_Float16)a4[2], (_Float16)a4[3]};
-        f16x4_t fb;
-        const int pcb = perm16(a0 + c16);
+  for (int kb = 0; kb < 8; ++kb) Sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (h0 != nullptr) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) fb[e] = sm.Tm[(a0 + 4 * g4 + e) * TLD + pcb];
-        const f32x4 y = mfma16k16(fa, fb, f32x4{0.f, 0.f, 0.f, 0.f});
-        const f16x4_t ft =
-            *reinterpret_cast<const f16x4_t*>(&sm.Tm[(a0 + 16 + c16) * TLD + perm16(a0 + 16 + 4 * g4)]);
-        const f16x4_t fy = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
-        const f32x4 t21 = mfma16k16(ft, fy, f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g4 + i) * TLD + pcb] = (_Float16)(-t21[i]);
-      }
-      // 32-merge: T_ba = -T_b (A_ba T_a), a = rows/cols 0..31, b = 32..63
-      f32x16 y = f32x16{};
-      const int pcol = perm16(col);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        f16x8 fb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) fb[e] = sm.Tm[(16 * s + 8 * h + e) * TLD + pcol];
-        y = mfma32(ld_f32x8_as_f16(&sm.A[(32 + col) * ALD + 16 * s + 8 * h]), fb, y);
-      }
-      f32x16 tba = f32x16{};
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        tba = mfma32(ld16(&sm.Tm[(32 + col) * TLD + 32 + 16 * s + 8 * h]), pack8(y, s), tba);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
-    }
-    lds_barrier();
-
-    // ================= P4: Vn = Tm X, O = scale (e^gam Q S^T + P Vn), state update
-    {
-      f16x8 Xb[2][2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) { Xb[tt][0] = pack8(KS[tt], 0); Xb[tt][1] = pack8(KS[tt], 1); }
-      f16x8 Vnb[2][2], Vdb[2][2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        f32x16 vn = f32x16{};
-        const _Float16* trow = &sm.Tm[(32 * tt + col) * TLD + 8 * h];
-#pragma unroll
-        for (int tp = 0; tp <= tt; ++tp) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) vn = mfma32(ld16(trow + 32 * tp + 16 * s), Xb[tp][s], vn);
-        }
-        Vnb[tt][0] = pack8(vn, 0);
-        Vnb[tt][1] = pack8(vn, 1);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 ed = *reinterpret_cast<const f32x4*>(&g_ed[32 * tt + 8 * g + 4 * h]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) vn[4 * g + r] *= ed[r];
-        }
-        Vdb[tt][0] = pack8(vn, 0);
-        Vdb[tt][1] = pack8(vn, 1);
-      }
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const _Float16* prow = &sm.P[(32 * tt + col) * TLD + 8 * h];
-#pragma unroll
-        for (int tp = 0; tp <= tt; ++tp) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) QS[tt] = mfma32(ld16(prow + 32 * tp + 16 * s), Vnb[tp][s], QS[tt]);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          opack[tt][i] = pack_bf16x2(scale * QS[tt][2 * i], scale * QS[tt][2 * i + 1]);
-      }
-      o_t0 = t0;
-      const float egL = g_eg[L - 1];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        Sacc[j] *= egL;
-        const _Float16* ktrow = &sm.KT[(32 * j + col) * TLD + 8 * h];
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) Sacc[j] = mfma32(ld16(ktrow + 32 * tp + 16 * s), Vdb[tp][s], Sacc[j]);
-        }
-      }
-    }
-    lds_barrier();
+    for (int kb = 0; kb < 8; ++kb) Sacc[kb] = *reinterpret_cast<const f32x4*>(h0 + state_off + 16 * kb + 4 * g);
   }
 
-  // ---- output of the last chunk (rows past its end are not written)
+  // ---------------- prologue: chunk 0 copied and prepared
   if (n_chunks > 0) {
-    const int L = len - (n_chunks - 1) * C;
-    const uint32_t loff = uint32_t(vrow) + uint32_t(4 * h) * uint32_t(v_stride);
+    copy_kq(0);
+    copy_v(0);
+    wait_vm<0>();
+    lds_barrier();
+    convert_kq(0, 0);
+    for (int tile = wave; tile < 10; tile += kWaves) tile_A(tile, gbuf[0]);
+    lds_barrier();
+    if (wave < 2) diag_and_merge16(wave);
+    else for (int tile = wave - 2; tile < 10; tile += kWaves - 2) tile_P(tile, gbuf[0], 0);
+    lds_barrier();
+    if (n_chunks > 1) copy_kq(1);
+  }
+
+  for (int ch = 0; ch < n_chunks; ++ch) {
+    const int t0 = bos + ch * C;
+    const int L = chunk_len(ch);
+    const int kb_buf = ch & 1;
+    const float* gd = gbuf[ch & 1];
+    const bool more = ch + 1 < n_chunks;
+
+    // ================= P1: K S^T, Q S^T, X (chain);  32-row merge of Tm_ch (wave 7)
+    f32x4 KS[4], QS[4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tb = 0; tb < 4; ++tb) { KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; }
+    {
+      const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
+      const _Float16* qbase = &sm.Qc[c * KCLD + 8 * g];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int p = 0; p < 4; ++p) {
+        const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 4 * g + r;
-          uint16_t* rowp = out + size_t(o_t0 + 32 * tt + 8 * g + r) * v_stride + size_t(hv) * D;
-          if (32 * tt + acc_row(i, h) < L) rowp[loff] = uint16_t(opack[tt][i >> 1] >> (16 * (i & 1)));
+        for (int tb = 0; tb < 4; ++tb) {
+          KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
+          QS[tb] = mfma16(ld16(qbase + 16 * tb * KCLD + 32 * p), sb, QS[tb]);
         }
       }
     }
+    if (wave == kWaves - 1) merge32();
+    // X = beta (V - e^gam K S^T) in place of KS; e^gam Q S^T in place of QS
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const int t4 = 16 * tb + 4 * g;
+      const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[2 * C + t4]);
+      const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[C + t4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        KS[tb][i] = bt[i] * (bf16_bits_to_f32(rawV[raw_off(t4 + i, vrow)]) - eg[i] * KS[tb][i]);
+        QS[tb][i] *= eg[i];
+      }
+    }
+    if (more) wait_vm<0>();     // K / Q rows and gates of chunk ch+1 (copied during P3 of ch-1)
+    lds_barrier();
+
+    // ================= P2: Tm X, O, Vd (chain);  A_{ch+1}, fp16 K/Q_{ch+1} (prep)
+    if (more) copy_v(ch + 1);   // every wave has read V of chunk ch
+    f16x8 Vdb[2];
+    float egL;
+    {
+      const f16x8 Xb[2] = {pack2(KS[0], KS[1]), pack2(KS[2], KS[3])};
+      f32x4 Vn[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        Vn[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const _Float16* trow = &sm.Tm[(16 * tb + c) * TLD + 8 * g];
+#pragma unroll
+        for (int p = 0; p <= (tb >> 1); ++p) Vn[tb] = mfma16(ld16(trow + 32 * p), Xb[p], Vn[tb]);
+      }
+      const f16x8 Vnb[2] = {pack2(Vn[0], Vn[1]), pack2(Vn[2], Vn[3])};
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const f32x4 ed = *reinterpret_cast<const f32x4*>(&gd[3 * C + 16 * tb + 4 * g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Vn[tb][i] *= ed[i];
+      }
+      Vdb[0] = pack2(Vn[0], Vn[1]);
+      Vdb[1] = pack2(Vn[2], Vn[3]);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
+#pragma unroll
+        for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sm.Ost[(16 * tb + 4 * g + i) * KCLD + vrow] = f32_to_bf16_bits(scale * QS[tb][i]);
+      }
+      egL = gd[2 * C + L - 1];
+    }
+    if (more) {
+      for (int tile = wave; tile < 10; tile += kWaves) tile_A(tile, gbuf[(ch + 1) & 1]);
+      convert_kq(ch + 1, kb_buf ^ 1);
+    }
+    lds_barrier();
+
+    // ================= P3: state update (chain);  diagonal blocks / 16-row merges and P tiles of
+    //                      chunk ch+1 (prep); stores of O_ch; copies of chunk ch+2
+    {
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        Sacc[kb] *= egL;
+        const int kq = p32(16 * kb + 4 * (c & 3));    // this lane's quad of columns
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int tr0 = 32 * p + 4 * g + (c >> 2);
+          const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
+          const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
+          const f16x8 fa = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          Sacc[kb] = mfma16(fa, Vdb[p], Sacc[kb]);
+        }
+      }
+    }
+    if (more) {
+      if (wave < 2) diag_and_merge16(wave);
+      else for (int tile = wave - 2; tile < 10; tile += kWaves - 2) tile_P(tile, gbuf[(ch + 1) & 1], kb_buf ^ 1);
+    }
+    {
+      // O_ch: 16-byte stores of rows t < L (2 per lane)
+      uint16_t* obase = out + size_t(t0) * v_stride + size_t(hv) * D;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int qi = tid + kThreads * r;
+        const int row = qi >> 4, c8 = (qi & 15) * 8;
+        const uint4 w = *reinterpret_cast<const uint4*>(&sm.Ost[row * KCLD + c8]);
+        if (L == C || row < L) *reinterpret_cast<uint4*>(obase + size_t(row) * v_stride + c8) = w;
+      }
+    }
+    if (ch + 2 < n_chunks) {
+      copy_kq(ch + 2);
+      // V of chunk ch+1 (copied at the start of P2) has landed once at most the
+      // 2 output stores and the 4 (+1) K/Q/gate copies issued after it remain.
+      if (wave == 0) wait_vm<7>(); else wait_vm<6>();
+    } else if (more) {
+      wait_vm<2>();
+    }
+    lds_barrier();
   }
 
   // ---- final state
   float* dst = ht + state_off;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      *reinterpret_cast<f32x4*>(dst + 32 * j + 8 * g + 4 * h) =
-          f32x4{Sacc[j][4 * g + 0], Sacc[j][4 * g + 1], Sacc[j][4 * g + 2], Sacc[j][4 * g + 3]};
-    }
-  }
+  for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
 }
 
 int check_prefill_args(const void* q, const void* k, const void* v, const void* A_log,
@@ -548,9 +618,18 @@ int check_prefill_args(const void* q, const void* k, const void* v, const void* 
   return GDN_OK;
 }
 
+// Gate data: GSZ floats per (chunk slot, v-head), floor(T / C) + N slots.
+size_t gate_workspace_bytes(int N, int T, int HV) {
+  return (size_t(T / C) + size_t(N)) * size_t(HV) * GSZ * sizeof(float);
+}
+
 }  // namespace
 
-extern "C" size_t gdn_prefill_workspace_bytes(int, int, int, int) { return 0; }
+extern "C" size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV) {
+  (void)HQ;
+  if (N <= 0 || T < 0 || HV <= 0) return 0;
+  return gate_workspace_bytes(N, T, HV);
+}
 
 extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                const float* state, const float* A_log, const uint16_t* a,
@@ -558,23 +637,31 @@ extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint1
                                int cu_is_int32, int N, int T, int HQ, int HV, float scale,
                                uint16_t* out, float* final_state, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
                                     N, T, HQ, HV);
   if (rc != GDN_OK) return rc;
   if (N == 0) return GDN_OK;
-  const dim3 grid(unsigned(N) * unsigned(HV));
-  const dim3 block(kThreads);
+  if (workspace == nullptr || workspace_bytes < gate_workspace_bytes(N, T, HV) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
+    return GDN_ERR_WORKSPACE;
+  float* gws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 ggrid{unsigned(HV), unsigned(N), 1u};
+  const dim3 grid{unsigned(N) * unsigned(HV), 1u, 1u};
+  const dim3 block(kThreads);
+  const dim3 gblock(kGateThreads);
   if (cu_is_int32) {
-    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state,
-                       A_log, a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), T, HQ, HV,
-                       scale, out, final_state);
+    const int32_t* cu = static_cast<const int32_t*>(cu_seqlens);
+    hipLaunchKernelGGL(gdn_prefill_gates_kernel<int32_t>, ggrid, gblock, 0, st, A_log, a, dt_bias,
+                       b, cu, T, HV, gws);
+    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state, cu,
+                       gws, T, HQ, HV, scale, out, final_state);
   } else {
-    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state,
-                       A_log, a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), T, HQ, HV,
-                       scale, out, final_state);
+    const int64_t* cu = static_cast<const int64_t*>(cu_seqlens);
+    hipLaunchKernelGGL(gdn_prefill_gates_kernel<int64_t>, ggrid, gblock, 0, st, A_log, a, dt_bias,
+                       b, cu, T, HV, gws);
+    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state, cu,
+                       gws, T, HQ, HV, scale, out, final_state);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : -int(err);
