@@ -30,6 +30,8 @@
 // row 16s + 8(e/4) + 4h + e%4 of the tile), with the A operand read from LDS
 // in the matching order: no cross-lane shuffles, only fp32->fp16 packs.
 
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "../../include/gdn_hip.h"
 
@@ -39,13 +41,23 @@ using namespace gdn;
 
 constexpr int D = kHeadDim;   // 128
 constexpr int C = 64;         // chunk
-constexpr int KCLD = D + 8;   // Kc / Qc / Ost row stride (halves): 272 B rows
-constexpr int TLD = C + 8;    // Tm / P row stride (halves): 144 B rows
-constexpr int ALD = C + 4;    // A row stride (floats): 272 B rows
-constexpr int GSZ = 4 * C;    // floats of gate data per chunk: gam, beta, e^gam, e^(gam_L - gam)
-constexpr int kWaves = 8;     // two per SIMD
+// Row strides, chosen so that the MFMA operand reads (16-byte reads down 16
+// rows, and the transposing 8-byte reads down 4 rows x 4 quads) are free of
+// LDS bank conflicts: rows of 288 B (Kc / Qc, A) and 160 B (Tm / P).
+constexpr int KCLD = D + 16;  // Kc / Qc row stride (halves): 288 B rows
+constexpr int OLD = D + 8;    // Ost row stride (halves): 272 B rows
+constexpr int TLD = C + 16;   // Tm / P row stride (halves): 160 B rows
+constexpr int ALD = C + 8;    // A row stride (floats): 288 B rows
+// Gate data per chunk, GSZ floats: gam log2(e) | beta | e^gam | scale e^gam | e^(gam_L - gam)
+// (gam = chunk-local cumsum of the log-decay, gam_L its value at the chunk's last token).
+constexpr int G_L2 = 0, G_BETA = C, G_EG = 2 * C, G_EGS = 3 * C, G_ED = 4 * C;
+constexpr int GSZ = 5 * C;
+constexpr int kChainWaves = 8;              // state-chain waves, 16 state rows each
+constexpr int kPrepWaves = 8;               // preparation / copy waves
+constexpr int kWaves = kChainWaves + kPrepWaves;
 constexpr int kThreads = kWaves * 64;
-constexpr int kRowsPerWave = D / kWaves;   // 16 state rows (v) per wave
+constexpr int kPrepThreads = kPrepWaves * 64;
+constexpr int kRowsPerWave = D / kChainWaves;   // 16 state rows (v) per chain wave
 constexpr int kGateThreads = 256;          // gate pre-pass: one wave per chunk
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
@@ -77,7 +89,7 @@ struct __align__(16) Smem {
   _Float16 Tm[C * TLD];        // (I + A)^-1 [t][p32(t')]
   _Float16 P[C * TLD];         // decayed causal Q K^T [t][p32(t')]
   float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32)
-  uint16_t Ost[C * KCLD];      // output chunk staging (bf16) [t][v]
+  uint16_t Ost[C * OLD];       // output chunk staging (bf16) [t][v]
 };
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
@@ -178,14 +190,13 @@ __device__ __forceinline__ int gate_slot0(int bos, int n) { return bos / C + n; 
 
 // Gates of every chunk (reference PRE:1706-1722 and the chunk-local cumsum of
 // PRE:1721): one block per (v-head, sequence), one wave per chunk, lane = token.
-// Writes, per chunk, gam (chunk-local cumsum of the log-decay), beta, e^gam and
-// e^(gam_last - gam) to gws[(chunk, hv)]; rows past the sequence end carry a
-// zero log-decay and beta = 0.
+// Writes the GSZ floats of gate data of each chunk to gws[(chunk slot, hv)];
+// rows past the sequence end carry a zero log-decay and beta = 0.
 template <typename CuT>
 __global__ __launch_bounds__(kGateThreads) void gdn_prefill_gates_kernel(
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
-    const CuT* __restrict__ cu_seqlens, int T, int HV, float* __restrict__ gws) {
+    const CuT* __restrict__ cu_seqlens, int T, int HV, float scale, float* __restrict__ gws) {
   const int hv = blockIdx.x;
   const int n = blockIdx.y;
   const int wave = threadIdx.x >> 6;
@@ -210,27 +221,41 @@ __global__ __launch_bounds__(kGateThreads) void gdn_prefill_gates_kernel(
       if (lane >= off) ld += y;
     }
     const float gl = __shfl(ld, L - 1, 64);
+    const float eg = expf(ld);
     float* g = gws + (size_t(slot0 + ch) * HV + hv) * GSZ;
-    g[lane] = ld;
-    g[C + lane] = bt;
-    g[2 * C + lane] = expf(ld);
-    g[3 * C + lane] = expf(gl - ld);
+    g[G_L2 + lane] = ld * 1.44269504088896341f;
+    g[G_BETA + lane] = bt;
+    g[G_EG + lane] = eg;
+    g[G_EGS + lane] = scale * eg;
+    g[G_ED + lane] = expf(gl - ld);
   }
 }
 
-// The state chain.  One workgroup (8 waves, two per SIMD) per (sequence,
-// v-head); wave w owns state rows v in [16w, 16w+16) and runs all of its
-// products as 16x16x32 MFMAs.  Software pipeline: in iteration i the waves run
-// the state-dependent work of chunk i and the state-independent preparation of
+// Lower 16x16 tiles of a 64x64 chunk matrix, row-major: tile -> (ti, tj).
+template <int TILE>
+struct Tile16 {
+  static constexpr int ti = TILE < 1 ? 0 : TILE < 3 ? 1 : TILE < 6 ? 2 : 3;
+  static constexpr int tj = TILE - (ti * (ti + 1)) / 2;
+};
+template <int N>
+using IC = std::integral_constant<int, N>;
+
+// The state chain.  One workgroup of 16 waves per (sequence, v-head): waves
+// 0-7 run the chain (wave w owns state rows v in [16w, 16w+16), all of its
+// products are 16x16x32 MFMAs), waves 8-15 prepare chunks, store outputs and
+// issue every copy into LDS; each SIMD hosts two waves of each kind.  In
+// iteration i the chain works on chunk i while the preparation waves build
 // chunk i+1, in three phases separated by LDS barriers:
-//   P1  chain i : K S^T, Q S^T, X            prep : 32-row merge of Tm_i (wave 7)
-//   P2  chain i : Tm X, O -> Ost, Vd          prep : A_{i+1} = K K^T tiles, K/Q_{i+1} -> fp16
-//   P3  chain i : S update (K^T by            prep : diagonal blocks and 16-row merges of
-//                 transposing LDS reads)            Tm_{i+1} (waves 0-1), P_{i+1} tiles
-//                                                   (waves 2-7), stores of O_i, copies
-//                                                   of chunk i+2
-// Copies into LDS (K, Q, V rows, gate data) are issued two phases or more
-// before their first use and waited for with explicit vmcnt counts.
+//   P1  chain : K S^T, Q S^T, X             prep : 32-row merge of Tm_i
+//   P2  chain : Tm X, O -> Ost, Vd           prep : copy of V_{i+1}; A_{i+1} = K K^T tiles;
+//                                                  K/Q_{i+1} -> fp16
+//   P3  chain : S update (K^T by             prep : diagonal blocks and 16-row merges of
+//               transposing LDS reads)             Tm_{i+1}; P_{i+1} tiles; stores of O_i;
+//                                                  copies of K/Q/gates of chunk i+2
+// Copies are issued two phases or more before their first use and waited for
+// with explicit vmcnt counts by the waves that issued them.  Which wave
+// computes which tile is fixed at compile time, so tile offsets are
+// immediates.
 template <typename CuT>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -245,13 +270,17 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   const int n = blockIdx.x / HV;
   const int hv = blockIdx.x - n * HV;
   const int hq = hv / (HV / HQ);
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int g = lane >> 4;        // lane group (16x16 MFMA layouts)
-  const int c = lane & 15;
-  const int v0 = kRowsPerWave * wave;
-  const int vrow = v0 + c;        // state row v owned by this lane
+  int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keep it scalar
+  int lane = tid & 63;
+  int g = lane >> 4;              // lane group (16x16 MFMA layouts)
+  int c = lane & 15;
+  const bool is_chain = wave < kChainWaves;
+  const int pw = wave - kChainWaves;          // preparation wave index (valid when !is_chain)
+  int ptid = tid - kChainWaves * 64;          // preparation thread index
+  const int v0 = kRowsPerWave * (wave & (kChainWaves - 1));
+  const int vrow = v0 + c;        // state row v owned by this lane (chain waves)
+  const float scale_l2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__log2f(scale))));
 
   int bos, len;
   seq_bounds(cu_seqlens, n, T, bos, len);
@@ -270,30 +299,34 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     sm.P[R * TLD + pc] = (_Float16)0.f;
   }
 
-  // ---------------- copies into LDS.  An instruction covers 4 rows: lane l
-  // carries row row0 + l/16, swizzle slot l%16 (rows past the chunk end are
-  // clamped to its last row).  Wave w copies K/Q rows [8w, 8w+8) and V rows
-  // [8w, 8w+8).
-  auto copy_kq = [&](int ch) {      // 4 instructions per wave (+1 gate row on wave 0)
+  // ---------------- copies into LDS (preparation waves).  An instruction
+  // covers 4 rows: lane l carries row row0 + l/16, swizzle slot l%16 (rows past
+  // the chunk end are clamped to its last row).  Preparation wave p copies
+  // K/Q/V rows [8p, 8p+8); preparation wave 0 also copies the gate data.
+  auto copy_kq = [&](int ch) {      // 4 instructions per wave (+2 on preparation wave 0)
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int row0 = 8 * wave + 4 * r;
+      const int row0 = 8 * pw + 4 * r;
       const int row = row0 + (lane >> 4);
       const int src_chunk = (lane & 15) ^ (row & 15);
       const size_t off = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_chunk;
       lds_dma16(k + off, &raw.k[row0 * D]);
       lds_dma16(q + off, &raw.q[row0 * D]);
     }
-    if (wave == 0) lds_dma16(gws + (size_t(slot0 + ch) * HV + hv) * GSZ + 4 * lane, &gbuf[ch & 1][0]);
+    if (pw == 0) {
+      const float* gsrc = gws + (size_t(slot0 + ch) * HV + hv) * GSZ;
+      lds_dma16(gsrc + 4 * lane, &gbuf[ch & 1][0]);
+      if (lane < (GSZ - 256) / 4) lds_dma16(gsrc + 256 + 4 * lane, &gbuf[ch & 1][256]);
+    }
   };
   auto copy_v = [&](int ch) {       // 2 instructions per wave
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int row0 = 8 * wave + 4 * r;
+      const int row0 = 8 * pw + 4 * r;
       const int row = row0 + (lane >> 4);
       const int src_chunk = (lane & 15) ^ (row & 15);
       lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + 8 * src_chunk,
@@ -308,14 +341,16 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const int L = chunk_len(ch);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int item = tid + kThreads * r;
+      const int item = ptid + kPrepThreads * r;
       const int row = item >> 4;
       const int cc = (item & 15) * 8;                 // logical columns cc..cc+7
       uint4 kw = *reinterpret_cast<const uint4*>(&raw.k[raw_off(row, cc)]);
       uint4 qw = *reinterpret_cast<const uint4*>(&raw.q[raw_off(row, cc)]);
-      const uint32_t m = row < L ? 0xffffffffu : 0u;
-      kw.x &= m; kw.y &= m; kw.z &= m; kw.w &= m;
-      qw.x &= m; qw.y &= m; qw.z &= m; qw.w &= m;
+      if (L < C) {
+        const uint32_t m = row < L ? 0xffffffffu : 0u;
+        kw.x &= m; kw.y &= m; kw.z &= m; kw.w &= m;
+        qw.x &= m; qw.y &= m; qw.z &= m; qw.w &= m;
+      }
       float kf[8], qf[8];
       unpack_bf16x2(kw.x, kf[0], kf[1]); unpack_bf16x2(kw.y, kf[2], kf[3]);
       unpack_bf16x2(kw.z, kf[4], kf[5]); unpack_bf16x2(kw.w, kf[6], kf[7]);
@@ -330,40 +365,44 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       *reinterpret_cast<f16x4_t*>(qd + pb) = f16x4_t{(_Float16)qf[4], (_Float16)qf[5], (_Float16)qf[6], (_Float16)qf[7]};
     }
   };
-  auto tile_coords = [](int tile, int& ti, int& tj) {
-    ti = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
-    tj = tile - (ti * (ti + 1)) / 2;
-  };
-  // A tile (ti, tj) = tril_strict(beta_i e^{gam_i - gam_j} K K^T) from the raw
-  // bf16 rows (bf16 MFMA: the inputs are exact).
-  auto tile_A = [&](int tile, const float* gd) {
-    int ti, tj;
-    tile_coords(tile, ti, tj);
-    const int ra = 16 * ti + c, rb = 16 * tj + c;
+  // Per-lane swizzled offsets of the 8-column pieces this lane reads from a
+  // raw row r with r % 16 == c: piece 4 ks + g sits in slot (4 ks + g) ^ c.
+  int raw_lane[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) raw_lane[ks] = c * D + 8 * ((4 * ks + g) ^ c);
+  // A tile = tril_strict(beta_i e^{gam_i - gam_j} K K^T) from the raw bf16
+  // rows (bf16 MFMA: the inputs are exact).  Diagonal tiles also store the
+  // transpose of their strict lower part in the (otherwise unused) upper part.
+  auto tile_A = [&](auto tile_c, const float* gd) {
+    constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
+    constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
     bf16x8_t fa[4], fb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      fa[ks] = ld16_bf(&raw.k[raw_off(ra, 32 * ks + 8 * g)]);
-      fb[ks] = ld16_bf(&raw.k[raw_off(rb, 32 * ks + 8 * g)]);
+      fa[ks] = ld16_bf(&raw.k[raw_lane[ks] + 16 * ti * D]);
+      fb[ks] = ld16_bf(&raw.k[raw_lane[ks] + 16 * tj * D]);
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fa[ks], fb[ks], acc);
-    const int cc = 16 * tj + c;
-    const float gc = gd[cc];
-    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[16 * ti + 4 * g]);
-    const f32x4 br = *reinterpret_cast<const f32x4*>(&gd[C + 16 * ti + 4 * g]);
+    const float gc = gd[G_L2 + 16 * tj + c];
+    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * ti + 4 * g]);
+    const f32x4 br = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * ti + 4 * g]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rr = 16 * ti + 4 * g + i;
-      const float dec = exp_fast(fminf(gr[i] - gc, 0.f));
-      sm.A[rr * ALD + cc] = rr > cc ? br[i] * dec * acc[i] : 0.f;
+      const float val = br[i] * __builtin_amdgcn_exp2f(gr[i] - gc) * acc[i];
+      if (ti != tj) {
+        sm.A[(16 * ti + 4 * g + i) * ALD + 16 * tj + c] = val;
+      } else if (4 * g + i > c) {
+        sm.A[(16 * ti + 4 * g + i) * ALD + 16 * tj + c] = val;
+        sm.A[(16 * ti + c) * ALD + 16 * tj + 4 * g + i] = val;
+      }
     }
   };
-  // P tile (ti, tj) = tril_incl(e^{gam_i - gam_j} Q K^T) from the fp16 copies.
-  auto tile_P = [&](int tile, const float* gd, int kb) {
-    int ti, tj;
-    tile_coords(tile, ti, tj);
+  // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the fp16 copies.
+  auto tile_P = [&](auto tile_c, const float* gd, int kb) {
+    constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
+    constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
     f16x8 fa[4], fb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -373,48 +412,58 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[ks], fb[ks], acc);
-    const int cc = 16 * tj + c;
-    const float gc = gd[cc];
-    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[16 * ti + 4 * g]);
-    const int pcc = p32(cc);
+    const float gc = gd[G_L2 + 16 * tj + c] - scale_l2;
+    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * ti + 4 * g]);
+    const int pcc = p32(16 * tj + c);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rr = 16 * ti + 4 * g + i;
-      const float dec = exp_fast(fminf(gr[i] - gc, 0.f));
-      sm.P[rr * TLD + pcc] = (_Float16)(rr >= cc ? dec * acc[i] : 0.f);
+      float val = __builtin_amdgcn_exp2f(gr[i] - gc) * acc[i];
+      if (ti == tj) val = (4 * g + i >= c) ? val : 0.f;
+      sm.P[(16 * ti + 4 * g + i) * TLD + pcc] = (_Float16)val;
     }
   };
-  // Diagonal blocks 2w and 2w+1 of Tm (w = 0, 1) by forward substitution in
-  // fp32 -- lane groups 0-1 take block 2w, groups 2-3 block 2w+1 (the two
-  // groups of a block compute the same column and both write it) -- then the
-  // 16-row merge inside the 32-row block: T_{2w+1,2w} = -T_{2w+1} A T_{2w}.
-  auto diag_and_merge16 = [&](int w) {
-    {
-      const int bb = 2 * w + (g >> 1);
-      const float* Ab = &sm.A[(16 * bb) * ALD + 16 * bb];
-      // Opaque copy of the column index: keeps the 16 identity selects inside
-      // the chunk loop instead of being hoisted into registers.
-      int cid = c;
-      asm volatile("" : "+v"(cid));
-      float x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s = (i == cid) ? 1.f : 0.f;
-#pragma unroll
-        for (int j4 = 0; j4 < i; j4 += 4) {
-          const f32x4 arow = *reinterpret_cast<const f32x4*>(&Ab[i * ALD + j4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (j4 + e < i) s = fmaf(-arow[e], x[j4 + e], s);
-        }
-        x[i] = s;
-      }
-      const int pc = p32(16 * bb + c);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sm.Tm[(16 * bb + i) * TLD + pc] = (_Float16)x[i];
+  // A tiles of a chunk: 10 tiles over the 8 preparation waves.
+  auto tiles_A = [&](const float* gd) {
+    switch (pw) {
+      case 0: tile_A(IC<0>{}, gd); tile_A(IC<8>{}, gd); break;
+      case 1: tile_A(IC<2>{}, gd); tile_A(IC<7>{}, gd); break;
+      case 2: tile_A(IC<5>{}, gd); break;
+      case 3: tile_A(IC<9>{}, gd); break;
+      case 4: tile_A(IC<1>{}, gd); break;
+      case 5: tile_A(IC<3>{}, gd); break;
+      case 6: tile_A(IC<4>{}, gd); break;
+      default: tile_A(IC<6>{}, gd); break;
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's diagonal writes done
-    const int a0 = 32 * w;
+  };
+  // Diagonal 16x16 blocks of Tm: lane group g inverts block g by forward
+  // substitution in fp32 (lane = column).
+  auto diag_all4 = [&]() {
+    const float* Ab = &sm.A[(16 * g) * ALD + 16 * g];
+    // Opaque copy of the column index: keeps the 16 identity selects inside
+    // the chunk loop instead of being hoisted into registers.
+    int cid = c;
+    asm volatile("" : "+v"(cid));
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      // bound the live A rows: loads of rows 4b.. are not hoisted above row 4b
+      if ((i & 3) == 0) asm volatile("" ::: "memory");
+      float sum = (i == cid) ? 1.f : 0.f;
+#pragma unroll
+      for (int j4 = 0; j4 < i; j4 += 4) {
+        const f32x4 arow = *reinterpret_cast<const f32x4*>(&Ab[i * ALD + j4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (j4 + e < i) sum = fmaf(-arow[e], x[j4 + e], sum);
+      }
+      x[i] = sum;
+    }
+    const int pc = p32(16 * g + c);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sm.Tm[(16 * g + i) * TLD + pc] = (_Float16)x[i];
+  };
+  // 16-row merge inside the 32-row block at a0: T_{a0+16.., a0..} = -T_22 A_21 T_11.
+  auto merge16 = [&](int a0) {
     const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sm.A[(a0 + 16 + c) * ALD + a0 + 4 * g]);
     const f16x4_t fa = {(_Float16)a4[0], (_Float16)a4[1], (_Float16)a4[2], (_Float16)a4[3]};
     f16x4_t fb;
@@ -427,6 +476,19 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const f32x4 t21 = mfma16k16(ft, fy, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
     for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g + i) * TLD + pcb] = (_Float16)(-t21[i]);
+  };
+  // Preparation wave 0 builds the diagonal blocks of Tm; the P tiles go to waves 1-6.
+  auto diag_or_tiles_P = [&](const float* gd, int kb) {
+    switch (pw) {
+      case 0: diag_all4(); break;
+      case 1: tile_P(IC<0>{}, gd, kb); tile_P(IC<8>{}, gd, kb); break;
+      case 2: tile_P(IC<2>{}, gd, kb); tile_P(IC<7>{}, gd, kb); break;
+      case 3: tile_P(IC<5>{}, gd, kb); tile_P(IC<6>{}, gd, kb); break;
+      case 4: tile_P(IC<9>{}, gd, kb); tile_P(IC<4>{}, gd, kb); break;
+      case 5: tile_P(IC<1>{}, gd, kb); break;
+      case 6: tile_P(IC<3>{}, gd, kb); break;
+      default: break;
+    }
   };
   // 32-row merge of Tm: T_ba = -T_b (A_ba T_a) with 32x32x16 MFMAs
   // (lane = column l % 32, half h = l / 32).
@@ -454,159 +516,183 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
   };
-
-  // ---------------- initial state: Sacc[kb][i] = S[vrow][16 kb + 4 g + i]
-  f32x4 Sacc[8];
-  const size_t state_off = (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
-#pragma unroll
-  for (int kb = 0; kb < 8; ++kb) Sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (h0 != nullptr) {
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb) Sacc[kb] = *reinterpret_cast<const f32x4*>(h0 + state_off + 16 * kb + 4 * g);
-  }
-
-  // ---------------- prologue: chunk 0 copied and prepared
-  if (n_chunks > 0) {
-    copy_kq(0);
-    copy_v(0);
-    wait_vm<0>();
-    lds_barrier();
-    convert_kq(0, 0);
-    for (int tile = wave; tile < 10; tile += kWaves) tile_A(tile, gbuf[0]);
-    lds_barrier();
-    if (wave < 2) diag_and_merge16(wave);
-    else for (int tile = wave - 2; tile < 10; tile += kWaves - 2) tile_P(tile, gbuf[0], 0);
-    lds_barrier();
-    if (n_chunks > 1) copy_kq(1);
-  }
-
-  for (int ch = 0; ch < n_chunks; ++ch) {
+  // O of a chunk: 16-byte stores of rows t < L (2 per preparation lane).
+  auto store_out = [&](int ch) {
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
-    const int kb_buf = ch & 1;
-    const float* gd = gbuf[ch & 1];
-    const bool more = ch + 1 < n_chunks;
+    uint16_t* obase = out + size_t(t0) * v_stride + size_t(hv) * D;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int qi = ptid + kPrepThreads * r;
+      const int row = qi >> 4, c8 = (qi & 15) * 8;
+      const uint4 w = *reinterpret_cast<const uint4*>(&sm.Ost[row * OLD + c8]);
+      if (L == C || row < L) *reinterpret_cast<uint4*>(obase + size_t(row) * v_stride + c8) = w;
+    }
+  };
 
-    // ================= P1: K S^T, Q S^T, X (chain);  32-row merge of Tm_ch (wave 7)
-    f32x4 KS[4], QS[4];
+  if (is_chain) {
+    // ================= chain waves
+    // initial state: Sacc[kb][i] = S[vrow][16 kb + 4 g + i]
+    f32x4 Sacc[8];
+    const size_t state_off = (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) { KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; }
-    {
-      const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
-      const _Float16* qbase = &sm.Qc[c * KCLD + 8 * g];
+    for (int kb = 0; kb < 8; ++kb) Sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (h0 != nullptr) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+      for (int kb = 0; kb < 8; ++kb) Sacc[kb] = *reinterpret_cast<const f32x4*>(h0 + state_off + 16 * kb + 4 * g);
+    }
+    if (n_chunks > 0) {           // prologue: the preparation waves build chunk 0
+      lds_barrier();
+      lds_barrier();
+      lds_barrier();
+      lds_barrier();
+    }
+    for (int ch = 0; ch < n_chunks; ++ch) {
+      const int L = chunk_len(ch);
+      const int kb_buf = ch & 1;
+      const float* gd = gbuf[ch & 1];
+
+      // ---- P1: K S^T, Q S^T, X
+      f32x4 KS[4], QS[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) { KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; }
+      {
+        const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
+        const _Float16* qbase = &sm.Qc[c * KCLD + 8 * g];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
+            QS[tb] = mfma16(ld16(qbase + 16 * tb * KCLD + 32 * p), sb, QS[tb]);
+          }
+        }
+      }
+      // X = beta (V - e^gam K S^T) in place of KS; scale e^gam Q S^T in place of QS
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int t4 = 16 * tb + 4 * g;
+        const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + t4]);
+        const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + t4]);
+        const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + t4]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          KS[tb][i] = bt[i] * (bf16_bits_to_f32(rawV[raw_off(t4 + i, vrow)]) - eg[i] * KS[tb][i]);
+          QS[tb][i] *= egs[i];
+        }
+      }
+      lds_barrier();
+
+      // ---- P2: Tm X, O -> Ost, Vd
+      f16x8 Vdb[2];
+      {
+        const f16x8 Xb[2] = {pack2(KS[0], KS[1]), pack2(KS[2], KS[3])};
+        f32x4 Vn[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-          KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
-          QS[tb] = mfma16(ld16(qbase + 16 * tb * KCLD + 32 * p), sb, QS[tb]);
+          Vn[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          const _Float16* trow = &sm.Tm[(16 * tb + c) * TLD + 8 * g];
+#pragma unroll
+          for (int p = 0; p <= (tb >> 1); ++p) Vn[tb] = mfma16(ld16(trow + 32 * p), Xb[p], Vn[tb]);
+        }
+        const f16x8 Vnb[2] = {pack2(Vn[0], Vn[1]), pack2(Vn[2], Vn[3])};
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const f32x4 ed = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb + 4 * g]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Vn[tb][i] *= ed[i];
+        }
+        Vdb[0] = pack2(Vn[0], Vn[1]);
+        Vdb[1] = pack2(Vn[2], Vn[3]);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
+#pragma unroll
+          for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            sm.Ost[(16 * tb + 4 * g + i) * OLD + vrow] = f32_to_bf16_bits(QS[tb][i]);
         }
       }
-    }
-    if (wave == kWaves - 1) merge32();
-    // X = beta (V - e^gam K S^T) in place of KS; e^gam Q S^T in place of QS
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const int t4 = 16 * tb + 4 * g;
-      const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[2 * C + t4]);
-      const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[C + t4]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        KS[tb][i] = bt[i] * (bf16_bits_to_f32(rawV[raw_off(t4 + i, vrow)]) - eg[i] * KS[tb][i]);
-        QS[tb][i] *= eg[i];
-      }
-    }
-    if (more) wait_vm<0>();     // K / Q rows and gates of chunk ch+1 (copied during P3 of ch-1)
-    lds_barrier();
+      const float egL = gd[G_EG + L - 1];
+      lds_barrier();
 
-    // ================= P2: Tm X, O, Vd (chain);  A_{ch+1}, fp16 K/Q_{ch+1} (prep)
-    if (more) copy_v(ch + 1);   // every wave has read V of chunk ch
-    f16x8 Vdb[2];
-    float egL;
-    {
-      const f16x8 Xb[2] = {pack2(KS[0], KS[1]), pack2(KS[2], KS[3])};
-      f32x4 Vn[4];
+      // ---- P3a / P3b: state update, S = e^{gam_L} S + K^T Vd, in two halves of k
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        Vn[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const _Float16* trow = &sm.Tm[(16 * tb + c) * TLD + 8 * g];
+      for (int half = 0; half < 2; ++half) {
 #pragma unroll
-        for (int p = 0; p <= (tb >> 1); ++p) Vn[tb] = mfma16(ld16(trow + 32 * p), Xb[p], Vn[tb]);
-      }
-      const f16x8 Vnb[2] = {pack2(Vn[0], Vn[1]), pack2(Vn[2], Vn[3])};
+        for (int kb = 4 * half; kb < 4 * half + 4; ++kb) {
+          Sacc[kb] *= egL;
+          const int kq = p32(16 * kb + 4 * (c & 3));    // this lane's quad of columns
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const f32x4 ed = *reinterpret_cast<const f32x4*>(&gd[3 * C + 16 * tb + 4 * g]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Vn[tb][i] *= ed[i];
-      }
-      Vdb[0] = pack2(Vn[0], Vn[1]);
-      Vdb[1] = pack2(Vn[2], Vn[3]);
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
-#pragma unroll
-        for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          sm.Ost[(16 * tb + 4 * g + i) * KCLD + vrow] = f32_to_bf16_bits(scale * QS[tb][i]);
-      }
-      egL = gd[2 * C + L - 1];
-    }
-    if (more) {
-      for (int tile = wave; tile < 10; tile += kWaves) tile_A(tile, gbuf[(ch + 1) & 1]);
-      convert_kq(ch + 1, kb_buf ^ 1);
-    }
-    lds_barrier();
-
-    // ================= P3: state update (chain);  diagonal blocks / 16-row merges and P tiles of
-    //                      chunk ch+1 (prep); stores of O_ch; copies of chunk ch+2
-    {
-#pragma unroll
-      for (int kb = 0; kb < 8; ++kb) {
-        Sacc[kb] *= egL;
-        const int kq = p32(16 * kb + 4 * (c & 3));    // this lane's quad of columns
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const int tr0 = 32 * p + 4 * g + (c >> 2);
-          const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
-          const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
-          const f16x8 fa = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          Sacc[kb] = mfma16(fa, Vdb[p], Sacc[kb]);
+          for (int p = 0; p < 2; ++p) {
+            const int tr0 = 32 * p + 4 * g + (c >> 2);
+            const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
+            const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
+            const f16x8 fa = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            Sacc[kb] = mfma16(fa, Vdb[p], Sacc[kb]);
+          }
         }
+        lds_barrier();
       }
     }
-    if (more) {
-      if (wave < 2) diag_and_merge16(wave);
-      else for (int tile = wave - 2; tile < 10; tile += kWaves - 2) tile_P(tile, gbuf[(ch + 1) & 1], kb_buf ^ 1);
-    }
-    {
-      // O_ch: 16-byte stores of rows t < L (2 per lane)
-      uint16_t* obase = out + size_t(t0) * v_stride + size_t(hv) * D;
+    float* dst = ht + state_off;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int qi = tid + kThreads * r;
-        const int row = qi >> 4, c8 = (qi & 15) * 8;
-        const uint4 w = *reinterpret_cast<const uint4*>(&sm.Ost[row * KCLD + c8]);
-        if (L == C || row < L) *reinterpret_cast<uint4*>(obase + size_t(row) * v_stride + c8) = w;
+    for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
+  } else {
+    // ================= preparation waves
+    if (n_chunks > 0) {           // prologue: chunk 0 copied and prepared
+      copy_kq(0);
+      copy_v(0);
+      wait_vm<0>();
+      lds_barrier();
+      convert_kq(0, 0);
+      tiles_A(gbuf[0]);
+      lds_barrier();
+      diag_or_tiles_P(gbuf[0], 0);
+      lds_barrier();
+      if (pw < 2) merge16(32 * pw);
+      lds_barrier();
+      if (n_chunks > 1) copy_kq(1);
+    }
+    for (int ch = 0; ch < n_chunks; ++ch) {
+      asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g), "+v"(c), "+v"(ptid));
+      const int kb_buf = ch & 1;
+      const bool more = ch + 1 < n_chunks;
+      // ---- P1: 32-row merge of Tm_ch; stores of O_{ch-1}; K/Q rows and gates of
+      //      chunk ch+1 landed (copied in P3a of ch-1; only the 2 stores may remain)
+      if (pw == kPrepWaves - 1) merge32();
+      if (ch > 0) {
+        store_out(ch - 1);
+        if (more) wait_vm<2>();
+      } else if (more) {
+        wait_vm<0>();
       }
+      lds_barrier();
+      // ---- P2: V copy, A tiles and fp16 K/Q of chunk ch+1
+      if (more) {
+        copy_v(ch + 1);           // every chain wave has read V of chunk ch
+        tiles_A(gbuf[(ch + 1) & 1]);
+        convert_kq(ch + 1, kb_buf ^ 1);
+      }
+      lds_barrier();
+      // ---- P3a: Tm diagonal blocks and P tiles of chunk ch+1; copies of chunk ch+2
+      if (more) diag_or_tiles_P(gbuf[(ch + 1) & 1], kb_buf ^ 1);
+      if (ch + 2 < n_chunks) copy_kq(ch + 2);
+      lds_barrier();
+      // ---- P3b: 16-row merges of Tm_{ch+1}; V of chunk ch+1 landed (only the 4
+      //      (+2) K/Q/gate copies of chunk ch+2 may remain)
+      if (more && pw < 2) merge16(32 * pw);
+      if (ch + 2 < n_chunks) {
+        if (pw == 0) wait_vm<6>(); else wait_vm<4>();
+      } else if (more) {
+        wait_vm<0>();
+      }
+      lds_barrier();
     }
-    if (ch + 2 < n_chunks) {
-      copy_kq(ch + 2);
-      // V of chunk ch+1 (copied at the start of P2) has landed once at most the
-      // 2 output stores and the 4 (+1) K/Q/gate copies issued after it remain.
-      if (wave == 0) wait_vm<7>(); else wait_vm<6>();
-    } else if (more) {
-      wait_vm<2>();
-    }
-    lds_barrier();
+    if (n_chunks > 0) store_out(n_chunks - 1);
   }
-
-  // ---- final state
-  float* dst = ht + state_off;
-#pragma unroll
-  for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
 }
 
 int check_prefill_args(const void* q, const void* k, const void* v, const void* A_log,
@@ -653,13 +739,13 @@ extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint1
   if (cu_is_int32) {
     const int32_t* cu = static_cast<const int32_t*>(cu_seqlens);
     hipLaunchKernelGGL(gdn_prefill_gates_kernel<int32_t>, ggrid, gblock, 0, st, A_log, a, dt_bias,
-                       b, cu, T, HV, gws);
+                       b, cu, T, HV, scale, gws);
     hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state, cu,
                        gws, T, HQ, HV, scale, out, final_state);
   } else {
     const int64_t* cu = static_cast<const int64_t*>(cu_seqlens);
     hipLaunchKernelGGL(gdn_prefill_gates_kernel<int64_t>, ggrid, gblock, 0, st, A_log, a, dt_bias,
-                       b, cu, T, HV, gws);
+                       b, cu, T, HV, scale, gws);
     hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state, cu,
                        gws, T, HQ, HV, scale, out, final_state);
   }
