@@ -74,6 +74,11 @@ def _traffic(name: str):
     return None
 
 
+# Untimed prefill launches before the timed ones (~15 ms of work): lets the GPU
+# reach its steady clocks, which the first few launches of a run do not show.
+PREFILL_WARMUP = 30
+
+
 def timed_launches(launch, n_steps: int, warmup: int):
     """Run ``launch(i)`` warmup + n_steps times; return (total_ms, mean_launch_ms).
 
@@ -184,7 +189,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--prefill-steps", type=int, default=30)
     ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -223,7 +228,7 @@ def main():
 
     if args.only in ("all", "prefill"):
         try:
-            r = bench_prefill(dev, args.prefill_steps, max(2, args.warmup // 5))
+            r = bench_prefill(dev, args.prefill_steps, PREFILL_WARMUP)
             ms = r["total_ms"] / args.prefill_steps
             tfl = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
             line["prefill"] = {

@@ -1,34 +1,36 @@
-// GDN chunked varlen prefill, one fused kernel (gfx950 / CDNA4, wave64, MFMA).
+// GDN chunked varlen prefill (gfx950 / CDNA4, wave64, MFMA).
 //
 // Replaces the reference prefill pipeline (five Triton launches plus host
 // metadata; gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py
-// :1570-1633, 1728-1759, 1762-1802).  One workgroup owns one
-// (sequence, v-head) chain and walks its 64-token chunks in order; the fp32
-// state S [V=128, K=128] never leaves registers between chunks, and nothing
-// but q/k/v/a/b is read and o / final state written.
+// :1570-1633, 1728-1759, 1762-1802) by two launches: a gate pre-pass that
+// writes the per-chunk gate data, and one chain kernel in which a workgroup
+// owns one (sequence, v-head) chain and walks its 64-token chunks in order.
+// The fp32 state S [V=128, K=128] never leaves registers between chunks, and
+// nothing but q/k/v/a/b and the gate data is read and o / final state written.
 //
 // Per chunk (C = 64 rows, gam = chunk-local cumsum of the log-decay,
 // S = state at chunk start), the same mathematics as the reference
 // (kernel.py:509-525, 661-796, 1153-1339, 1447-1496) arranged so that W and U
 // are never formed:
-//   A   = tril_strict(beta_i e^{gam_i-gam_j} K K^T)      (MFMA 16x16x32)
-//   P   = tril_incl(e^{gam_i-gam_j} Q K^T)                (MFMA 16x16x32)
-//   Tm  = (I + A)^-1      (fp32 16x16 diagonal blocks, MFMA block merges)
-//   X   = diag(beta) (V - diag(e^gam) K S^T)               (MFMA 32x32x16)
-//   Vn  = Tm X          ( = U - W S^T of the reference )   (MFMA 32x32x16)
-//   O   = scale (diag(e^gam) Q S^T + P Vn)                 (MFMA 32x32x16)
-//   S  <- e^{gam_L} S + (diag(e^{gam_L-gam}) Vn)^T K       (MFMA 32x32x16)
-// MFMA operands are fp16 (bf16 inputs convert exactly in fp16's normal
-// range; fp16 keeps 3 more mantissa bits than bf16 for the fp32 state and
-// intermediates), accumulation is fp32.
+//   A   = tril_strict(beta_i e^{gam_i-gam_j} K K^T)      (bf16 MFMA, exact products)
+//   P   = scale tril_incl(e^{gam_i-gam_j} Q K^T)          (bf16 MFMA, exact products)
+//   Tm  = (I + A)^-1      (fp32 16x16 diagonal blocks by substitution, MFMA block merges)
+//   X   = diag(beta) (V - diag(e^gam) K S^T)
+//   Vn  = Tm X          ( = U - W S^T of the reference )
+//   O   = scale diag(e^gam) Q S^T + P Vn
+//   S  <- e^{gam_L} S + (diag(e^{gam_L-gam}) Vn)^T K
+// The products with S, X and Vn run on fp16 operands (bf16 inputs convert
+// exactly in fp16's normal range; fp16 keeps 3 more mantissa bits than bf16
+// for the state and intermediates) with fp32 accumulation.
 //
-// Wave w of the 4 waves owns state rows v in [32w, 32w+32): every product
-// that touches S, X, Vn or O is split along v, so the waves never exchange
-// state.  The state lives as S^T accumulator tiles; because an MFMA reduces
-// over an arbitrary pairing of its 16 k-slots, each accumulator tile is used
-// directly as the B operand of the next product (k-slot e of lane half h is
-// row 16s + 8(e/4) + 4h + e%4 of the tile), with the A operand read from LDS
-// in the matching order: no cross-lane shuffles, only fp32->fp16 packs.
+// Chain wave w (of 8) owns state rows v in [16w, 16w+16): every product that
+// touches S, X, Vn or O is split along v, so the waves never exchange state.
+// The state lives as S^T accumulator tiles of 16x16x32 MFMAs; because an MFMA
+// reduces over an arbitrary pairing of its k-slots, two stacked accumulator
+// tiles are used directly as the B operand of the next product (k-slot e of
+// lane group q is row 16(e/4) + 4q + e%4), with the A operand read from LDS in
+// the matching order (the p32 column order below): no cross-lane shuffles,
+// only fp32->fp16 packs.
 
 #include <type_traits>
 
@@ -245,17 +247,18 @@ using IC = std::integral_constant<int, N>;
 // products are 16x16x32 MFMAs), waves 8-15 prepare chunks, store outputs and
 // issue every copy into LDS; each SIMD hosts two waves of each kind.  In
 // iteration i the chain works on chunk i while the preparation waves build
-// chunk i+1, in three phases separated by LDS barriers:
-//   P1  chain : K S^T, Q S^T, X             prep : 32-row merge of Tm_i
-//   P2  chain : Tm X, O -> Ost, Vd           prep : copy of V_{i+1}; A_{i+1} = K K^T tiles;
-//                                                  K/Q_{i+1} -> fp16
-//   P3  chain : S update (K^T by             prep : diagonal blocks and 16-row merges of
-//               transposing LDS reads)             Tm_{i+1}; P_{i+1} tiles; stores of O_i;
-//                                                  copies of K/Q/gates of chunk i+2
-// Copies are issued two phases or more before their first use and waited for
-// with explicit vmcnt counts by the waves that issued them.  Which wave
-// computes which tile is fixed at compile time, so tile offsets are
-// immediates.
+// chunk i+1, in four phases separated by LDS barriers:
+//   P1   chain : K S^T, X                   prep : 32-row merge of Tm_i; stores of O_{i-1}
+//   P2   chain : scale e^gam Q S^T, Tm X,   prep : copy of V_{i+1}; A_{i+1} tiles;
+//                P Vn, O -> Ost, Vd                fp16 K_{i+1}
+//   P3a  chain : S update, first half of k  prep : diagonal blocks of Tm_{i+1} (wave 8);
+//                                                  P_{i+1} tiles; fp16 Q_{i+1}
+//   P3b  chain : S update, second half      prep : 16-row merges of Tm_{i+1}; copies of
+//                                                  K/Q/gates of chunk i+2
+// The S update reads K^T through transposing LDS reads.  Copies are issued one
+// phase or more before their first use and waited for with explicit vmcnt
+// counts by the waves that issued them.  Which wave computes which tile is
+// fixed at compile time, so tile offsets are immediates.
 template <typename CuT>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -335,35 +338,30 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   };
 
   // ---------------- preparation steps (state-independent)
-  // K/Q rows (raw bf16) -> Kc[kb] / Qc in fp16, rows past the end -> 0.  Two
-  // 8-column pieces per lane.
-  auto convert_kq = [&](int ch, int kb) {
-    const int L = chunk_len(ch);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int item = ptid + kPrepThreads * r;
+  // Raw bf16 rows -> fp16 operand rows [t][p32(k)], rows t >= L -> 0; items
+  // (row, 8-column piece) first, first + step, ... below 1024.
+  auto convert_rows = [&](const uint16_t* src, _Float16* dst, int L, int first, int step) {
+    for (int item = first; item < C * (D / 8); item += step) {
       const int row = item >> 4;
       const int cc = (item & 15) * 8;                 // logical columns cc..cc+7
-      uint4 kw = *reinterpret_cast<const uint4*>(&raw.k[raw_off(row, cc)]);
-      uint4 qw = *reinterpret_cast<const uint4*>(&raw.q[raw_off(row, cc)]);
+      uint4 w = *reinterpret_cast<const uint4*>(&src[raw_off(row, cc)]);
       if (L < C) {
         const uint32_t m = row < L ? 0xffffffffu : 0u;
-        kw.x &= m; kw.y &= m; kw.z &= m; kw.w &= m;
-        qw.x &= m; qw.y &= m; qw.z &= m; qw.w &= m;
+        w.x &= m; w.y &= m; w.z &= m; w.w &= m;
       }
-      float kf[8], qf[8];
-      unpack_bf16x2(kw.x, kf[0], kf[1]); unpack_bf16x2(kw.y, kf[2], kf[3]);
-      unpack_bf16x2(kw.z, kf[4], kf[5]); unpack_bf16x2(kw.w, kf[6], kf[7]);
-      unpack_bf16x2(qw.x, qf[0], qf[1]); unpack_bf16x2(qw.y, qf[2], qf[3]);
-      unpack_bf16x2(qw.z, qf[4], qf[5]); unpack_bf16x2(qw.w, qf[6], qf[7]);
-      _Float16* kd = &sm.Kc[kb][row * KCLD];
-      _Float16* qd = &sm.Qc[row * KCLD];
-      const int pa = p32(cc), pb = p32(cc + 4);
-      *reinterpret_cast<f16x4_t*>(kd + pa) = f16x4_t{(_Float16)kf[0], (_Float16)kf[1], (_Float16)kf[2], (_Float16)kf[3]};
-      *reinterpret_cast<f16x4_t*>(kd + pb) = f16x4_t{(_Float16)kf[4], (_Float16)kf[5], (_Float16)kf[6], (_Float16)kf[7]};
-      *reinterpret_cast<f16x4_t*>(qd + pa) = f16x4_t{(_Float16)qf[0], (_Float16)qf[1], (_Float16)qf[2], (_Float16)qf[3]};
-      *reinterpret_cast<f16x4_t*>(qd + pb) = f16x4_t{(_Float16)qf[4], (_Float16)qf[5], (_Float16)qf[6], (_Float16)qf[7]};
+      float f[8];
+      unpack_bf16x2(w.x, f[0], f[1]); unpack_bf16x2(w.y, f[2], f[3]);
+      unpack_bf16x2(w.z, f[4], f[5]); unpack_bf16x2(w.w, f[6], f[7]);
+      _Float16* d = &dst[row * KCLD];
+      *reinterpret_cast<f16x4_t*>(d + p32(cc)) = f16x4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+      *reinterpret_cast<f16x4_t*>(d + p32(cc + 4)) = f16x4_t{(_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
     }
+  };
+  // K rows of chunk ch -> Kc[kb] (all preparation waves).
+  auto convert_k = [&](int ch, int kb) { convert_rows(raw.k, sm.Kc[kb], chunk_len(ch), ptid, kPrepThreads); };
+  // Q rows of chunk ch -> Qc (preparation waves 1-7).
+  auto convert_q = [&](int ch) {
+    convert_rows(raw.q, sm.Qc, chunk_len(ch), ptid - 64, kPrepThreads - 64);
   };
   // Per-lane swizzled offsets of the 8-column pieces this lane reads from a
   // raw row r with r % 16 == c: piece 4 ks + g sits in slot (4 ks + g) ^ c.
@@ -399,19 +397,21 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
     }
   };
-  // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the fp16 copies.
-  auto tile_P = [&](auto tile_c, const float* gd, int kb) {
+  // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the raw bf16 rows
+  // (bf16 MFMA: the inputs are exact).  Rows past the chunk end hold copies of
+  // its last row; they only reach output rows that are never stored.
+  auto tile_P = [&](auto tile_c, const float* gd) {
     constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
     constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
-    f16x8 fa[4], fb[4];
+    bf16x8_t fa[4], fb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      fa[ks] = ld16(&sm.Qc[(16 * ti + c) * KCLD + 32 * ks + 8 * g]);
-      fb[ks] = ld16(&sm.Kc[kb][(16 * tj + c) * KCLD + 32 * ks + 8 * g]);
+      fa[ks] = ld16_bf(&raw.q[raw_lane[ks] + 16 * ti * D]);
+      fb[ks] = ld16_bf(&raw.k[raw_lane[ks] + 16 * tj * D]);
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[ks], fb[ks], acc);
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fa[ks], fb[ks], acc);
     const float gc = gd[G_L2 + 16 * tj + c] - scale_l2;
     const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * ti + 4 * g]);
     const int pcc = p32(16 * tj + c);
@@ -478,15 +478,15 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g + i) * TLD + pcb] = (_Float16)(-t21[i]);
   };
   // Preparation wave 0 builds the diagonal blocks of Tm; the P tiles go to waves 1-6.
-  auto diag_or_tiles_P = [&](const float* gd, int kb) {
+  auto diag_or_tiles_P = [&](const float* gd) {
     switch (pw) {
       case 0: diag_all4(); break;
-      case 1: tile_P(IC<0>{}, gd, kb); tile_P(IC<8>{}, gd, kb); break;
-      case 2: tile_P(IC<2>{}, gd, kb); tile_P(IC<7>{}, gd, kb); break;
-      case 3: tile_P(IC<5>{}, gd, kb); tile_P(IC<6>{}, gd, kb); break;
-      case 4: tile_P(IC<9>{}, gd, kb); tile_P(IC<4>{}, gd, kb); break;
-      case 5: tile_P(IC<1>{}, gd, kb); break;
-      case 6: tile_P(IC<3>{}, gd, kb); break;
+      case 1: tile_P(IC<0>{}, gd); tile_P(IC<8>{}, gd); break;
+      case 2: tile_P(IC<2>{}, gd); tile_P(IC<7>{}, gd); break;
+      case 3: tile_P(IC<5>{}, gd); tile_P(IC<6>{}, gd); break;
+      case 4: tile_P(IC<9>{}, gd); tile_P(IC<4>{}, gd); break;
+      case 5: tile_P(IC<1>{}, gd); break;
+      case 6: tile_P(IC<3>{}, gd); break;
       default: break;
     }
   };
@@ -553,40 +553,49 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       const float* gd = gbuf[ch & 1];
 
       // ---- P1: K S^T, Q S^T, X
-      f32x4 KS[4], QS[4];
+      f32x4 KS[4];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) { KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f}; }
+      for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
       {
         const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
+        }
+      }
+      // X = beta (V - e^gam K S^T) in place of KS
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int t4 = 16 * tb + 4 * g;
+        const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + t4]);
+        const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + t4]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          KS[tb][i] = bt[i] * (bf16_bits_to_f32(rawV[raw_off(t4 + i, vrow)]) - eg[i] * KS[tb][i]);
+      }
+      lds_barrier();
+
+      // ---- P2: scale e^gam Q S^T, Tm X, O -> Ost, Vd
+      f16x8 Vdb[2];
+      {
+        f32x4 QS[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
         const _Float16* qbase = &sm.Qc[c * KCLD + 8 * g];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) {
-            KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
-            QS[tb] = mfma16(ld16(qbase + 16 * tb * KCLD + 32 * p), sb, QS[tb]);
-          }
+          for (int tb = 0; tb < 4; ++tb) QS[tb] = mfma16(ld16(qbase + 16 * tb * KCLD + 32 * p), sb, QS[tb]);
         }
-      }
-      // X = beta (V - e^gam K S^T) in place of KS; scale e^gam Q S^T in place of QS
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const int t4 = 16 * tb + 4 * g;
-        const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + t4]);
-        const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + t4]);
-        const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + t4]);
+        for (int tb = 0; tb < 4; ++tb) {
+          const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          KS[tb][i] = bt[i] * (bf16_bits_to_f32(rawV[raw_off(t4 + i, vrow)]) - eg[i] * KS[tb][i]);
-          QS[tb][i] *= egs[i];
+          for (int i = 0; i < 4; ++i) QS[tb][i] *= egs[i];
         }
-      }
-      lds_barrier();
-
-      // ---- P2: Tm X, O -> Ost, Vd
-      f16x8 Vdb[2];
-      {
         const f16x8 Xb[2] = {pack2(KS[0], KS[1]), pack2(KS[2], KS[3])};
         f32x4 Vn[4];
 #pragma unroll
@@ -647,10 +656,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       copy_v(0);
       wait_vm<0>();
       lds_barrier();
-      convert_kq(0, 0);
+      convert_k(0, 0);
       tiles_A(gbuf[0]);
       lds_barrier();
-      diag_or_tiles_P(gbuf[0], 0);
+      diag_or_tiles_P(gbuf[0]);
+      if (pw > 0) convert_q(0);
       lds_barrier();
       if (pw < 2) merge16(32 * pw);
       lds_barrier();
@@ -670,20 +680,24 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         wait_vm<0>();
       }
       lds_barrier();
-      // ---- P2: V copy, A tiles and fp16 K/Q of chunk ch+1
+      // ---- P2: V copy, A tiles and fp16 K of chunk ch+1
       if (more) {
         copy_v(ch + 1);           // every chain wave has read V of chunk ch
         tiles_A(gbuf[(ch + 1) & 1]);
-        convert_kq(ch + 1, kb_buf ^ 1);
+        convert_k(ch + 1, kb_buf ^ 1);
       }
       lds_barrier();
-      // ---- P3a: Tm diagonal blocks and P tiles of chunk ch+1; copies of chunk ch+2
-      if (more) diag_or_tiles_P(gbuf[(ch + 1) & 1], kb_buf ^ 1);
-      if (ch + 2 < n_chunks) copy_kq(ch + 2);
+      // ---- P3a: Tm diagonal blocks, P tiles and fp16 Q of chunk ch+1 (Q S^T of
+      //      chunk ch was taken in P2)
+      if (more) {
+        diag_or_tiles_P(gbuf[(ch + 1) & 1]);
+        if (pw > 0) convert_q(ch + 1);
+      }
       lds_barrier();
-      // ---- P3b: 16-row merges of Tm_{ch+1}; V of chunk ch+1 landed (only the 4
-      //      (+2) K/Q/gate copies of chunk ch+2 may remain)
+      // ---- P3b: 16-row merges of Tm_{ch+1}; copies of chunk ch+2 (the raw rows of
+      //      ch+1 are read); V of chunk ch+1 landed (only those 4 (+2) copies remain)
       if (more && pw < 2) merge16(32 * pw);
+      if (ch + 2 < n_chunks) copy_kq(ch + 2);
       if (ch + 2 < n_chunks) {
         if (pw == 0) wait_vm<6>(); else wait_vm<4>();
       } else if (more) {
