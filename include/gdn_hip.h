@@ -92,7 +92,9 @@ size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV);
  *                 cu_seqlens[N] == T, non-decreasing (empty sequences allowed).
  *   scale       : the caller resolves None/0 to 1/sqrt(D) (kernel.py:1777-1778).
  *   workspace   : device buffer of at least gdn_prefill_workspace_bytes(...)
- *                 bytes (may be NULL when that is 0).
+ *                 bytes (that is 0 in this implementation: NULL is accepted).
+ * Sequences whose cu_seqlens ranges overlap or run backwards are read in
+ * bounds, but their results are unspecified.
  */
 int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     const float* state, const float* A_log, const uint16_t* a,

@@ -52,6 +52,25 @@ __device__ __forceinline__ float dpp_f32(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
 }
 
+// DPP move with a row mask: rows outside row_mask receive 0.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_f32_rows(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, kRowMask, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (lanes shifted in from
+// outside a row read 0): a scan within each 16-lane row by row_shr, then the
+// row totals carried forward by row_bcast:15 / row_bcast:31.
+__device__ __forceinline__ float wave_inclusive_scan(float x) {
+  x += dpp_f32<0x111>(x);             // row_shr:1
+  x += dpp_f32<0x112>(x);             // row_shr:2
+  x += dpp_f32<0x114>(x);             // row_shr:4
+  x += dpp_f32<0x118>(x);             // row_shr:8
+  x += dpp_f32_rows<0x142, 0xa>(x);   // row_bcast:15 into rows 1 and 3
+  x += dpp_f32_rows<0x143, 0xc>(x);   // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
 // Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
 __device__ __forceinline__ float row16_sum(float x) {
   x += dpp_f32<0x128>(x);   // row_ror:8

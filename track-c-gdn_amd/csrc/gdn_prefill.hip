@@ -2,11 +2,10 @@
 //
 // Replaces the reference prefill pipeline (five Triton launches plus host
 // metadata; gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py
-// :1570-1633, 1728-1759, 1762-1802) by two launches: a gate pre-pass that
-// writes the per-chunk gate data, and one chain kernel in which a workgroup
-// owns one (sequence, v-head) chain and walks its 64-token chunks in order.
-// The fp32 state S [V=128, K=128] never leaves registers between chunks, and
-// nothing but q/k/v/a/b and the gate data is read and o / final state written.
+// :1570-1633, 1728-1759, 1762-1802) by one launch: a workgroup owns one
+// (sequence, v-head) chain and walks its 64-token chunks in order, gates
+// included.  The fp32 state S [V=128, K=128] never leaves registers between
+// chunks, and nothing but q/k/v/a/b is read and o / final state written.
 //
 // Per chunk (C = 64 rows, gam = chunk-local cumsum of the log-decay,
 // S = state at chunk start), the same mathematics as the reference
@@ -60,7 +59,6 @@ constexpr int kWaves = kChainWaves + kPrepWaves;
 constexpr int kThreads = kWaves * 64;
 constexpr int kPrepThreads = kPrepWaves * 64;
 constexpr int kRowsPerWave = D / kChainWaves;   // 16 state rows (v) per chain wave
-constexpr int kGateThreads = 256;          // gate pre-pass: one wave per chunk
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -185,54 +183,6 @@ __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos
   len = int(e0 - b0);
 }
 
-// Gate-data slot of chunk 0 of sequence n: floor(bos / C) + n.  For ordered
-// sequences the slot ranges are disjoint, and for any clamped bounds the last
-// slot is at most floor(T / C) + N - 1, which sizes the workspace.
-__device__ __forceinline__ int gate_slot0(int bos, int n) { return bos / C + n; }
-
-// Gates of every chunk (reference PRE:1706-1722 and the chunk-local cumsum of
-// PRE:1721): one block per (v-head, sequence), one wave per chunk, lane = token.
-// Writes the GSZ floats of gate data of each chunk to gws[(chunk slot, hv)];
-// rows past the sequence end carry a zero log-decay and beta = 0.
-template <typename CuT>
-__global__ __launch_bounds__(kGateThreads) void gdn_prefill_gates_kernel(
-    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
-    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
-    const CuT* __restrict__ cu_seqlens, int T, int HV, float scale, float* __restrict__ gws) {
-  const int hv = blockIdx.x;
-  const int n = blockIdx.y;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  int bos, len;
-  seq_bounds(cu_seqlens, n, T, bos, len);
-  const int slot0 = gate_slot0(bos, n);
-  const int n_chunks = (len + C - 1) / C;
-  const float a_log_exp = expf(A_log[hv]);
-  const float dtb = dt_bias[hv];
-  for (int ch = wave; ch < n_chunks; ch += kGateThreads / 64) {
-    const int L = min(C, len - ch * C);
-    float ld = 0.f, bt = 0.f;
-    if (lane < L) {
-      const size_t gi = size_t(bos + ch * C + lane) * HV + hv;
-      ld = -a_log_exp * softplus_stable(bf16_bits_to_f32(a[gi]) + dtb);
-      bt = sigmoidf_(bf16_bits_to_f32(b[gi]));
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(ld, off, 64);
-      if (lane >= off) ld += y;
-    }
-    const float gl = __shfl(ld, L - 1, 64);
-    const float eg = expf(ld);
-    float* g = gws + (size_t(slot0 + ch) * HV + hv) * GSZ;
-    g[G_L2 + lane] = ld * 1.44269504088896341f;
-    g[G_BETA + lane] = bt;
-    g[G_EG + lane] = eg;
-    g[G_EGS + lane] = scale * eg;
-    g[G_ED + lane] = expf(gl - ld);
-  }
-}
-
 // Lower 16x16 tiles of a 64x64 chunk matrix, row-major: tile -> (ti, tj).
 template <int TILE>
 struct Tile16 {
@@ -248,13 +198,14 @@ using IC = std::integral_constant<int, N>;
 // issue every copy into LDS; each SIMD hosts two waves of each kind.  In
 // iteration i the chain works on chunk i while the preparation waves build
 // chunk i+1, in four phases separated by LDS barriers:
-//   P1   chain : K S^T, X                   prep : 32-row merge of Tm_i; stores of O_{i-1}
+//   P1   chain : K S^T, X                   prep : 32-row merge of Tm_i; stores of O_{i-1};
+//                                                  gate data of chunk i+1 (wave 8)
 //   P2   chain : scale e^gam Q S^T, Tm X,   prep : copy of V_{i+1}; A_{i+1} tiles;
 //                P Vn, O -> Ost, Vd                fp16 K_{i+1}
 //   P3a  chain : S update, first half of k  prep : diagonal blocks of Tm_{i+1} (wave 8);
 //                                                  P_{i+1} tiles; fp16 Q_{i+1}
 //   P3b  chain : S update, second half      prep : 16-row merges of Tm_{i+1}; copies of
-//                                                  K/Q/gates of chunk i+2
+//                                                  K/Q of chunk i+2, a/b for its gates
 // The S update reads K^T through transposing LDS reads.  Copies are issued one
 // phase or more before their first use and waited for with explicit vmcnt
 // counts by the waves that issued them.  Which wave computes which tile is
@@ -263,7 +214,9 @@ template <typename CuT>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ h0,
-    const CuT* __restrict__ cu_seqlens, const float* __restrict__ gws, int T, int HQ, int HV,
+    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
+    const CuT* __restrict__ cu_seqlens, int T, int HQ, int HV,
     float scale, uint16_t* __restrict__ out, float* __restrict__ ht) {
   __shared__ Smem sm;
   __shared__ SmemRaw raw;
@@ -287,7 +240,10 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 
   int bos, len;
   seq_bounds(cu_seqlens, n, T, bos, len);
-  const int slot0 = gate_slot0(bos, n);
+  // gate inputs of this head (uniform)
+  const float a_log_exp = expf(A_log[hv]);
+  const float dtb = dt_bias[hv];
+  uint16_t ga = 0, gb = 0;          // a, b of token (chunk start + lane), preparation wave 0
   const size_t qk_stride = size_t(HQ) * D;   // elements per token in q / k
   const size_t v_stride = size_t(HV) * D;    // elements per token in v / out
   const int n_chunks = (len + C - 1) / C;
@@ -306,7 +262,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // covers 4 rows: lane l carries row row0 + l/16, swizzle slot l%16 (rows past
   // the chunk end are clamped to its last row).  Preparation wave p copies
   // K/Q/V rows [8p, 8p+8); preparation wave 0 also copies the gate data.
-  auto copy_kq = [&](int ch) {      // 4 instructions per wave (+2 on preparation wave 0)
+  auto copy_kq = [&](int ch) {      // 4 instructions per wave (+2 loads of a, b on preparation wave 0)
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
 #pragma unroll
@@ -318,10 +274,10 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       lds_dma16(k + off, &raw.k[row0 * D]);
       lds_dma16(q + off, &raw.q[row0 * D]);
     }
-    if (pw == 0) {
-      const float* gsrc = gws + (size_t(slot0 + ch) * HV + hv) * GSZ;
-      lds_dma16(gsrc + 4 * lane, &gbuf[ch & 1][0]);
-      if (lane < (GSZ - 256) / 4) lds_dma16(gsrc + 256 + 4 * lane, &gbuf[ch & 1][256]);
+    if (pw == 0) {                  // a, b of the chunk's tokens for gate_compute
+      const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
+      ga = a[gi];
+      gb = b[gi];
     }
   };
   auto copy_v = [&](int ch) {       // 2 instructions per wave
@@ -335,6 +291,33 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + 8 * src_chunk,
                 &rawV[row0 * D]);
     }
+  };
+
+  // Gate data of chunk ch (reference PRE:1706-1722 and the chunk-local cumsum
+  // of PRE:1721) from a / b loaded by copy_kq, into gbuf[ch & 1]: lane =
+  // token; rows past the sequence end carry a zero log-decay and beta = 0.
+  // Preparation wave 0, after its copies of chunk ch have been waited for.
+  auto gate_compute = [&](int ch) {
+    constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
+    const int L = chunk_len(ch);
+    float ld = 0.f, bt = 0.f;
+    if (lane < L) {
+      // softplus(x) = max(x, 0) + ln(1 + e^-|x|); sigmoid(y) = 1 / (1 + e^-y)
+      const float x = bf16_bits_to_f32(ga) + dtb;
+      const float sp = fmaxf(x, 0.f) + kLn2 * __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e));
+      ld = -a_log_exp * sp;
+      bt = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-bf16_bits_to_f32(gb) * kLog2e));
+    }
+    ld = wave_inclusive_scan(ld);       // gam: chunk-local cumsum (<= 0)
+    const float l2 = ld * kLog2e;
+    const float gl2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), L - 1));
+    const float eg = __builtin_amdgcn_exp2f(l2);
+    float* gdst = gbuf[ch & 1];
+    gdst[G_L2 + lane] = l2;
+    gdst[G_BETA + lane] = bt;
+    gdst[G_EG + lane] = eg;
+    gdst[G_EGS + lane] = scale * eg;
+    gdst[G_ED + lane] = __builtin_amdgcn_exp2f(gl2 - l2);
   };
 
   // ---------------- preparation steps (state-independent)
@@ -655,6 +638,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       copy_kq(0);
       copy_v(0);
       wait_vm<0>();
+      if (pw == 0) gate_compute(0);
       lds_barrier();
       convert_k(0, 0);
       tiles_A(gbuf[0]);
@@ -679,6 +663,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       } else if (more) {
         wait_vm<0>();
       }
+      if (more && pw == 0) gate_compute(ch + 1);
       lds_barrier();
       // ---- P2: V copy, A tiles and fp16 K of chunk ch+1
       if (more) {
@@ -718,17 +703,14 @@ int check_prefill_args(const void* q, const void* k, const void* v, const void* 
   return GDN_OK;
 }
 
-// Gate data: GSZ floats per (chunk slot, v-head), floor(T / C) + N slots.
-size_t gate_workspace_bytes(int N, int T, int HV) {
-  return (size_t(T / C) + size_t(N)) * size_t(HV) * GSZ * sizeof(float);
-}
-
 }  // namespace
 
 extern "C" size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV) {
+  (void)N;
+  (void)T;
   (void)HQ;
-  if (N <= 0 || T < 0 || HV <= 0) return 0;
-  return gate_workspace_bytes(N, T, HV);
+  (void)HV;
+  return 0;
 }
 
 extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -737,31 +719,23 @@ extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint1
                                int cu_is_int32, int N, int T, int HQ, int HV, float scale,
                                uint16_t* out, float* final_state, void* workspace,
                                size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
                                     N, T, HQ, HV);
   if (rc != GDN_OK) return rc;
   if (N == 0) return GDN_OK;
-  if (workspace == nullptr || workspace_bytes < gate_workspace_bytes(N, T, HV) ||
-      (reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
-    return GDN_ERR_WORKSPACE;
-  float* gws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 ggrid{unsigned(HV), unsigned(N), 1u};
   const dim3 grid{unsigned(N) * unsigned(HV), 1u, 1u};
   const dim3 block(kThreads);
-  const dim3 gblock(kGateThreads);
   if (cu_is_int32) {
-    const int32_t* cu = static_cast<const int32_t*>(cu_seqlens);
-    hipLaunchKernelGGL(gdn_prefill_gates_kernel<int32_t>, ggrid, gblock, 0, st, A_log, a, dt_bias,
-                       b, cu, T, HV, scale, gws);
-    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state, cu,
-                       gws, T, HQ, HV, scale, out, final_state);
+    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state, A_log,
+                       a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), T, HQ, HV, scale,
+                       out, final_state);
   } else {
-    const int64_t* cu = static_cast<const int64_t*>(cu_seqlens);
-    hipLaunchKernelGGL(gdn_prefill_gates_kernel<int64_t>, ggrid, gblock, 0, st, A_log, a, dt_bias,
-                       b, cu, T, HV, scale, gws);
-    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state, cu,
-                       gws, T, HQ, HV, scale, out, final_state);
+    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state, A_log,
+                       a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), T, HQ, HV, scale,
+                       out, final_state);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : -int(err);
