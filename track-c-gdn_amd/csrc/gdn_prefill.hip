@@ -216,16 +216,26 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ v, const float* __restrict__ h0,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
-    const CuT* __restrict__ cu_seqlens, int T, int HQ, int HV,
+    const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV,
     float scale, uint16_t* __restrict__ out, float* __restrict__ ht) {
   __shared__ Smem sm;
   __shared__ SmemRaw raw;
   __shared__ __align__(16) uint16_t rawV[C * D];     // V chunk (bf16, swizzled), DMA target
   __shared__ __align__(16) float gbuf[2][GSZ];       // gate data, DMA target, double-buffered
 
-  const int n = blockIdx.x / HV;
-  const int hv = blockIdx.x - n * HV;
-  const int hq = hv / (HV / HQ);
+  // Workgroup -> (sequence n, v-head hv).  The R = HV/HQ v-heads that share a
+  // qk-head read the same K/Q rows; they get workgroup ids 8 apart, which the
+  // dispatcher places on the same XCD (ids go round-robin over the 8 XCDs),
+  // so the second read of a K/Q row can hit that XCD's L2.  Unit u = (n, hq)
+  // and member m map to id 8 (R (u / 8) + m) + u % 8; ids past the last unit
+  // exit at once.
+  const int R = HV / HQ;
+  const int xcd = blockIdx.x & 7, row = blockIdx.x >> 3;
+  const int unit = 8 * (row / R) + xcd;
+  if (unit >= N * HQ) return;
+  const int n = unit / HQ;
+  const int hq = unit - n * HQ;
+  const int hv = hq * R + (row - (row / R) * R);
   int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keep it scalar
   int lane = tid & 63;
@@ -726,15 +736,16 @@ extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint1
   if (rc != GDN_OK) return rc;
   if (N == 0) return GDN_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid{unsigned(N) * unsigned(HV), 1u, 1u};
+  const unsigned units = unsigned(N) * unsigned(HQ);
+  const dim3 grid{8u * unsigned(HV / HQ) * ((units + 7u) / 8u), 1u, 1u};
   const dim3 block(kThreads);
   if (cu_is_int32) {
     hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state, A_log,
-                       a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), T, HQ, HV, scale,
+                       a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), N, T, HQ, HV, scale,
                        out, final_state);
   } else {
     hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state, A_log,
-                       a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), T, HQ, HV, scale,
+                       a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), N, T, HQ, HV, scale,
                        out, final_state);
   }
   const hipError_t err = hipGetLastError();
