@@ -223,19 +223,19 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   __shared__ __align__(16) uint16_t rawV[C * D];     // V chunk (bf16, swizzled), DMA target
   __shared__ __align__(16) float gbuf[2][GSZ];       // gate data, DMA target, double-buffered
 
-  // Workgroup -> (sequence n, v-head hv).  The R = HV/HQ v-heads that share a
+  // Workgroup -> (sequence n, v-head hv).  The G = HV/HQ v-heads that share a
   // qk-head read the same K/Q rows; they get workgroup ids 8 apart, which the
   // dispatcher places on the same XCD (ids go round-robin over the 8 XCDs),
   // so the second read of a K/Q row can hit that XCD's L2.  Unit u = (n, hq)
-  // and member m map to id 8 (R (u / 8) + m) + u % 8; ids past the last unit
+  // and member m map to id 8 (G (u / 8) + m) + u % 8; ids past the last unit
   // exit at once.
-  const int R = HV / HQ;
-  const int xcd = blockIdx.x & 7, row = blockIdx.x >> 3;
-  const int unit = 8 * (row / R) + xcd;
+  const int heads_per_qk = HV / HQ;
+  const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
+  const int unit = 8 * (id_row / heads_per_qk) + xcd;
   if (unit >= N * HQ) return;
   const int n = unit / HQ;
   const int hq = unit - n * HQ;
-  const int hv = hq * R + (row - (row / R) * R);
+  const int hv = hq * heads_per_qk + (id_row - (id_row / heads_per_qk) * heads_per_qk);
   int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keep it scalar
   int lane = tid & 63;
