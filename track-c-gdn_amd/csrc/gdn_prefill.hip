@@ -18,9 +18,11 @@
 //   Vn  = Tm X          ( = U - W S^T of the reference )
 //   O   = scale diag(e^gam) Q S^T + P Vn
 //   S  <- e^{gam_L} S + (diag(e^{gam_L-gam}) Vn)^T K
-// The products with S, X and Vn run on fp16 operands (bf16 inputs convert
-// exactly in fp16's normal range; fp16 keeps 3 more mantissa bits than bf16
-// for the state and intermediates) with fp32 accumulation.
+// The products on the state's path (K S^T, Tm X, the S update) run on fp16
+// operands (bf16 inputs convert exactly in fp16's normal range; fp16 keeps 3
+// more mantissa bits than bf16 for the state and intermediates); Q S^T, which
+// only reaches the bf16 output, takes the raw bf16 Q rows and a bf16 copy of
+// S.  All products accumulate in fp32.
 //
 // Chain wave w (of 8) owns state rows v in [16w, 16w+16): every product that
 // touches S, X, Vn or O is split along v, so the waves never exchange state.
@@ -44,9 +46,8 @@ constexpr int D = kHeadDim;   // 128
 constexpr int C = 64;         // chunk
 // Row strides, chosen so that the MFMA operand reads (16-byte reads down 16
 // rows, and the transposing 8-byte reads down 4 rows x 4 quads) are free of
-// LDS bank conflicts: rows of 288 B (Kc / Qc, A) and 160 B (Tm / P).
-constexpr int KCLD = D + 16;  // Kc / Qc row stride (halves): 288 B rows
-constexpr int OLD = D + 8;    // Ost row stride (halves): 272 B rows
+// LDS bank conflicts: rows of 288 B (Kc, A) and 160 B (Tm / P).
+constexpr int KCLD = D + 16;  // Kc row stride (halves): 288 B rows
 constexpr int TLD = C + 16;   // Tm / P row stride (halves): 160 B rows
 constexpr int ALD = C + 8;    // A row stride (floats): 288 B rows
 // Gate data per chunk, GSZ floats: gam log2(e) | beta | e^gam | scale e^gam | e^(gam_L - gam)
@@ -62,6 +63,7 @@ constexpr int kRowsPerWave = D / kChainWaves;   // 16 state rows (v) per chain w
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 // Column order inside every 32-column group of the fp16 operand tiles: column
@@ -79,17 +81,15 @@ __device__ __forceinline__ int p32(int c) {
 __device__ __forceinline__ int raw_off(int t, int col) { return t * D + 8 * ((col >> 3) ^ (t & 15)) + (col & 7); }
 
 struct __align__(16) SmemRaw {
-  uint16_t k[C * D];           // next chunk's K rows (bf16, swizzled), DMA target
-  uint16_t q[C * D];           // next chunk's Q rows (bf16, swizzled), DMA target
+  uint16_t k[2][C * D];        // K rows of the chunks of parity 0 / 1 (bf16, swizzled), DMA target
+  uint16_t q[2][C * D];        // Q rows of the chunks of parity 0 / 1 (bf16, swizzled), DMA target
 };
 
 struct __align__(16) Smem {
   _Float16 Kc[2][C * KCLD];    // K chunk in fp16 [t][p32(k)], double-buffered
-  _Float16 Qc[C * KCLD];       // Q chunk in fp16 [t][p32(k)]
   _Float16 Tm[C * TLD];        // (I + A)^-1 [t][p32(t')]
   _Float16 P[C * TLD];         // decayed causal Q K^T [t][p32(t')]
   float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32)
-  uint16_t Ost[C * OLD];       // output chunk staging (bf16) [t][v]
 };
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
@@ -131,6 +131,12 @@ __device__ __forceinline__ f16x8 ld_f32x8_as_f16(const float* p) {
 __device__ __forceinline__ f16x8 pack2(const f32x4& a, const f32x4& b) {
   return f16x8{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
                (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
+}
+
+// Two stacked 16x16 accumulator tiles -> one 8-slot bf16 operand.
+__device__ __forceinline__ bf16x8_t pack2_bf(const f32x4& a, const f32x4& b) {
+  return bf16x8_t{(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                  (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
 }
 
 __device__ __forceinline__ f16x8 pack8(const f32x16& x, int s) {
@@ -194,19 +200,22 @@ using IC = std::integral_constant<int, N>;
 
 // The state chain.  One workgroup of 16 waves per (sequence, v-head): waves
 // 0-7 run the chain (wave w owns state rows v in [16w, 16w+16), all of its
-// products are 16x16x32 MFMAs), waves 8-15 prepare chunks, store outputs and
-// issue every copy into LDS; each SIMD hosts two waves of each kind.  In
-// iteration i the chain works on chunk i while the preparation waves build
-// chunk i+1, in four phases separated by LDS barriers:
-//   P1   chain : K S^T, X                   prep : 32-row merge of Tm_i; stores of O_{i-1};
-//                                                  gate data of chunk i+1 (wave 8)
-//   P2   chain : scale e^gam Q S^T, Tm X,   prep : copy of V_{i+1}; A_{i+1} tiles;
-//                P Vn, O -> Ost, Vd                fp16 K_{i+1}
-//   P3a  chain : S update, first half of k  prep : diagonal blocks of Tm_{i+1} (wave 8);
-//                                                  P_{i+1} tiles; fp16 Q_{i+1}
-//   P3b  chain : S update, second half      prep : 16-row merges of Tm_{i+1}; copies of
-//                                                  K/Q of chunk i+2, a/b for its gates
-// The S update reads K^T through transposing LDS reads.  Copies are issued one
+// products are 16x16x32 MFMAs) and store the outputs; waves 8-15 prepare
+// chunks and issue every copy into LDS; each SIMD hosts two waves of each
+// kind.  In iteration i the chain works on chunk i while the preparation
+// waves build chunk i+1, in four phases separated by LDS barriers:
+//   P1   chain : K S^T, X                   prep : Tm_i merges (wave 15); gate data
+//                                                  of chunk i+1 (wave 8)
+//   P2   chain : Vn = Tm X, Vd              prep : copy of V_{i+1}; A_{i+1} tiles
+//   P3a  chain : O = scale e^gam Q S^T      prep : rows 0-11 of the Tm_{i+1} diagonal
+//                + P Vn -> HBM; S update,          blocks (wave 8); fp16 K_{i+1}
+//                first half of k
+//   P3b  chain : S update, second half      prep : rows 12-15 of those blocks (wave 8);
+//                                                  P_{i+1} tiles; copies of K/Q of
+//                                                  chunk i+2, a/b for its gates
+// Raw K and Q rows are double-buffered by chunk parity, so the chain reads the
+// Q rows of chunk i while the P tiles of chunk i+1 read the next ones.  The S
+// update reads K^T through transposing LDS reads.  Copies are issued one
 // phase or more before their first use and waited for with explicit vmcnt
 // counts by the waves that issued them.  Which wave computes which tile is
 // fixed at compile time, so tile offsets are immediates.
@@ -281,8 +290,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       const int row = row0 + (lane >> 4);
       const int src_chunk = (lane & 15) ^ (row & 15);
       const size_t off = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_chunk;
-      lds_dma16(k + off, &raw.k[row0 * D]);
-      lds_dma16(q + off, &raw.q[row0 * D]);
+      lds_dma16(k + off, &raw.k[ch & 1][row0 * D]);
+      lds_dma16(q + off, &raw.q[ch & 1][row0 * D]);
     }
     if (pw == 0) {                  // a, b of the chunk's tokens for gate_compute
       const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
@@ -351,10 +360,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     }
   };
   // K rows of chunk ch -> Kc[kb] (all preparation waves).
-  auto convert_k = [&](int ch, int kb) { convert_rows(raw.k, sm.Kc[kb], chunk_len(ch), ptid, kPrepThreads); };
-  // Q rows of chunk ch -> Qc (preparation waves 1-7).
-  auto convert_q = [&](int ch) {
-    convert_rows(raw.q, sm.Qc, chunk_len(ch), ptid - 64, kPrepThreads - 64);
+  auto convert_k = [&](int ch, int first, int step) {
+    convert_rows(raw.k[ch & 1], sm.Kc[ch & 1], chunk_len(ch), first, step);
   };
   // Per-lane swizzled offsets of the 8-column pieces this lane reads from a
   // raw row r with r % 16 == c: piece 4 ks + g sits in slot (4 ks + g) ^ c.
@@ -364,14 +371,14 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // A tile = tril_strict(beta_i e^{gam_i - gam_j} K K^T) from the raw bf16
   // rows (bf16 MFMA: the inputs are exact).  Diagonal tiles also store the
   // transpose of their strict lower part in the (otherwise unused) upper part.
-  auto tile_A = [&](auto tile_c, const float* gd) {
+  auto tile_A = [&](auto tile_c, const float* gd, int pb) {
     constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
     constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
     bf16x8_t fa[4], fb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      fa[ks] = ld16_bf(&raw.k[raw_lane[ks] + 16 * ti * D]);
-      fb[ks] = ld16_bf(&raw.k[raw_lane[ks] + 16 * tj * D]);
+      fa[ks] = ld16_bf(&raw.k[pb][raw_lane[ks] + 16 * ti * D]);
+      fb[ks] = ld16_bf(&raw.k[pb][raw_lane[ks] + 16 * tj * D]);
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -393,14 +400,14 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the raw bf16 rows
   // (bf16 MFMA: the inputs are exact).  Rows past the chunk end hold copies of
   // its last row; they only reach output rows that are never stored.
-  auto tile_P = [&](auto tile_c, const float* gd) {
+  auto tile_P = [&](auto tile_c, const float* gd, int pb) {
     constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
     constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
     bf16x8_t fa[4], fb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      fa[ks] = ld16_bf(&raw.q[raw_lane[ks] + 16 * ti * D]);
-      fb[ks] = ld16_bf(&raw.k[raw_lane[ks] + 16 * tj * D]);
+      fa[ks] = ld16_bf(&raw.q[pb][raw_lane[ks] + 16 * ti * D]);
+      fb[ks] = ld16_bf(&raw.k[pb][raw_lane[ks] + 16 * tj * D]);
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -415,30 +422,31 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       sm.P[(16 * ti + 4 * g + i) * TLD + pcc] = (_Float16)val;
     }
   };
-  // A tiles of a chunk: 10 tiles over the 8 preparation waves.
-  auto tiles_A = [&](const float* gd) {
+  // A tiles of the chunk of parity pb: 10 tiles over the 8 preparation waves.
+  auto tiles_A = [&](const float* gd, int pb) {
     switch (pw) {
-      case 0: tile_A(IC<0>{}, gd); tile_A(IC<8>{}, gd); break;
-      case 1: tile_A(IC<2>{}, gd); tile_A(IC<7>{}, gd); break;
-      case 2: tile_A(IC<5>{}, gd); break;
-      case 3: tile_A(IC<9>{}, gd); break;
-      case 4: tile_A(IC<1>{}, gd); break;
-      case 5: tile_A(IC<3>{}, gd); break;
-      case 6: tile_A(IC<4>{}, gd); break;
-      default: tile_A(IC<6>{}, gd); break;
+      case 0: tile_A(IC<0>{}, gd, pb); tile_A(IC<8>{}, gd, pb); break;
+      case 1: tile_A(IC<2>{}, gd, pb); tile_A(IC<7>{}, gd, pb); break;
+      case 2: tile_A(IC<5>{}, gd, pb); break;
+      case 3: tile_A(IC<9>{}, gd, pb); break;
+      case 4: tile_A(IC<1>{}, gd, pb); break;
+      case 5: tile_A(IC<3>{}, gd, pb); break;
+      case 6: tile_A(IC<4>{}, gd, pb); break;
+      default: tile_A(IC<6>{}, gd, pb); break;
     }
   };
-  // Diagonal 16x16 blocks of Tm: lane group g inverts block g by forward
-  // substitution in fp32 (lane = column).
-  auto diag_all4 = [&]() {
+  // Rows [I0, I1) of the diagonal 16x16 blocks of Tm: lane group g inverts
+  // block g by forward substitution in fp32 (lane = column); x holds the
+  // solved rows, so a later call continues where an earlier one stopped.
+  auto diag_rows = [&](auto i0_c, auto i1_c, float(&x)[16]) {
+    constexpr int I0 = decltype(i0_c)::value, I1 = decltype(i1_c)::value;
     const float* Ab = &sm.A[(16 * g) * ALD + 16 * g];
-    // Opaque copy of the column index: keeps the 16 identity selects inside
+    // Opaque copy of the column index: keeps the identity selects inside
     // the chunk loop instead of being hoisted into registers.
     int cid = c;
     asm volatile("" : "+v"(cid));
-    float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = I0; i < I1; ++i) {
       // bound the live A rows: loads of rows 4b.. are not hoisted above row 4b
       if ((i & 3) == 0) asm volatile("" ::: "memory");
       float sum = (i == cid) ? 1.f : 0.f;
@@ -453,7 +461,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     }
     const int pc = p32(16 * g + c);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.Tm[(16 * g + i) * TLD + pc] = (_Float16)x[i];
+    for (int i = I0; i < I1; ++i) sm.Tm[(16 * g + i) * TLD + pc] = (_Float16)x[i];
   };
   // 16-row merge inside the 32-row block at a0: T_{a0+16.., a0..} = -T_22 A_21 T_11.
   auto merge16 = [&](int a0) {
@@ -470,16 +478,16 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g + i) * TLD + pcb] = (_Float16)(-t21[i]);
   };
-  // Preparation wave 0 builds the diagonal blocks of Tm; the P tiles go to waves 1-6.
-  auto diag_or_tiles_P = [&](const float* gd) {
+  // P tiles of the chunk of parity pb: 10 tiles over preparation waves 1-7.
+  auto tiles_P = [&](const float* gd, int pb) {
     switch (pw) {
-      case 0: diag_all4(); break;
-      case 1: tile_P(IC<0>{}, gd); tile_P(IC<8>{}, gd); break;
-      case 2: tile_P(IC<2>{}, gd); tile_P(IC<7>{}, gd); break;
-      case 3: tile_P(IC<5>{}, gd); tile_P(IC<6>{}, gd); break;
-      case 4: tile_P(IC<9>{}, gd); tile_P(IC<4>{}, gd); break;
-      case 5: tile_P(IC<1>{}, gd); break;
-      case 6: tile_P(IC<3>{}, gd); break;
+      case 1: tile_P(IC<0>{}, gd, pb); tile_P(IC<8>{}, gd, pb); break;
+      case 2: tile_P(IC<2>{}, gd, pb); tile_P(IC<7>{}, gd, pb); break;
+      case 3: tile_P(IC<5>{}, gd, pb); tile_P(IC<6>{}, gd, pb); break;
+      case 4: tile_P(IC<9>{}, gd, pb); break;
+      case 5: tile_P(IC<1>{}, gd, pb); break;
+      case 6: tile_P(IC<3>{}, gd, pb); break;
+      case 7: tile_P(IC<4>{}, gd, pb); break;
       default: break;
     }
   };
@@ -509,20 +517,6 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
   };
-  // O of a chunk: 16-byte stores of rows t < L (2 per preparation lane).
-  auto store_out = [&](int ch) {
-    const int t0 = bos + ch * C;
-    const int L = chunk_len(ch);
-    uint16_t* obase = out + size_t(t0) * v_stride + size_t(hv) * D;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int qi = ptid + kPrepThreads * r;
-      const int row = qi >> 4, c8 = (qi & 15) * 8;
-      const uint4 w = *reinterpret_cast<const uint4*>(&sm.Ost[row * OLD + c8]);
-      if (L == C || row < L) *reinterpret_cast<uint4*>(obase + size_t(row) * v_stride + c8) = w;
-    }
-  };
-
   if (is_chain) {
     // ================= chain waves
     // initial state: Sacc[kb][i] = S[vrow][16 kb + 4 g + i]
@@ -538,14 +532,18 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       lds_barrier();
       lds_barrier();
       lds_barrier();
-      lds_barrier();
     }
     for (int ch = 0; ch < n_chunks; ++ch) {
+      // Opaque refresh of the lane indices: lane-dependent LDS and HBM offsets
+      // are recomputed in every iteration instead of being hoisted out of the
+      // loop into registers that would not fit.
+      asm volatile("" : "+v"(g), "+v"(c), "+v"(lane));
       const int L = chunk_len(ch);
       const int kb_buf = ch & 1;
       const float* gd = gbuf[ch & 1];
+      const int vrow = v0 + c;
 
-      // ---- P1: K S^T, Q S^T, X
+      // ---- P1: K S^T, X
       f32x4 KS[4];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -570,25 +568,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
       lds_barrier();
 
-      // ---- P2: scale e^gam Q S^T, Tm X, O -> Ost, Vd
-      f16x8 Vdb[2];
+      // ---- P2: Vn = Tm X, Vd
+      f16x8 Vdb[2], Vnb[2];
       {
-        f32x4 QS[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const _Float16* qbase = &sm.Qc[c * KCLD + 8 * g];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) QS[tb] = mfma16(ld16(qbase + 16 * tb * KCLD + 32 * p), sb, QS[tb]);
-        }
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) QS[tb][i] *= egs[i];
-        }
         const f16x8 Xb[2] = {pack2(KS[0], KS[1]), pack2(KS[2], KS[3])};
         f32x4 Vn[4];
 #pragma unroll
@@ -598,7 +580,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
           for (int p = 0; p <= (tb >> 1); ++p) Vn[tb] = mfma16(ld16(trow + 32 * p), Xb[p], Vn[tb]);
         }
-        const f16x8 Vnb[2] = {pack2(Vn[0], Vn[1]), pack2(Vn[2], Vn[3])};
+        Vnb[0] = pack2(Vn[0], Vn[1]);
+        Vnb[1] = pack2(Vn[2], Vn[3]);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
           const f32x4 ed = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb + 4 * g]);
@@ -607,22 +590,69 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         }
         Vdb[0] = pack2(Vn[0], Vn[1]);
         Vdb[1] = pack2(Vn[2], Vn[3]);
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
-#pragma unroll
-          for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            sm.Ost[(16 * tb + 4 * g + i) * OLD + vrow] = f32_to_bf16_bits(QS[tb][i]);
-        }
       }
       const float egL = gd[G_EG + L - 1];
       lds_barrier();
 
-      // ---- P3a / P3b: state update, S = e^{gam_L} S + K^T Vd, in two halves of k
+      // ---- P3a / P3b: state update, S = e^{gam_L} S + K^T Vd, in two halves of
+      //      k; before it, in P3a, O = scale e^gam Q S^T + P Vn goes to HBM
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
+        if (half == 0) {
+          f32x4 QS[4];
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          // Element offsets, in a raw Q row t with t % 16 == c, of the two
+          // 4-column pieces lane group g feeds as k-slots 0-3 / 4-7 of the
+          // MFMA over column block p: columns 32 p + 4 g .. +3 and
+          // 32 p + 16 + 4 g .. +3, the order in which two stacked S^T
+          // accumulator tiles give the B operand.
+          const int sw = (g >> 1) ^ c;
+          const uint16_t* qraw = &raw.q[kb_buf][c * D + 4 * (g & 1)];
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const bf16x8_t sb = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+              const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p) ^ sw)]);
+              const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p + 2) ^ sw)]);
+              // keeps the two reads of one fragment next to each other: paired with
+              // reads of other fragments they would land in registers that need moves
+              asm volatile("" ::: "memory");
+              QS[tb] = mfma16_bf(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), sb, QS[tb]);
+            }
+          }
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) QS[tb][i] *= egs[i];
+            const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
+#pragma unroll
+            for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
+          }
+          // Row t of the chunk's output at obase + t row_bytes + this lane's
+          // column: a uniform row address plus a 32-bit lane offset.
+          char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
+          const size_t row_bytes = v_stride * sizeof(uint16_t);
+          const uint32_t olane = uint32_t(4 * g) * uint32_t(row_bytes) + uint32_t(vrow) * 2u;
+          if (L == C) {
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<uint16_t*>(obase + size_t(16 * tb + i) * row_bytes + olane) =
+                    f32_to_bf16_bits(QS[tb][i]);
+          } else {
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (16 * tb + 4 * g + i < L)
+                  *reinterpret_cast<uint16_t*>(obase + size_t(16 * tb + i) * row_bytes + olane) =
+                      f32_to_bf16_bits(QS[tb][i]);
+          }
+        }
 #pragma unroll
         for (int kb = 4 * half; kb < 4 * half + 4; ++kb) {
           Sacc[kb] *= egL;
@@ -639,59 +669,72 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         lds_barrier();
       }
     }
-    float* dst = ht + state_off;
+    asm volatile("" : "+v"(g), "+v"(c));
+    float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
   } else {
     // ================= preparation waves
-    if (n_chunks > 0) {           // prologue: chunk 0 copied and prepared
+    // The preparation waves run single-wave dependency chains (Tm inverse and
+    // merges, gates) that bound the chunk period; issuing their instructions
+    // ahead of the chain waves' shortens it.
+    __builtin_amdgcn_s_setprio(2);
+    float dx[16];                 // solved rows of the Tm diagonal blocks (preparation wave 0)
+    if (n_chunks > 0) {           // prologue: chunk 0 copied and prepared up to its Tm merges
       copy_kq(0);
       copy_v(0);
       wait_vm<0>();
       if (pw == 0) gate_compute(0);
+      if (n_chunks > 1) copy_kq(1);   // after gate_compute(0): reloads a and b
       lds_barrier();
-      convert_k(0, 0);
-      tiles_A(gbuf[0]);
+      tiles_A(gbuf[0], 0);
+      convert_k(0, ptid, kPrepThreads);
       lds_barrier();
-      diag_or_tiles_P(gbuf[0]);
-      if (pw > 0) convert_q(0);
+      if (pw == 0) {
+        diag_rows(IC<0>{}, IC<12>{}, dx);
+        diag_rows(IC<12>{}, IC<16>{}, dx);
+      } else {
+        tiles_P(gbuf[0], 0);
+      }
       lds_barrier();
-      if (pw < 2) merge16(32 * pw);
-      lds_barrier();
-      if (n_chunks > 1) copy_kq(1);
     }
     for (int ch = 0; ch < n_chunks; ++ch) {
       asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g), "+v"(c), "+v"(ptid));
-      const int kb_buf = ch & 1;
+      const int nb = (ch + 1) & 1;          // parity of chunk ch+1
       const bool more = ch + 1 < n_chunks;
-      // ---- P1: 32-row merge of Tm_ch; stores of O_{ch-1}; K/Q rows and gates of
-      //      chunk ch+1 landed (copied in P3a of ch-1; only the 2 stores may remain)
-      if (pw == kPrepWaves - 1) merge32();
-      if (ch > 0) {
-        store_out(ch - 1);
-        if (more) wait_vm<2>();
-      } else if (more) {
-        wait_vm<0>();
+      // ---- P1: Tm merges of chunk ch (preparation wave 7); K/Q rows, a and b of
+      //      chunk ch+1 landed (copied in P3b of ch-1); gate data of ch+1 (wave 0)
+      if (pw == kPrepWaves - 1) {
+        merge16(0);
+        merge16(32);
+        merge32();
       }
-      if (more && pw == 0) gate_compute(ch + 1);
+      if (more) {
+        wait_vm<0>();
+        if (pw == 0) gate_compute(ch + 1);
+      }
       lds_barrier();
-      // ---- P2: V copy, A tiles and fp16 K of chunk ch+1
+      // ---- P2: V copy and A tiles of chunk ch+1
       if (more) {
         copy_v(ch + 1);           // every chain wave has read V of chunk ch
-        tiles_A(gbuf[(ch + 1) & 1]);
-        convert_k(ch + 1, kb_buf ^ 1);
+        tiles_A(gbuf[nb], nb);
       }
       lds_barrier();
-      // ---- P3a: Tm diagonal blocks, P tiles and fp16 Q of chunk ch+1 (Q S^T of
-      //      chunk ch was taken in P2)
+      // ---- P3a: rows 0-11 of the Tm diagonal blocks (wave 0) and the fp16 K
+      //      rows (waves 1-7) of chunk ch+1; the chain has read Tm of ch in P2
       if (more) {
-        diag_or_tiles_P(gbuf[(ch + 1) & 1]);
-        if (pw > 0) convert_q(ch + 1);
+        if (pw == 0) diag_rows(IC<0>{}, IC<12>{}, dx);
+        else convert_k(ch + 1, ptid - 64, kPrepThreads - 64);
       }
       lds_barrier();
-      // ---- P3b: 16-row merges of Tm_{ch+1}; copies of chunk ch+2 (the raw rows of
-      //      ch+1 are read); V of chunk ch+1 landed (only those 4 (+2) copies remain)
-      if (more && pw < 2) merge16(32 * pw);
+      // ---- P3b: rows 12-15 of the Tm diagonal blocks (wave 0) and the P tiles
+      //      (waves 1-7) of chunk ch+1, the chain having read P of ch in P3a;
+      //      copies of chunk ch+2 into the raw buffers of ch; V of chunk ch+1
+      //      landed (only those 4 (+2) copies remain)
+      if (more) {
+        if (pw == 0) diag_rows(IC<12>{}, IC<16>{}, dx);
+        else tiles_P(gbuf[nb], nb);
+      }
       if (ch + 2 < n_chunks) copy_kq(ch + 2);
       if (ch + 2 < n_chunks) {
         if (pw == 0) wait_vm<6>(); else wait_vm<4>();
@@ -700,7 +743,6 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
       lds_barrier();
     }
-    if (n_chunks > 0) store_out(n_chunks - 1);
   }
 }
 
