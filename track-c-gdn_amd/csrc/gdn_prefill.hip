@@ -50,6 +50,7 @@ constexpr int C = 64;         // chunk
 constexpr int KCLD = D + 16;  // Kc row stride (halves): 288 B rows
 constexpr int TLD = C + 16;   // Tm / P row stride (halves): 160 B rows
 constexpr int ALD = C + 8;    // A row stride (floats): 288 B rows
+constexpr int BLD = C / 2 + 8;  // Aba row stride (halves): 80 B rows
 // Gate data per chunk, GSZ floats: gam log2(e) | beta | e^gam | scale e^gam | e^(gam_L - gam)
 // (gam = chunk-local cumsum of the log-decay, gam_L its value at the chunk's last token).
 constexpr int G_L2 = 0, G_BETA = C, G_EG = 2 * C, G_EGS = 3 * C, G_ED = 4 * C;
@@ -87,9 +88,10 @@ struct __align__(16) SmemRaw {
 
 struct __align__(16) Smem {
   _Float16 Kc[2][C * KCLD];    // K chunk in fp16 [t][p32(k)], double-buffered
-  _Float16 Tm[C * TLD];        // (I + A)^-1 [t][p32(t')]
+  _Float16 Tm[C * TLD];        // diagonal 32-row blocks of (I + A)^-1 [t][p32(t')]
   _Float16 P[C * TLD];         // decayed causal Q K^T [t][p32(t')]
-  float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32)
+  float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32), diagonal 32-row blocks
+  _Float16 Aba[(C / 2) * BLD]; // its lower-left 32x32 block in fp16 [t - 32][p32(t')]
 };
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
@@ -204,15 +206,18 @@ using IC = std::integral_constant<int, N>;
 // chunks and issue every copy into LDS; each SIMD hosts two waves of each
 // kind.  In iteration i the chain works on chunk i while the preparation
 // waves build chunk i+1, in four phases separated by LDS barriers:
-//   P1   chain : K S^T, X                   prep : Tm_i merges (wave 15); gate data
-//                                                  of chunk i+1 (wave 8)
-//   P2   chain : Vn = Tm X, Vd              prep : copy of V_{i+1}; A_{i+1} tiles
+//   P1   chain : K S^T (columns 64-127), X  prep : 16-row merges of Tm_i (waves 14, 15);
+//                                                  gate data of chunk i+1 (wave 8)
+//   P2   chain : Vn = Tm X, Vd,             prep : copy of V_{i+1}; A_{i+1} tiles of
+//                scale e^gam Q S^T                 the diagonal 32-row blocks
 //   P3a  chain : O = scale e^gam Q S^T      prep : rows 0-11 of the Tm_{i+1} diagonal
-//                + P Vn -> HBM; S update,          blocks (wave 8); fp16 K_{i+1}
-//                first half of k
-//   P3b  chain : S update, second half      prep : rows 12-15 of those blocks (wave 8);
-//                                                  P_{i+1} tiles; copies of K/Q of
-//                                                  chunk i+2, a/b for its gates
+//                + P Vn -> HBM; S update,          blocks (wave 8); lower-left A_{i+1}
+//                first half of k                   tiles; fp16 K_{i+1}
+//   P3b  chain : S update, second half;     prep : rows 12-15 of those blocks (wave 8);
+//                K S^T of chunk i+1                P_{i+1} tiles; copies of K/Q of
+//                (columns 0-63)                    chunk i+2, a/b for its gates
+// The 32-row merge of Tm is left to the chain: Vn = Tm X is applied as
+// Vn_top = T_a X_top, Vn_bot = T_b (X_bot - A_ba Vn_top).
 // Raw K and Q rows are double-buffered by chunk parity, so the chain reads the
 // Q rows of chunk i while the P tiles of chunk i+1 read the next ones.  The S
 // update reads K^T through transposing LDS reads.  Copies are issued one
@@ -389,7 +394,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float val = br[i] * __builtin_amdgcn_exp2f(gr[i] - gc) * acc[i];
-      if (ti != tj) {
+      if (ti >= 2 && tj <= 1) {   // lower-left 32x32 block: an MFMA operand of the chain
+        sm.Aba[(16 * (ti - 2) + 4 * g + i) * BLD + p32(16 * tj + c)] = (_Float16)val;
+      } else if (ti != tj) {
         sm.A[(16 * ti + 4 * g + i) * ALD + 16 * tj + c] = val;
       } else if (4 * g + i > c) {
         sm.A[(16 * ti + 4 * g + i) * ALD + 16 * tj + c] = val;
@@ -422,17 +429,28 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       sm.P[(16 * ti + 4 * g + i) * TLD + pcc] = (_Float16)val;
     }
   };
-  // A tiles of the chunk of parity pb: 10 tiles over the 8 preparation waves.
+  // A tiles of the chunk of parity pb inside the diagonal 32-row blocks (the
+  // inverse's input): 6 tiles over preparation waves 0-5.
   auto tiles_A = [&](const float* gd, int pb) {
     switch (pw) {
-      case 0: tile_A(IC<0>{}, gd, pb); tile_A(IC<8>{}, gd, pb); break;
-      case 1: tile_A(IC<2>{}, gd, pb); tile_A(IC<7>{}, gd, pb); break;
+      case 0: tile_A(IC<0>{}, gd, pb); break;
+      case 1: tile_A(IC<2>{}, gd, pb); break;
       case 2: tile_A(IC<5>{}, gd, pb); break;
       case 3: tile_A(IC<9>{}, gd, pb); break;
       case 4: tile_A(IC<1>{}, gd, pb); break;
-      case 5: tile_A(IC<3>{}, gd, pb); break;
-      case 6: tile_A(IC<4>{}, gd, pb); break;
-      default: tile_A(IC<6>{}, gd, pb); break;
+      case 5: tile_A(IC<8>{}, gd, pb); break;
+      default: break;
+    }
+  };
+  // The lower-left 32x32 block (Aba, read by the chain): 4 tiles over
+  // preparation waves 4-7, in a phase in which the chain does not read Aba.
+  auto tiles_Aba = [&](const float* gd, int pb) {
+    switch (pw) {
+      case 4: tile_A(IC<3>{}, gd, pb); break;
+      case 5: tile_A(IC<4>{}, gd, pb); break;
+      case 6: tile_A(IC<6>{}, gd, pb); break;
+      case 7: tile_A(IC<7>{}, gd, pb); break;
+      default: break;
     }
   };
   // Rows [I0, I1) of the diagonal 16x16 blocks of Tm: lane group g inverts
@@ -491,72 +509,51 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       default: break;
     }
   };
-  // 32-row merge of Tm: T_ba = -T_b (A_ba T_a) with 32x32x16 MFMAs
-  // (lane = column l % 32, half h = l / 32).
-  auto merge32 = [&]() {
-    const int col = lane & 31, h = lane >> 5;
-    f32x16 y = f32x16{};
-    const int pcol = p32(col);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      f16x8 fb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) fb[e] = sm.Tm[(16 * s + 8 * h + e) * TLD + pcol];
-      y = mfma32(ld_f32x8_as_f16(&sm.A[(32 + col) * ALD + 16 * s + 8 * h]), fb, y);
-    }
-    f32x16 tba = f32x16{};
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      // k-slots of half h: rows 16 s + {4h..4h+3, 8+4h..8+4h+3} of Y
-      const _Float16* trow = &sm.Tm[(32 + col) * TLD + 32];
-      const f16x4_t lo = *reinterpret_cast<const f16x4_t*>(trow + p32(16 * s + 4 * h));
-      const f16x4_t hi = *reinterpret_cast<const f16x4_t*>(trow + p32(16 * s + 8 + 4 * h));
-      const f16x8 fa = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      tba = mfma32(fa, pack8(y, s), tba);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sm.Tm[(32 + acc_row(i, h)) * TLD + pcol] = (_Float16)(-tba[i]);
-  };
   if (is_chain) {
     // ================= chain waves
     // initial state: Sacc[kb][i] = S[vrow][16 kb + 4 g + i]
     f32x4 Sacc[8];
-    const size_t state_off = (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) Sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (h0 != nullptr) {
+      const float* src = h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
-      for (int kb = 0; kb < 8; ++kb) Sacc[kb] = *reinterpret_cast<const f32x4*>(h0 + state_off + 16 * kb + 4 * g);
+      for (int kb = 0; kb < 8; ++kb) Sacc[kb] = *reinterpret_cast<const f32x4*>(src + 16 * kb + 4 * g);
     }
+    // KS += K[:, 32 p0 .. 32 p0 + 63] S^T[32 p0 .., :] for the chunk whose fp16 K
+    // rows are in Kc[kb_buf] (16 v columns of this wave); columns 0-63 use
+    // state entries k < 64, updated in the first half of the state update.
+    f32x4 KS[4];
+    auto k_times_s_half = [&](int kb_buf, int p0) {
+      asm volatile("" : "+v"(g), "+v"(c));   // lane offsets recomputed here, not kept live
+      const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
+#pragma unroll
+      for (int p = p0; p < p0 + 2; ++p) {
+        const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
+      }
+    };
     if (n_chunks > 0) {           // prologue: the preparation waves build chunk 0
       lds_barrier();
       lds_barrier();
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      k_times_s_half(0, 0);
       lds_barrier();
     }
     for (int ch = 0; ch < n_chunks; ++ch) {
       // Opaque refresh of the lane indices: lane-dependent LDS and HBM offsets
       // are recomputed in every iteration instead of being hoisted out of the
       // loop into registers that would not fit.
-      asm volatile("" : "+v"(g), "+v"(c), "+v"(lane));
+      asm volatile("" : "+v"(g), "+v"(c));
       const int L = chunk_len(ch);
       const int kb_buf = ch & 1;
       const float* gd = gbuf[ch & 1];
       const int vrow = v0 + c;
 
-      // ---- P1: K S^T, X
-      f32x4 KS[4];
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      {
-        const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
-        }
-      }
-      // X = beta (V - e^gam K S^T) in place of KS
+      // ---- P1: rest of K S^T (columns 64-127), X = beta (V - e^gam K S^T) in place of KS
+      k_times_s_half(kb_buf, 2);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         const int t4 = 16 * tb + 4 * g;
@@ -568,65 +565,83 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
       lds_barrier();
 
-      // ---- P2: Vn = Tm X, Vd
+      // ---- P2: Vn = Tm X, Vd; scale e^gam Q S^T
+      asm volatile("" : "+v"(g), "+v"(c));
       f16x8 Vdb[2], Vnb[2];
       {
-        const f16x8 Xb[2] = {pack2(KS[0], KS[1]), pack2(KS[2], KS[3])};
+        // Tm = [[T_a, 0], [-T_b A_ba T_a, T_b]] in 32-row blocks, so
+        // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).
         f32x4 Vn[4];
+        const f16x8 Xtop = pack2(KS[0], KS[1]);
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          Vn[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-          const _Float16* trow = &sm.Tm[(16 * tb + c) * TLD + 8 * g];
-#pragma unroll
-          for (int p = 0; p <= (tb >> 1); ++p) Vn[tb] = mfma16(ld16(trow + 32 * p), Xb[p], Vn[tb]);
-        }
+        for (int tb = 0; tb < 2; ++tb)
+          Vn[tb] = mfma16(ld16(&sm.Tm[(16 * tb + c) * TLD + 8 * g]), Xtop, f32x4{0.f, 0.f, 0.f, 0.f});
         Vnb[0] = pack2(Vn[0], Vn[1]);
+        // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
+        auto decayed = [&](int tb0) {
+          const f32x4 e0 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 4 * g]);
+          const f32x4 e1 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 16 + 4 * g]);
+          return pack2(Vn[tb0] * e0, Vn[tb0 + 1] * e1);
+        };
+        Vdb[0] = decayed(0);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+          const f32x4 y = mfma16(ld16(&sm.Aba[(16 * tb + c) * BLD + 8 * g]), Vnb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int i = 0; i < 4; ++i) KS[2 + tb][i] -= y[i];
+        }
+        const f16x8 Xbot = pack2(KS[2], KS[3]);
+#pragma unroll
+        for (int tb = 2; tb < 4; ++tb)
+          Vn[tb] = mfma16(ld16(&sm.Tm[(16 * tb + c) * TLD + 32 + 8 * g]), Xbot, f32x4{0.f, 0.f, 0.f, 0.f});
         Vnb[1] = pack2(Vn[2], Vn[3]);
+        Vdb[1] = decayed(2);
+      }
+      asm volatile("" ::: "memory");    // Q S^T reads start after Tm X (register pressure)
+      asm volatile("" : "+v"(g), "+v"(c));
+      f32x4 QS[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      {
+        // Element offsets, in a raw Q row t with t % 16 == c, of the two
+        // 4-column pieces lane group g feeds as k-slots 0-3 / 4-7 of the
+        // MFMA over column block p: columns 32 p + 4 g .. +3 and
+        // 32 p + 16 + 4 g .. +3, the order in which two stacked S^T
+        // accumulator tiles give the B operand.
+        const int sw = (g >> 1) ^ c;
+        const uint16_t* qraw = &raw.q[kb_buf][c * D + 4 * (g & 1)];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const bf16x8_t sb = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p) ^ sw)]);
+            const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p + 2) ^ sw)]);
+            // keeps the two reads of one fragment next to each other: paired with
+            // reads of other fragments they would land in registers that need moves
+            asm volatile("" ::: "memory");
+            QS[tb] = mfma16_bf(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), sb, QS[tb]);
+          }
+        }
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-          const f32x4 ed = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb + 4 * g]);
+          const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Vn[tb][i] *= ed[i];
+          for (int i = 0; i < 4; ++i) QS[tb][i] *= egs[i];
         }
-        Vdb[0] = pack2(Vn[0], Vn[1]);
-        Vdb[1] = pack2(Vn[2], Vn[3]);
       }
       const float egL = gd[G_EG + L - 1];
       lds_barrier();
 
       // ---- P3a / P3b: state update, S = e^{gam_L} S + K^T Vd, in two halves of
-      //      k; before it, in P3a, O = scale e^gam Q S^T + P Vn goes to HBM
+      //      k.  Before it, in P3a, O = scale e^gam Q S^T + P Vn goes to HBM;
+      //      after it, in P3b, K S^T of chunk ch+1 over columns 0-63.
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
+        asm volatile("" : "+v"(g), "+v"(c));
         if (half == 0) {
-          f32x4 QS[4];
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-          // Element offsets, in a raw Q row t with t % 16 == c, of the two
-          // 4-column pieces lane group g feeds as k-slots 0-3 / 4-7 of the
-          // MFMA over column block p: columns 32 p + 4 g .. +3 and
-          // 32 p + 16 + 4 g .. +3, the order in which two stacked S^T
-          // accumulator tiles give the B operand.
-          const int sw = (g >> 1) ^ c;
-          const uint16_t* qraw = &raw.q[kb_buf][c * D + 4 * (g & 1)];
-#pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            const bf16x8_t sb = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-              const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p) ^ sw)]);
-              const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p + 2) ^ sw)]);
-              // keeps the two reads of one fragment next to each other: paired with
-              // reads of other fragments they would land in registers that need moves
-              asm volatile("" ::: "memory");
-              QS[tb] = mfma16_bf(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), sb, QS[tb]);
-            }
-          }
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
-            const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) QS[tb][i] *= egs[i];
             const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
 #pragma unroll
             for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
@@ -635,7 +650,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           // column: a uniform row address plus a 32-bit lane offset.
           char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
           const size_t row_bytes = v_stride * sizeof(uint16_t);
-          const uint32_t olane = uint32_t(4 * g) * uint32_t(row_bytes) + uint32_t(vrow) * 2u;
+          const uint32_t olane = uint32_t(4 * g) * uint32_t(row_bytes) + uint32_t(v0 + c) * 2u;
           if (L == C) {
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb)
@@ -666,6 +681,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
             Sacc[kb] = mfma16(fa, Vdb[p], Sacc[kb]);
           }
         }
+        if (half == 1) {    // after the last chunk this reads stale rows and is never used
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          k_times_s_half(kb_buf ^ 1, 0);
+        }
         lds_barrier();
       }
     }
@@ -688,6 +708,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       if (n_chunks > 1) copy_kq(1);   // after gate_compute(0): reloads a and b
       lds_barrier();
       tiles_A(gbuf[0], 0);
+      tiles_Aba(gbuf[0], 0);
       convert_k(0, ptid, kPrepThreads);
       lds_barrier();
       if (pw == 0) {
@@ -702,29 +723,30 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g), "+v"(c), "+v"(ptid));
       const int nb = (ch + 1) & 1;          // parity of chunk ch+1
       const bool more = ch + 1 < n_chunks;
-      // ---- P1: Tm merges of chunk ch (preparation wave 7); K/Q rows, a and b of
+      // ---- P1: 16-row Tm merges of chunk ch (waves 6, 7); K/Q rows, a and b of
       //      chunk ch+1 landed (copied in P3b of ch-1); gate data of ch+1 (wave 0)
-      if (pw == kPrepWaves - 1) {
-        merge16(0);
-        merge16(32);
-        merge32();
-      }
+      if (pw >= kPrepWaves - 2) merge16(32 * (pw - (kPrepWaves - 2)));
       if (more) {
         wait_vm<0>();
         if (pw == 0) gate_compute(ch + 1);
       }
       lds_barrier();
-      // ---- P2: V copy and A tiles of chunk ch+1
+      // ---- P2: V copy and the A tiles of the diagonal 32-row blocks of chunk ch+1
       if (more) {
         copy_v(ch + 1);           // every chain wave has read V of chunk ch
         tiles_A(gbuf[nb], nb);
       }
       lds_barrier();
-      // ---- P3a: rows 0-11 of the Tm diagonal blocks (wave 0) and the fp16 K
-      //      rows (waves 1-7) of chunk ch+1; the chain has read Tm of ch in P2
+      // ---- P3a: rows 0-11 of the Tm diagonal blocks (wave 0), the lower-left A
+      //      tiles and the fp16 K rows (waves 1-7) of chunk ch+1; the chain has
+      //      read Tm and Aba of ch in P2
       if (more) {
-        if (pw == 0) diag_rows(IC<0>{}, IC<12>{}, dx);
-        else convert_k(ch + 1, ptid - 64, kPrepThreads - 64);
+        if (pw == 0) {
+          diag_rows(IC<0>{}, IC<12>{}, dx);
+        } else {
+          tiles_Aba(gbuf[nb], nb);   // the chain read Aba of chunk ch in P2
+          convert_k(ch + 1, ptid - 64, kPrepThreads - 64);
+        }
       }
       lds_barrier();
       // ---- P3b: rows 12-15 of the Tm diagonal blocks (wave 0) and the P tiles
