@@ -524,14 +524,25 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     // rows are in Kc[kb_buf] (16 v columns of this wave); columns 0-63 use
     // state entries k < 64, updated in the first half of the state update.
     f32x4 KS[4];
+    // All 8 K fragments are read before the first product, so that their LDS
+    // latency is paid once.
     auto k_times_s_half = [&](int kb_buf, int p0) {
       asm volatile("" : "+v"(g), "+v"(c));   // lane offsets recomputed here, not kept live
       const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
+      f16x8 kf[2][4];
 #pragma unroll
-      for (int p = p0; p < p0 + 2; ++p) {
-        const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+      for (int p = 0; p < 2; ++p)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) KS[tb] = mfma16(ld16(kbase + 16 * tb * KCLD + 32 * p), sb, KS[tb]);
+        for (int tb = 0; tb < 4; ++tb) kf[p][tb] = ld16(kbase + 16 * tb * KCLD + 32 * (p0 + p));
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const f16x8 sb = pack2(Sacc[2 * (p0 + p)], Sacc[2 * (p0 + p) + 1]);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          asm volatile("" : "+v"(kf[p][tb]));   // products wait here, not between the reads
+          KS[tb] = mfma16(kf[p][tb], sb, KS[tb]);
+        }
       }
     };
     if (n_chunks > 0) {           // prologue: the preparation waves build chunk 0
@@ -553,6 +564,18 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       const int vrow = v0 + c;
 
       // ---- P1: rest of K S^T (columns 64-127), X = beta (V - e^gam K S^T) in place of KS
+      // V[t][vrow] for t = 16 tb + 4 g + i: rows with t % 16 = 4 g + i share
+      // the swizzle, so 4 lane offsets serve the 16 reads.
+      uint16_t vv[4][4];
+      {
+        const uint16_t* vbase = &rawV[(4 * g) * D + (vrow & 7)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint16_t* vrow_i = vbase + i * D + 8 * ((vrow >> 3) ^ (4 * g + i));
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) vv[tb][i] = vrow_i[16 * tb * D];
+        }
+      }
       k_times_s_half(kb_buf, 2);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
@@ -560,8 +583,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + t4]);
         const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + t4]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          KS[tb][i] = bt[i] * (bf16_bits_to_f32(rawV[raw_off(t4 + i, vrow)]) - eg[i] * KS[tb][i]);
+        for (int i = 0; i < 4; ++i) KS[tb][i] = bt[i] * (bf16_bits_to_f32(vv[tb][i]) - eg[i] * KS[tb][i]);
       }
       lds_barrier();
 
@@ -571,11 +593,19 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       {
         // Tm = [[T_a, 0], [-T_b A_ba T_a, T_b]] in 32-row blocks, so
         // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).
+        // the 6 operand tiles are read up front: one LDS latency for the chain
+        f16x8 ta[2], ab[2], tb2[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          ta[j] = ld16(&sm.Tm[(16 * j + c) * TLD + 8 * g]);
+          ab[j] = ld16(&sm.Aba[(16 * j + c) * BLD + 8 * g]);
+          tb2[j] = ld16(&sm.Tm[(16 * (j + 2) + c) * TLD + 32 + 8 * g]);
+        }
+        asm volatile("" ::: "memory");
         f32x4 Vn[4];
         const f16x8 Xtop = pack2(KS[0], KS[1]);
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-          Vn[tb] = mfma16(ld16(&sm.Tm[(16 * tb + c) * TLD + 8 * g]), Xtop, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int tb = 0; tb < 2; ++tb) Vn[tb] = mfma16(ta[tb], Xtop, f32x4{0.f, 0.f, 0.f, 0.f});
         Vnb[0] = pack2(Vn[0], Vn[1]);
         // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
         auto decayed = [&](int tb0) {
@@ -586,14 +616,13 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         Vdb[0] = decayed(0);
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
-          const f32x4 y = mfma16(ld16(&sm.Aba[(16 * tb + c) * BLD + 8 * g]), Vnb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+          const f32x4 y = mfma16(ab[tb], Vnb[0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
           for (int i = 0; i < 4; ++i) KS[2 + tb][i] -= y[i];
         }
         const f16x8 Xbot = pack2(KS[2], KS[3]);
 #pragma unroll
-        for (int tb = 2; tb < 4; ++tb)
-          Vn[tb] = mfma16(ld16(&sm.Tm[(16 * tb + c) * TLD + 32 + 8 * g]), Xbot, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int tb = 2; tb < 4; ++tb) Vn[tb] = mfma16(tb2[tb - 2], Xbot, f32x4{0.f, 0.f, 0.f, 0.f});
         Vnb[1] = pack2(Vn[2], Vn[3]);
         Vdb[1] = decayed(2);
       }
@@ -611,16 +640,27 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         const int sw = (g >> 1) ^ c;
         const uint16_t* qraw = &raw.q[kb_buf][c * D + 4 * (g & 1)];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const bf16x8_t sb = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+        for (int pp = 0; pp < 4; pp += 2) {     // 8 fragments read, then 8 products
+          bf16x8_t qf[2][4];
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) {
-            const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p) ^ sw)]);
-            const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p + 2) ^ sw)]);
-            // keeps the two reads of one fragment next to each other: paired with
-            // reads of other fragments they would land in registers that need moves
-            asm volatile("" ::: "memory");
-            QS[tb] = mfma16_bf(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), sb, QS[tb]);
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+              const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * (pp + p)) ^ sw)]);
+              const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * (pp + p) + 2) ^ sw)]);
+              // keeps the two reads of one fragment next to each other: paired with
+              // reads of other fragments they would land in registers that need moves
+              asm volatile("" ::: "memory");
+              qf[p][tb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const bf16x8_t sb = pack2_bf(Sacc[2 * (pp + p)], Sacc[2 * (pp + p) + 1]);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+              asm volatile("" : "+v"(qf[p][tb]));
+              QS[tb] = mfma16_bf(qf[p][tb], sb, QS[tb]);
+            }
           }
         }
 #pragma unroll
@@ -640,12 +680,19 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       for (int half = 0; half < 2; ++half) {
         asm volatile("" : "+v"(g), "+v"(c));
         if (half == 0) {
+          f16x8 pf[6];              // P tiles (t-block, k-block): 00 10 20 21 30 31
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) {
-            const _Float16* prow = &sm.P[(16 * tb + c) * TLD + 8 * g];
+          for (int tb = 0, j = 0; tb < 4; ++tb)
 #pragma unroll
-            for (int p = 0; p <= (tb >> 1); ++p) QS[tb] = mfma16(ld16(prow + 32 * p), Vnb[p], QS[tb]);
-          }
+            for (int p = 0; p <= (tb >> 1); ++p, ++j) pf[j] = ld16(&sm.P[(16 * tb + c) * TLD + 8 * g + 32 * p]);
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int tb = 0, j = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int p = 0; p <= (tb >> 1); ++p, ++j) {
+              asm volatile("" : "+v"(pf[j]));
+              QS[tb] = mfma16(pf[j], Vnb[p], QS[tb]);
+            }
           // Row t of the chunk's output at obase + t row_bytes + this lane's
           // column: a uniform row address plus a 32-bit lane offset.
           char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
@@ -669,16 +716,28 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           }
         }
 #pragma unroll
-        for (int kb = 4 * half; kb < 4 * half + 4; ++kb) {
-          Sacc[kb] *= egL;
-          const int kq = p32(16 * kb + 4 * (c & 3));    // this lane's quad of columns
+        for (int kb0 = 4 * half; kb0 < 4 * half + 4; kb0 += 2) {   // 4 K^T fragments read, then 4 products
+          f16x8 fa[2][2];
 #pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            const int tr0 = 32 * p + 4 * g + (c >> 2);
-            const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
-            const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
-            const f16x8 fa = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            Sacc[kb] = mfma16(fa, Vdb[p], Sacc[kb]);
+          for (int j = 0; j < 2; ++j) {
+            const int kq = p32(16 * (kb0 + j) + 4 * (c & 3));    // this lane's quad of columns
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const int tr0 = 32 * p + 4 * g + (c >> 2);
+              const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
+              const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
+              fa[j][p] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+          }
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            Sacc[kb0 + j] *= egL;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              asm volatile("" : "+v"(fa[j][p]));
+              Sacc[kb0 + j] = mfma16(fa[j][p], Vdb[p], Sacc[kb0 + j]);
+            }
           }
         }
         if (half == 1) {    // after the last chunk this reads stale rows and is never used
