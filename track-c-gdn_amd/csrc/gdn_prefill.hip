@@ -181,6 +181,21 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
                :: "s"(lds_addr), "v"(src) : "memory");
 }
 
+// Round-to-nearest-even fp32 pair -> packed bf16 pair (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
+
+// The two bf16 halves of a dword to base0 + off and base1 + off: bases uniform
+// (SGPR pairs), off a 32-bit lane offset, so no 64-bit address arithmetic per
+// store.  Nothing in the kernel reads what these stores write.
+__device__ __forceinline__ void store_bf16x2_saddr(const char* base0, const char* base1, uint32_t off,
+                                                   uint32_t two) {
+  asm volatile("global_store_short %0, %1, %2\n\tglobal_store_short_d16_hi %0, %1, %3"
+               :: "v"(off), "v"(two), "s"(base0), "s"(base1) : "memory");
+}
+
 // Tokens [bos, bos + len) of sequence n, clamped into [0, T].
 template <typename CuT>
 __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {
@@ -702,9 +717,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<uint16_t*>(obase + size_t(16 * tb + i) * row_bytes + olane) =
-                    f32_to_bf16_bits(QS[tb][i]);
+              for (int i = 0; i < 4; i += 2)
+                store_bf16x2_saddr(obase + size_t(16 * tb + i) * row_bytes, obase + size_t(16 * tb + i + 1) * row_bytes,
+                                   olane, cvt_pk_bf16(QS[tb][i], QS[tb][i + 1]));
           } else {
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb)
