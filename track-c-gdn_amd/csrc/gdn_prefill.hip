@@ -181,6 +181,15 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
                :: "s"(lds_addr), "v"(src) : "memory");
 }
 
+// The same copy from base + off: base uniform (an SGPR pair), off a 32-bit
+// lane offset (no 64-bit address arithmetic per copy).
+__device__ __forceinline__ void lds_dma16_saddr(const void* base, uint32_t off, void* lds_dst) {
+  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr), "v"(off), "s"(base) : "memory");
+}
+
 // Round-to-nearest-even fp32 pair -> packed bf16 pair (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -301,9 +310,29 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // covers 4 rows: lane l carries row row0 + l/16, swizzle slot l%16 (rows past
   // the chunk end are clamped to its last row).  Preparation wave p copies
   // K/Q/V rows [8p, 8p+8); preparation wave 0 also copies the gate data.
+  // Byte offsets, from a chunk's first row, of the 16 bytes this lane copies
+  // of rows 8 pw + 4 r + lane / 16 (r = 0, 1) of q / k and of v: fixed per
+  // lane, so full chunks copy with a uniform base and no per-copy arithmetic.
+  uint32_t dma_qk[2], dma_v[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = 8 * pw + 4 * r + (lane >> 4);
+    const uint32_t slot = uint32_t((lane & 15) ^ (row & 15)) * 16u;
+    dma_qk[r] = uint32_t(row) * uint32_t(qk_stride * 2) + slot;
+    dma_v[r] = uint32_t(row) * uint32_t(v_stride * 2) + slot;
+  }
   auto copy_kq = [&](int ch) {      // 4 instructions per wave (+2 loads of a, b on preparation wave 0)
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
+    if (L == C) {
+      const uint16_t* kb = k + size_t(t0) * qk_stride + size_t(hq) * D;
+      const uint16_t* qb = q + size_t(t0) * qk_stride + size_t(hq) * D;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        lds_dma16_saddr(kb, dma_qk[r], &raw.k[ch & 1][(8 * pw + 4 * r) * D]);
+        lds_dma16_saddr(qb, dma_qk[r], &raw.q[ch & 1][(8 * pw + 4 * r) * D]);
+      }
+    } else {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int row0 = 8 * pw + 4 * r;
@@ -312,6 +341,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       const size_t off = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_chunk;
       lds_dma16(k + off, &raw.k[ch & 1][row0 * D]);
       lds_dma16(q + off, &raw.q[ch & 1][row0 * D]);
+    }
     }
     if (pw == 0) {                  // a, b of the chunk's tokens for gate_compute
       const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
@@ -322,6 +352,12 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   auto copy_v = [&](int ch) {       // 2 instructions per wave
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
+    if (L == C) {
+      const uint16_t* vb = v + size_t(t0) * v_stride + size_t(hv) * D;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) lds_dma16_saddr(vb, dma_v[r], &rawV[(8 * pw + 4 * r) * D]);
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int row0 = 8 * pw + 4 * r;
