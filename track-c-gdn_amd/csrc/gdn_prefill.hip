@@ -396,28 +396,38 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   };
 
   // ---------------- preparation steps (state-independent)
-  // Raw bf16 rows -> fp16 operand rows [t][p32(k)], rows t >= L -> 0; items
-  // (row, 8-column piece) first, first + step, ... below 1024.
-  auto convert_rows = [&](const uint16_t* src, _Float16* dst, int L, int first, int step) {
-    for (int item = first; item < C * (D / 8); item += step) {
-      const int row = item >> 4;
-      const int cc = (item & 15) * 8;                 // logical columns cc..cc+7
-      uint4 w = *reinterpret_cast<const uint4*>(&src[raw_off(row, cc)]);
+  // Raw bf16 K rows of chunk ch -> fp16 operand rows Kc[ch & 1] [t][p32(k)],
+  // rows t >= L -> 0, by preparation waves 1-7: items (row, 8-column piece)
+  // ptid - 64 + 448 j, j = 0..2, below 1024.  Their LDS offsets are fixed per
+  // lane and computed once; columns cc + 4.. land 8 halves after cc.. (p32).
+  constexpr int kCvThreads = kPrepThreads - 64;
+  uint32_t cv_src[3], cv_dst[3];    // byte offsets into a raw K buffer / a Kc buffer
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int item = (ptid - 64) + kCvThreads * j;
+    const int row = item >> 4, cc = (item & 15) * 8;
+    cv_src[j] = uint32_t(raw_off(row, cc)) * 2u;
+    cv_dst[j] = uint32_t(row * KCLD + p32(cc)) * 2u;
+  }
+  auto convert_k = [&](int ch) {
+    const char* src = reinterpret_cast<const char*>(raw.k[ch & 1]);
+    char* dst = reinterpret_cast<char*>(sm.Kc[ch & 1]);
+    const int L = chunk_len(ch);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      if (j == 2 && (ptid - 64) + kCvThreads * j >= C * (D / 8)) break;   // uniform per wave
+      uint4 w = *reinterpret_cast<const uint4*>(src + cv_src[j]);
       if (L < C) {
-        const uint32_t m = row < L ? 0xffffffffu : 0u;
+        const uint32_t m = ((ptid - 64) + kCvThreads * j) / 16 < L ? 0xffffffffu : 0u;
         w.x &= m; w.y &= m; w.z &= m; w.w &= m;
       }
       float f[8];
       unpack_bf16x2(w.x, f[0], f[1]); unpack_bf16x2(w.y, f[2], f[3]);
       unpack_bf16x2(w.z, f[4], f[5]); unpack_bf16x2(w.w, f[6], f[7]);
-      _Float16* d = &dst[row * KCLD];
-      *reinterpret_cast<f16x4_t*>(d + p32(cc)) = f16x4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
-      *reinterpret_cast<f16x4_t*>(d + p32(cc + 4)) = f16x4_t{(_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
+      _Float16* d = reinterpret_cast<_Float16*>(dst + cv_dst[j]);
+      *reinterpret_cast<f16x4_t*>(d) = f16x4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+      *reinterpret_cast<f16x4_t*>(d + 8) = f16x4_t{(_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
     }
-  };
-  // K rows of chunk ch -> Kc[kb] (all preparation waves).
-  auto convert_k = [&](int ch, int first, int step) {
-    convert_rows(raw.k[ch & 1], sm.Kc[ch & 1], chunk_len(ch), first, step);
   };
   // Per-lane swizzled offsets of the 8-column pieces this lane reads from a
   // raw row r with r % 16 == c: piece 4 ks + g sits in slot (4 ks + g) ^ c.
@@ -819,7 +829,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       lds_barrier();
       tiles_A(gbuf[0], 0);
       tiles_Aba(gbuf[0], 0);
-      convert_k(0, ptid, kPrepThreads);
+      if (pw > 0) convert_k(0);
       lds_barrier();
       if (pw == 0) {
         diag_rows(IC<0>{}, IC<12>{}, dx);
@@ -855,7 +865,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           diag_rows(IC<0>{}, IC<12>{}, dx);
         } else {
           tiles_Aba(gbuf[nb], nb);   // the chain read Aba of chunk ch in P2
-          convert_k(ch + 1, ptid - 64, kPrepThreads - 64);
+          convert_k(ch + 1);
         }
       }
       lds_barrier();
