@@ -435,8 +435,10 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) raw_lane[ks] = c * D + 8 * ((4 * ks + g) ^ c);
   // A tile = tril_strict(beta_i e^{gam_i - gam_j} K K^T) from the raw bf16
-  // rows (bf16 MFMA: the inputs are exact).  Diagonal tiles also store the
-  // transpose of their strict lower part in the (otherwise unused) upper part.
+  // rows (bf16 MFMA: the inputs are exact).  The product is formed transposed
+  // (K_j K_i^T), so that lane (g, c) holds row 16 ti + c, columns 16 tj + 4 g
+  // .. +3 of the tile: 4 adjacent entries, one store.  Diagonal tiles store
+  // zeros above the diagonal.
   auto tile_A = [&](auto tile_c, const float* gd, int pb) {
     constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
     constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
@@ -448,26 +450,28 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fa[ks], fb[ks], acc);
-    const float gc = gd[G_L2 + 16 * tj + c];
-    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * ti + 4 * g]);
-    const f32x4 br = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * ti + 4 * g]);
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
+    const float gr = gd[G_L2 + 16 * ti + c];
+    const float br = gd[G_BETA + 16 * ti + c];
+    const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
+    f32x4 val;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float val = br[i] * __builtin_amdgcn_exp2f(gr[i] - gc) * acc[i];
-      if (ti >= 2 && tj <= 1) {   // lower-left 32x32 block: an MFMA operand of the chain
-        sm.Aba[(16 * (ti - 2) + 4 * g + i) * BLD + p32(16 * tj + c)] = (_Float16)val;
-      } else if (ti != tj) {
-        sm.A[(16 * ti + 4 * g + i) * ALD + 16 * tj + c] = val;
-      } else if (4 * g + i > c) {
-        sm.A[(16 * ti + 4 * g + i) * ALD + 16 * tj + c] = val;
-        sm.A[(16 * ti + c) * ALD + 16 * tj + 4 * g + i] = val;
-      }
+      val[i] = br * __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
+      if (ti == tj) val[i] = (c > 4 * g + i) ? val[i] : 0.f;
+    }
+    if (ti >= 2 && tj <= 1) {     // lower-left 32x32 block: an MFMA operand of the chain
+      *reinterpret_cast<f16x4_t*>(&sm.Aba[(16 * (ti - 2) + c) * BLD + 8 * g + 4 * tj]) =
+          f16x4_t{(_Float16)val[0], (_Float16)val[1], (_Float16)val[2], (_Float16)val[3]};
+    } else {
+      *reinterpret_cast<f32x4*>(&sm.A[(16 * ti + c) * ALD + 16 * tj + 4 * g]) = val;
     }
   };
   // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the raw bf16 rows
-  // (bf16 MFMA: the inputs are exact).  Rows past the chunk end hold copies of
-  // its last row; they only reach output rows that are never stored.
+  // (bf16 MFMA: the inputs are exact), formed transposed like the A tiles:
+  // lane (g, c) holds row 16 ti + c, columns 16 tj + 4 g .. +3, which are 4
+  // adjacent positions of the p32 order.  Rows past the chunk end hold copies
+  // of its last row; they only reach output rows that are never stored.
   auto tile_P = [&](auto tile_c, const float* gd, int pb) {
     constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
     constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
@@ -479,16 +483,17 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fa[ks], fb[ks], acc);
-    const float gc = gd[G_L2 + 16 * tj + c] - scale_l2;
-    const f32x4 gr = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * ti + 4 * g]);
-    const int pcc = p32(16 * tj + c);
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
+    const float gr = gd[G_L2 + 16 * ti + c] + scale_l2;
+    const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
+    f16x4_t val;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float val = __builtin_amdgcn_exp2f(gr[i] - gc) * acc[i];
-      if (ti == tj) val = (4 * g + i >= c) ? val : 0.f;
-      sm.P[(16 * ti + 4 * g + i) * TLD + pcc] = (_Float16)val;
+      float x = __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
+      if (ti == tj) x = (c >= 4 * g + i) ? x : 0.f;
+      val[i] = (_Float16)x;
     }
+    *reinterpret_cast<f16x4_t*>(&sm.P[(16 * ti + c) * TLD + 32 * (tj >> 1) + 8 * g + 4 * (tj & 1)]) = val;
   };
   // A tiles of the chunk of parity pb inside the diagonal 32-row blocks (the
   // inverse's input): 6 tiles over preparation waves 0-5.
