@@ -306,72 +306,62 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     sm.P[R * TLD + pc] = (_Float16)0.f;
   }
 
-  // ---------------- copies into LDS (preparation waves).  An instruction
+  // ---------------- copies into LDS (preparation waves 1-7).  An instruction
   // covers 4 rows: lane l carries row row0 + l/16, swizzle slot l%16 (rows past
-  // the chunk end are clamped to its last row).  Preparation wave p copies
-  // K/Q/V rows [8p, 8p+8); preparation wave 0 also copies the gate data.
+  // the chunk end are clamped to its last row).  Wave p copies K/Q/V rows
+  // [8p, 8p+8), wave 7 also rows [0, 8): 2 instructions per copy (4 on wave 7).
+  // Preparation wave 0 issues no copies, only its loads of a and b, so the
+  // waits the compiler places for those count nothing else.
+  const int n_groups = pw == 0 ? 0 : (pw == kPrepWaves - 1 ? 4 : 2);
+  auto group_row0 = [&](int j) { return j < 2 ? 8 * pw + 4 * j : 4 * (j - 2); };
   // Byte offsets, from a chunk's first row, of the 16 bytes this lane copies
-  // of rows 8 pw + 4 r + lane / 16 (r = 0, 1) of q / k and of v: fixed per
-  // lane, so full chunks copy with a uniform base and no per-copy arithmetic.
-  uint32_t dma_qk[2], dma_v[2];
+  // in group j, for q / k and for v: fixed per lane, so full chunks copy from
+  // a uniform base with no per-copy address arithmetic.
+  uint32_t dma_qk[4], dma_v[4];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = 8 * pw + 4 * r + (lane >> 4);
+  for (int j = 0; j < 4; ++j) {
+    const int row = group_row0(j) + (lane >> 4);
     const uint32_t slot = uint32_t((lane & 15) ^ (row & 15)) * 16u;
-    dma_qk[r] = uint32_t(row) * uint32_t(qk_stride * 2) + slot;
-    dma_v[r] = uint32_t(row) * uint32_t(v_stride * 2) + slot;
+    dma_qk[j] = uint32_t(row) * uint32_t(qk_stride * 2) + slot;
+    dma_v[j] = uint32_t(row) * uint32_t(v_stride * 2) + slot;
   }
-  auto copy_kq = [&](int ch) {      // 4 instructions per wave (+2 loads of a, b on preparation wave 0)
+  auto copy_rows = [&](const uint16_t* src, size_t stride, size_t col0, const uint32_t* offs, int ch,
+                       uint16_t* dst) {
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
     if (L == C) {
-      const uint16_t* kb = k + size_t(t0) * qk_stride + size_t(hq) * D;
-      const uint16_t* qb = q + size_t(t0) * qk_stride + size_t(hq) * D;
+      const uint16_t* base = src + size_t(t0) * stride + col0;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        lds_dma16_saddr(kb, dma_qk[r], &raw.k[ch & 1][(8 * pw + 4 * r) * D]);
-        lds_dma16_saddr(qb, dma_qk[r], &raw.q[ch & 1][(8 * pw + 4 * r) * D]);
-      }
+      for (int j = 0; j < 4; ++j)
+        if (j < n_groups) lds_dma16_saddr(base, offs[j], &dst[group_row0(j) * D]);
     } else {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int row0 = 8 * pw + 4 * r;
-      const int row = row0 + (lane >> 4);
-      const int src_chunk = (lane & 15) ^ (row & 15);
-      const size_t off = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_chunk;
-      lds_dma16(k + off, &raw.k[ch & 1][row0 * D]);
-      lds_dma16(q + off, &raw.q[ch & 1][row0 * D]);
-    }
-    }
-    if (pw == 0) {                  // a, b of the chunk's tokens for gate_compute
-      const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
-      ga = a[gi];
-      gb = b[gi];
+      for (int j = 0; j < 4; ++j) {
+        if (j < n_groups) {
+          const int row0 = group_row0(j);
+          const int row = row0 + (lane >> 4);
+          const int src_chunk = (lane & 15) ^ (row & 15);
+          lds_dma16(src + size_t(t0 + min(row, L - 1)) * stride + col0 + 8 * src_chunk, &dst[row0 * D]);
+        }
+      }
     }
   };
-  auto copy_v = [&](int ch) {       // 2 instructions per wave
-    const int t0 = bos + ch * C;
+  auto copy_kq = [&](int ch) {
+    copy_rows(k, qk_stride, size_t(hq) * D, dma_qk, ch, raw.k[ch & 1]);
+    copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1]);
+  };
+  auto copy_v = [&](int ch) { copy_rows(v, v_stride, size_t(hv) * D, dma_v, ch, rawV); };
+  auto load_ab = [&](int ch) {      // a, b of the chunk's tokens for gate_compute (wave 0)
     const int L = chunk_len(ch);
-    if (L == C) {
-      const uint16_t* vb = v + size_t(t0) * v_stride + size_t(hv) * D;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) lds_dma16_saddr(vb, dma_v[r], &rawV[(8 * pw + 4 * r) * D]);
-      return;
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int row0 = 8 * pw + 4 * r;
-      const int row = row0 + (lane >> 4);
-      const int src_chunk = (lane & 15) ^ (row & 15);
-      lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + 8 * src_chunk,
-                &rawV[row0 * D]);
-    }
+    const size_t gi = size_t(bos + ch * C + min(lane, L - 1)) * HV + hv;
+    ga = a[gi];
+    gb = b[gi];
   };
 
   // Gate data of chunk ch (reference PRE:1706-1722 and the chunk-local cumsum
-  // of PRE:1721) from a / b loaded by copy_kq, into gbuf[ch & 1]: lane =
+  // of PRE:1721) from a / b loaded by load_ab, into gbuf[ch & 1]: lane =
   // token; rows past the sequence end carry a zero log-decay and beta = 0.
-  // Preparation wave 0, after its copies of chunk ch have been waited for.
+  // Preparation wave 0.
   auto gate_compute = [&](int ch) {
     constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
     const int L = chunk_len(ch);
@@ -828,9 +818,13 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     if (n_chunks > 0) {           // prologue: chunk 0 copied and prepared up to its Tm merges
       copy_kq(0);
       copy_v(0);
+      if (pw == 0) load_ab(0);
       wait_vm<0>();
-      if (pw == 0) gate_compute(0);
-      if (n_chunks > 1) copy_kq(1);   // after gate_compute(0): reloads a and b
+      if (pw == 0) {
+        gate_compute(0);
+        if (n_chunks > 1) load_ab(1);
+      }
+      if (n_chunks > 1) copy_kq(1);
       lds_barrier();
       tiles_A(gbuf[0], 0);
       tiles_Aba(gbuf[0], 0);
@@ -848,12 +842,16 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g), "+v"(c), "+v"(ptid));
       const int nb = (ch + 1) & 1;          // parity of chunk ch+1
       const bool more = ch + 1 < n_chunks;
-      // ---- P1: 16-row Tm merges of chunk ch (waves 6, 7); K/Q rows, a and b of
-      //      chunk ch+1 landed (copied in P3b of ch-1); gate data of ch+1 (wave 0)
+      // ---- P1: 16-row Tm merges of chunk ch (waves 6, 7); K/Q rows of chunk
+      //      ch+1 landed (copied in P3b of ch-1); gate data of ch+1 from a and b
+      //      loaded in P1 of ch-1, then the loads of a and b of ch+2 (wave 0)
       if (pw >= kPrepWaves - 2) merge16(32 * (pw - (kPrepWaves - 2)));
       if (more) {
         wait_vm<0>();
-        if (pw == 0) gate_compute(ch + 1);
+        if (pw == 0) {
+          gate_compute(ch + 1);
+          if (ch + 2 < n_chunks) load_ab(ch + 2);
+        }
       }
       lds_barrier();
       // ---- P2: V copy and the A tiles of the diagonal 32-row blocks of chunk ch+1
@@ -877,16 +875,18 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       // ---- P3b: rows 12-15 of the Tm diagonal blocks (wave 0) and the P tiles
       //      (waves 1-7) of chunk ch+1, the chain having read P of ch in P3a;
       //      copies of chunk ch+2 into the raw buffers of ch; V of chunk ch+1
-      //      landed (only those 4 (+2) copies remain)
+      //      landed (only those 4 copies, 8 on wave 7, remain)
       if (more) {
         if (pw == 0) diag_rows(IC<12>{}, IC<16>{}, dx);
         else tiles_P(gbuf[nb], nb);
       }
-      if (ch + 2 < n_chunks) copy_kq(ch + 2);
-      if (ch + 2 < n_chunks) {
-        if (pw == 0) wait_vm<6>(); else wait_vm<4>();
-      } else if (more) {
-        wait_vm<0>();
+      if (pw > 0) {
+        if (ch + 2 < n_chunks) {
+          copy_kq(ch + 2);
+          if (pw == kPrepWaves - 1) wait_vm<8>(); else wait_vm<4>();
+        } else if (more) {
+          wait_vm<0>();
+        }
       }
       lds_barrier();
     }
