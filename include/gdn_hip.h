@@ -52,7 +52,7 @@ const char* gdn_error_string(int code);
  *   new_state  : [B, HV, V, K] fp32 output; may equal `state` (in-place update).
  *   scale      : applied to q; the caller resolves None/0 to 1/sqrt(D)
  *                (kernel.py:112-115).
- * HV must be a multiple of HQ and HV/HQ <= 4.
+ * HV must be a multiple of HQ.
  */
 int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                    const float* state, float* new_state,

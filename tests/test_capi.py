@@ -49,7 +49,8 @@ def test_argument_errors_return_before_launch():
     P = 0x1000  # never dereferenced: the checks fail first
     assert lib.gdn_decode_fwd(None, P, P, P, P, P, P, P, P, P, 1, 4, 8, 1.0, None) == capi.GDN_ERR_NULL
     assert lib.gdn_decode_fwd(P, P, P, P, P, P, P, P, P, P, 1, 4, 6, 1.0, None) == capi.GDN_ERR_SHAPE
-    assert lib.gdn_decode_fwd(P, P, P, P, P, P, P, P, P, P, 1, 2, 16, 1.0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_fwd(P, P, P, P, P, P, P, P, P, P, -1, 4, 8, 1.0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_fwd(P, P, P, P, P, P, P, P, P, P, 1, 0, 8, 1.0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_decode_pool_fwd(P, P, P, P, 4, None, P, P, P, P, P, 1, 4, 8, 1.0, None) == capi.GDN_ERR_NULL
     assert lib.gdn_prefill_fwd(None, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 0, None) == capi.GDN_ERR_NULL
     assert lib.gdn_prefill_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 7, 1.0, P, P, None, 0, None) == capi.GDN_ERR_SHAPE

@@ -9,13 +9,15 @@
 //   o     = scale * S_new q = scale * (S' q + delta (k . q))
 //
 // Mapping (gfx950, wave64):
-//   * one workgroup per (n, qk-head) owns all HV/HQ v-heads that read that
-//     qk-head, so q/k are fetched once; 4 waves per v-head, 32 rows per wave.
+//   * one workgroup of 8 waves per (n, v-head), 16 rows per wave; q/k are
+//     read once per v-head (they are 0.2% of the bytes).
 //   * a DPP row (16 lanes) owns one state row; lane c holds k = 4c..4c+3 and
 //     64+4c..64+4c+3, so each dwordx4 load covers four 256-byte row segments.
-//   * each lane keeps 8 rows (16 x float4 = 256 B) in registers: all loads are
+//   * each lane keeps 4 rows (8 x float4 = 128 B) in registers: all loads are
 //     issued before any arithmetic, the row reductions are 4 DPP adds each,
 //     and the updated row is written straight back (no LDS, no second pass).
+//   * 63 VGPRs, so 8 waves per SIMD stream the state: the same bytes in
+//     flight as 4 waves with 8 rows each, from twice as many waves.
 //   * in-place update (state_in == state_out) is safe: every element is read
 //     and written by the same lane.
 
@@ -27,9 +29,11 @@ namespace {
 using namespace gdn;
 
 constexpr int D = kHeadDim;
-constexpr int kWavesPerHead = 4;
-constexpr int kRowsPerWave = D / kWavesPerHead;   // 32
-constexpr int kRowsPerLane = kRowsPerWave / 4;    // 8 (4 DPP rows per wave)
+constexpr int kWavesPerHead = 8;
+constexpr int kRowsPerWave = D / kWavesPerHead;   // 16
+constexpr int kRowsPerLane = kRowsPerWave / 4;    // 4 (4 DPP rows per wave)
+constexpr int kThreadsPerHead = kWavesPerHead * kWave;
+static_assert(kRowsPerLane == 4, "v is read and o written as 4 bf16 per lane");
 
 template <bool kNonTemporal>
 __device__ __forceinline__ f32x4 load_state(const f32x4* p) {
@@ -54,7 +58,7 @@ __device__ __forceinline__ void load_bf16x8_split(const uint16_t* base, int c, f
 }
 
 template <bool kNonTemporal>
-__global__ __launch_bounds__(1024) void gdn_decode_kernel(
+__global__ __launch_bounds__(kThreadsPerHead, 8) void gdn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* state_in, float* state_out,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
@@ -62,11 +66,11 @@ __global__ __launch_bounds__(1024) void gdn_decode_kernel(
     uint16_t* __restrict__ out, const int32_t* __restrict__ slot_ids,
     int HQ, int HV, int pool_size, float scale) {
   const int ratio = HV / HQ;
-  const int n = blockIdx.x / HQ;
-  const int hq = blockIdx.x - n * HQ;
+  const int n = blockIdx.x / HV;
+  const int hv = blockIdx.x - n * HV;
+  const int hq = hv / ratio;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int hv = hq * ratio + wave / kWavesPerHead;
   const int row0 = (wave % kWavesPerHead) * kRowsPerWave;
   const int rsub = lane >> 4;     // DPP row within the wave
   const int c = lane & 15;        // lane within the DPP row
@@ -80,7 +84,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_kernel(
     slot = slot_ids[n];
     if (slot < 0 || slot >= pool_size) {
       // Unmapped sequence: no state access, zero output.
-      if (c == 0) *reinterpret_cast<uint4*>(o_ptr) = make_uint4(0, 0, 0, 0);
+      if (c == 0) *reinterpret_cast<uint2*>(o_ptr) = make_uint2(0, 0);
       return;
     }
   }
@@ -107,13 +111,11 @@ __global__ __launch_bounds__(1024) void gdn_decode_kernel(
   float kk[8], qq[8];
   load_bf16x8_split(k + qk_off, c, kk);
   load_bf16x8_split(q + qk_off, c, qq);
-  float vv[8];
+  float vv[kRowsPerLane];
   {
-    const uint4 vw = *reinterpret_cast<const uint4*>(v + nh * D + rbase);
+    const uint2 vw = *reinterpret_cast<const uint2*>(v + nh * D + rbase);
     unpack_bf16x2(vw.x, vv[0], vv[1]);
     unpack_bf16x2(vw.y, vv[2], vv[3]);
-    unpack_bf16x2(vw.z, vv[4], vv[5]);
-    unpack_bf16x2(vw.w, vv[6], vv[7]);
   }
 
   // Gates (reference DEC:59-65), uniform per wave.
@@ -152,12 +154,10 @@ __global__ __launch_bounds__(1024) void gdn_decode_kernel(
                               f32x4{x[4], x[5], x[6], x[7]});
   }
   if (c == 0) {
-    uint4 w;
+    uint2 w;
     w.x = pack_bf16x2(o_out[0], o_out[1]);
     w.y = pack_bf16x2(o_out[2], o_out[3]);
-    w.z = pack_bf16x2(o_out[4], o_out[5]);
-    w.w = pack_bf16x2(o_out[6], o_out[7]);
-    *reinterpret_cast<uint4*>(o_ptr) = w;
+    *reinterpret_cast<uint2*>(o_ptr) = w;
   }
 }
 
@@ -166,7 +166,6 @@ int check_decode_args(const void* q, const void* k, const void* v, const void* s
                       const void* out, int B, int HQ, int HV) {
   if (!q || !k || !v || !state_out || !A_log || !a || !dt_bias || !b || !out) return GDN_ERR_NULL;
   if (B < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return GDN_ERR_SHAPE;
-  if ((HV / HQ) * kWavesPerHead * kWave > 1024) return GDN_ERR_SHAPE;
   return GDN_OK;
 }
 
@@ -175,8 +174,8 @@ int launch_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
                   const uint16_t* b, uint16_t* out, const int32_t* slot_ids, int B, int HQ, int HV,
                   int pool_size, float scale, void* stream) {
   if (B == 0) return GDN_OK;
-  const dim3 grid(unsigned(B) * unsigned(HQ));
-  const dim3 block(unsigned(HV / HQ) * kWavesPerHead * kWave);
+  const dim3 grid(unsigned(B) * unsigned(HV));
+  const dim3 block(kThreadsPerHead);
   hipLaunchKernelGGL(gdn_decode_kernel<true>, grid, block, 0, static_cast<hipStream_t>(stream),
                      q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, slot_ids, HQ, HV,
                      pool_size, scale);

@@ -45,7 +45,7 @@ def _check_common(q, k, v, A_log, a, dt_bias, b):
     assert k.shape == q.shape
     assert v.dim() == 4 and v.shape[0] == B and v.shape[1] == 1 and v.shape[3] == D
     nv = v.shape[2]
-    assert nv % nq == 0 and nv // nq <= 4, "v-heads must be a multiple (<=4x) of qk-heads"
+    assert nv % nq == 0, "v-heads must be a multiple of qk-heads"
     assert A_log.numel() == nv and dt_bias.numel() == nv
     assert a.numel() == B * nv and b.numel() == B * nv
     return B, nq, nv
