@@ -523,15 +523,20 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     for (int i = I0; i < I1; ++i) {
       // bound the live A rows: loads of rows 4b.. are not hoisted above row 4b
       if ((i & 3) == 0) asm volatile("" ::: "memory");
-      float sum = (i == cid) ? 1.f : 0.f;
+      // two partial sums (alternate 4-column blocks) halve the dependent chain
+      float s0 = (i == cid) ? 1.f : 0.f, s1 = 0.f;
 #pragma unroll
       for (int j4 = 0; j4 < i; j4 += 4) {
         const f32x4 arow = *reinterpret_cast<const f32x4*>(&Ab[i * ALD + j4]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (j4 + e < i) sum = fmaf(-arow[e], x[j4 + e], sum);
+        for (int e = 0; e < 4; ++e) {
+          if (j4 + e < i) {
+            if ((j4 >> 2) & 1) s1 = fmaf(-arow[e], x[j4 + e], s1);
+            else s0 = fmaf(-arow[e], x[j4 + e], s0);
+          }
+        }
       }
-      x[i] = sum;
+      x[i] = i > 4 ? s0 + s1 : s0;
     }
     const int pc = p32(16 * g + c);
 #pragma unroll
