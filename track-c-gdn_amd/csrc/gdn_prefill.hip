@@ -55,12 +55,12 @@ constexpr int BLD = C / 2 + 8;  // Aba row stride (halves): 80 B rows
 // (gam = chunk-local cumsum of the log-decay, gam_L its value at the chunk's last token).
 constexpr int G_L2 = 0, G_BETA = C, G_EG = 2 * C, G_EGS = 3 * C, G_ED = 4 * C;
 constexpr int GSZ = 5 * C;
-constexpr int kChainWaves = 8;              // state-chain waves, 16 state rows each
-constexpr int kPrepWaves = 8;               // preparation / copy waves
+constexpr int kChainWaves = 4;              // state-chain waves, one per SIMD, 32 state rows each
+constexpr int kPrepWaves = 4;               // preparation / copy waves, one per SIMD
 constexpr int kWaves = kChainWaves + kPrepWaves;
 constexpr int kThreads = kWaves * 64;
 constexpr int kPrepThreads = kPrepWaves * 64;
-constexpr int kRowsPerWave = D / kChainWaves;   // 16 state rows (v) per chain wave
+constexpr int kRowsPerWave = D / kChainWaves;   // 32 state rows (v) per chain wave: two 16-column tiles
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -99,6 +99,17 @@ struct __align__(16) Smem {
 // statement is a compiler memory barrier as well.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroup barrier that leaves up to N of this wave's most recent LDS reads
+// in flight.  For a wave that reads LDS and never writes it: every read whose
+// value it has used before the barrier has completed, and what may still be
+// outstanding are reads whose values are used after it -- reads of data that
+// no wave overwrites in the next phase.
+template <int N>
+__device__ __forceinline__ void lds_barrier_keep() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" :: "n"(N) : "memory");
 }
 
 // Waits until at most N vector-memory operations of this wave are outstanding.
@@ -224,30 +235,34 @@ struct Tile16 {
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-// The state chain.  One workgroup of 16 waves per (sequence, v-head): waves
-// 0-7 run the chain (wave w owns state rows v in [16w, 16w+16), all of its
-// products are 16x16x32 MFMAs) and store the outputs; waves 8-15 prepare
-// chunks and issue every copy into LDS; each SIMD hosts two waves of each
-// kind.  In iteration i the chain works on chunk i while the preparation
-// waves build chunk i+1, in four phases separated by LDS barriers:
-//   P1   chain : K S^T (columns 64-127), X  prep : 16-row merges of Tm_i (waves 14, 15);
-//                                                  gate data of chunk i+1 (wave 8)
+// The state chain.  One workgroup of 8 waves per (sequence, v-head), two on
+// each SIMD: waves 0-3 run the chain (wave w owns state rows v in
+// [32w, 32w+32), two 16-row column tiles; all of its products are 16x16x32
+// MFMAs) and store the outputs; waves 4-7 (preparation waves 0-3) prepare
+// chunks and issue every copy into LDS.  In iteration i the chain works on
+// chunk i while the preparation waves build chunk i+1, in four phases
+// separated by LDS barriers:
+//   P1   chain : K S^T (columns 64-127), X  prep : 16-row merges of Tm_i (prep waves 2, 3);
+//                                                  rest of P_i; gate data of chunk i+1
+//                                                  (prep wave 0)
 //   P2   chain : Vn = Tm X, Vd,             prep : copy of V_{i+1}; A_{i+1} tiles of
 //                scale e^gam Q S^T                 the diagonal 32-row blocks
 //   P3a  chain : O = scale e^gam Q S^T      prep : rows 0-11 of the Tm_{i+1} diagonal
-//                + P Vn -> HBM; S update,          blocks (wave 8); lower-left A_{i+1}
-//                first half of k                   tiles; fp16 K_{i+1}
-//   P3b  chain : S update, second half;     prep : rows 12-15 of those blocks (wave 8);
-//                K S^T of chunk i+1                P_{i+1} tiles; copies of K/Q of
-//                (columns 0-63)                    chunk i+2, a/b for its gates
+//                + P Vn -> HBM; S update,          blocks (prep wave 0); lower-left
+//                first half of k                   A_{i+1} tiles; fp16 K_{i+1}
+//   P3b  chain : S update, second half;     prep : rows 12-15 of those blocks (prep
+//                K S^T of chunk i+1                wave 0); P_{i+1} tiles; copies of
+//                (columns 0-63)                    K/Q of chunk i+2
 // The 32-row merge of Tm is left to the chain: Vn = Tm X is applied as
 // Vn_top = T_a X_top, Vn_bot = T_b (X_bot - A_ba Vn_top).
 // Raw K and Q rows are double-buffered by chunk parity, so the chain reads the
 // Q rows of chunk i while the P tiles of chunk i+1 read the next ones.  The S
 // update reads K^T through transposing LDS reads.  Copies are issued one
 // phase or more before their first use and waited for with explicit vmcnt
-// counts by the waves that issued them.  Which wave computes which tile is
-// fixed at compile time, so tile offsets are immediates.
+// counts by the waves that issued them.  The chain reads the operands of a
+// phase at the end of the phase before whenever no wave overwrites them in
+// between, and its barriers leave those reads in flight.  Which wave computes
+// which tile is fixed at compile time, so tile offsets are immediates.
 template <typename CuT>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -306,20 +321,22 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     sm.P[R * TLD + pc] = (_Float16)0.f;
   }
 
-  // ---------------- copies into LDS (preparation waves 1-7).  An instruction
+  // ---------------- copies into LDS (preparation waves 1-3).  An instruction
   // covers 4 rows: lane l carries row row0 + l/16, swizzle slot l%16 (rows past
-  // the chunk end are clamped to its last row).  Wave p copies K/Q/V rows
-  // [8p, 8p+8), wave 7 also rows [0, 8): 2 instructions per copy (4 on wave 7).
+  // the chunk end are clamped to its last row).  The 16 groups of 4 rows go
+  // 6 / 5 / 5 to waves 1 / 2 / 3, one instruction per group and copy.
   // Preparation wave 0 issues no copies, only its loads of a and b, so the
   // waits the compiler places for those count nothing else.
-  const int n_groups = pw == 0 ? 0 : (pw == kPrepWaves - 1 ? 4 : 2);
-  auto group_row0 = [&](int j) { return j < 2 ? 8 * pw + 4 * j : 4 * (j - 2); };
+  constexpr int kMaxGroups = 6;
+  const int n_groups = pw == 0 ? 0 : (pw == 1 ? 6 : 5);
+  const int group0 = pw == 1 ? 0 : (pw == 2 ? 6 : 11);
+  auto group_row0 = [&](int j) { return 4 * (group0 + j); };
   // Byte offsets, from a chunk's first row, of the 16 bytes this lane copies
   // in group j, for q / k and for v: fixed per lane, so full chunks copy from
   // a uniform base with no per-copy address arithmetic.
-  uint32_t dma_qk[4], dma_v[4];
+  uint32_t dma_qk[kMaxGroups], dma_v[kMaxGroups];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kMaxGroups; ++j) {
     const int row = group_row0(j) + (lane >> 4);
     const uint32_t slot = uint32_t((lane & 15) ^ (row & 15)) * 16u;
     dma_qk[j] = uint32_t(row) * uint32_t(qk_stride * 2) + slot;
@@ -332,11 +349,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     if (L == C) {
       const uint16_t* base = src + size_t(t0) * stride + col0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < kMaxGroups; ++j)
         if (j < n_groups) lds_dma16_saddr(base, offs[j], &dst[group_row0(j) * D]);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kMaxGroups; ++j) {
         if (j < n_groups) {
           const int row0 = group_row0(j);
           const int row = row0 + (lane >> 4);
@@ -387,13 +404,14 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 
   // ---------------- preparation steps (state-independent)
   // Raw bf16 K rows of chunk ch -> fp16 operand rows Kc[ch & 1] [t][p32(k)],
-  // rows t >= L -> 0, by preparation waves 1-7: items (row, 8-column piece)
-  // ptid - 64 + 448 j, j = 0..2, below 1024.  Their LDS offsets are fixed per
+  // rows t >= L -> 0, by preparation waves 1-3: items (row, 8-column piece)
+  // ptid - 64 + 192 j, j = 0..5, below 1024.  Their LDS offsets are fixed per
   // lane and computed once; columns cc + 4.. land 8 halves after cc.. (p32).
   constexpr int kCvThreads = kPrepThreads - 64;
-  uint32_t cv_src[3], cv_dst[3];    // byte offsets into a raw K buffer / a Kc buffer
+  constexpr int kCvItems = (C * (D / 8) + kCvThreads - 1) / kCvThreads;   // 6
+  uint32_t cv_src[kCvItems], cv_dst[kCvItems];    // byte offsets into a raw K buffer / a Kc buffer
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
+  for (int j = 0; j < kCvItems; ++j) {
     const int item = (ptid - 64) + kCvThreads * j;
     const int row = item >> 4, cc = (item & 15) * 8;
     cv_src[j] = uint32_t(raw_off(row, cc)) * 2u;
@@ -404,8 +422,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     char* dst = reinterpret_cast<char*>(sm.Kc[ch & 1]);
     const int L = chunk_len(ch);
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      if (j == 2 && (ptid - 64) + kCvThreads * j >= C * (D / 8)) break;   // uniform per wave
+    for (int j = 0; j < kCvItems; ++j) {
+      if (j == kCvItems - 1 && (ptid - 64) + kCvThreads * j >= C * (D / 8)) break;   // uniform per wave
       uint4 w = *reinterpret_cast<const uint4*>(src + cv_src[j]);
       if (L < C) {
         const uint32_t m = ((ptid - 64) + kCvThreads * j) / 16 < L ? 0xffffffffu : 0u;
@@ -486,26 +504,22 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     *reinterpret_cast<f16x4_t*>(&sm.P[(16 * ti + c) * TLD + 32 * (tj >> 1) + 8 * g + 4 * (tj & 1)]) = val;
   };
   // A tiles of the chunk of parity pb inside the diagonal 32-row blocks (the
-  // inverse's input): 6 tiles over preparation waves 0-5.
+  // inverse's input): 6 tiles over the 4 preparation waves.
   auto tiles_A = [&](const float* gd, int pb) {
     switch (pw) {
-      case 0: tile_A(IC<0>{}, gd, pb); break;
-      case 1: tile_A(IC<2>{}, gd, pb); break;
-      case 2: tile_A(IC<5>{}, gd, pb); break;
-      case 3: tile_A(IC<9>{}, gd, pb); break;
-      case 4: tile_A(IC<1>{}, gd, pb); break;
-      case 5: tile_A(IC<8>{}, gd, pb); break;
-      default: break;
+      case 0: tile_A(IC<0>{}, gd, pb); tile_A(IC<2>{}, gd, pb); break;
+      case 1: tile_A(IC<5>{}, gd, pb); tile_A(IC<9>{}, gd, pb); break;
+      case 2: tile_A(IC<1>{}, gd, pb); break;
+      default: tile_A(IC<8>{}, gd, pb); break;
     }
   };
   // The lower-left 32x32 block (Aba, read by the chain): 4 tiles over
-  // preparation waves 4-7, in a phase in which the chain does not read Aba.
+  // preparation waves 1-3, in a phase in which the chain does not read Aba.
   auto tiles_Aba = [&](const float* gd, int pb) {
     switch (pw) {
-      case 4: tile_A(IC<3>{}, gd, pb); break;
-      case 5: tile_A(IC<4>{}, gd, pb); break;
-      case 6: tile_A(IC<6>{}, gd, pb); break;
-      case 7: tile_A(IC<7>{}, gd, pb); break;
+      case 1: tile_A(IC<3>{}, gd, pb); tile_A(IC<4>{}, gd, pb); break;
+      case 2: tile_A(IC<6>{}, gd, pb); break;
+      case 3: tile_A(IC<7>{}, gd, pb); break;
       default: break;
     }
   };
@@ -557,142 +571,134 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) sm.Tm[(a0 + 16 + 4 * g + i) * TLD + pcb] = (_Float16)(-t21[i]);
   };
-  // P tiles of the chunk of parity pb: 10 tiles over preparation waves 1-7.
-  auto tiles_P = [&](const float* gd, int pb) {
+  // P tiles of the chunk of parity pb over preparation waves 1-3, in two
+  // parts: 6 tiles after the chain's last read of the previous P (P3b of the
+  // previous iteration), 4 in P1 of the chunk's own iteration.
+  auto tiles_P1 = [&](const float* gd, int pb) {
     switch (pw) {
       case 1: tile_P(IC<0>{}, gd, pb); tile_P(IC<8>{}, gd, pb); break;
       case 2: tile_P(IC<2>{}, gd, pb); tile_P(IC<7>{}, gd, pb); break;
       case 3: tile_P(IC<5>{}, gd, pb); tile_P(IC<6>{}, gd, pb); break;
-      case 4: tile_P(IC<9>{}, gd, pb); break;
-      case 5: tile_P(IC<1>{}, gd, pb); break;
-      case 6: tile_P(IC<3>{}, gd, pb); break;
-      case 7: tile_P(IC<4>{}, gd, pb); break;
+      default: break;
+    }
+  };
+  auto tiles_P2 = [&](const float* gd, int pb) {
+    switch (pw) {
+      case 1: tile_P(IC<9>{}, gd, pb); tile_P(IC<1>{}, gd, pb); break;
+      case 2: tile_P(IC<3>{}, gd, pb); break;
+      case 3: tile_P(IC<4>{}, gd, pb); break;
       default: break;
     }
   };
   if (is_chain) {
     // ================= chain waves
-    // initial state: Sacc[kb][i] = S[vrow][16 kb + 4 g + i]
-    f32x4 Sacc[8];
+    // Column tile u (0, 1) of this wave holds state rows v = v0 + 16 u + c.
+    // initial state: Sacc[u][kb][i] = S[v0 + 16 u + c][16 kb + 4 g + i]
+    f32x4 Sacc[2][8];
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) Sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) Sacc[u][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (h0 != nullptr) {
       const float* src = h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
-      for (int kb = 0; kb < 8; ++kb) Sacc[kb] = *reinterpret_cast<const f32x4*>(src + 16 * kb + 4 * g);
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+          Sacc[u][kb] = *reinterpret_cast<const f32x4*>(src + size_t(16 * u) * D + 16 * kb + 4 * g);
     }
-    // KS += K[:, 32 p0 .. 32 p0 + 63] S^T[32 p0 .., :] for the chunk whose fp16 K
-    // rows are in Kc[kb_buf] (16 v columns of this wave); columns 0-63 use
-    // state entries k < 64, updated in the first half of the state update.
-    f32x4 KS[4];
-    // All 8 K fragments are read before the first product, so that their LDS
-    // latency is paid once.
-    auto k_times_s_half = [&](int kb_buf, int p0) {
-      asm volatile("" : "+v"(g), "+v"(c));   // lane offsets recomputed here, not kept live
+    // KS[u] += K[:, 32 p0 .. 32 p0 + 63] S^T[32 p0 .., tile u] for the chunk whose
+    // fp16 K rows are in Kc[kb_buf]; columns 0-63 use state entries k < 64,
+    // updated in the first half of the state update.  The 8 K fragments are
+    // read before the first product and serve both column tiles.
+    f32x4 KS[2][4];
+    // K fragments of column blocks p0, p0 + 1 of Kc[kb_buf]: issued ahead of
+    // their products (LDS reads wait behind the other waves' traffic).
+    typedef f16x8 KFrag[2][4];
+    auto load_kf = [&](int kb_buf, int p0, KFrag& kf) {
       const _Float16* kbase = &sm.Kc[kb_buf][c * KCLD + 8 * g];
-      f16x8 kf[2][4];
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) kf[p][tb] = ld16(kbase + 16 * tb * KCLD + 32 * (p0 + p));
-      asm volatile("" ::: "memory");
+    };
+    auto mul_kf = [&](int p0, KFrag& kf) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const f16x8 sb = pack2(Sacc[2 * (p0 + p)], Sacc[2 * (p0 + p) + 1]);
+        const f16x8 sb0 = pack2(Sacc[0][2 * (p0 + p)], Sacc[0][2 * (p0 + p) + 1]);
+        const f16x8 sb1 = pack2(Sacc[1][2 * (p0 + p)], Sacc[1][2 * (p0 + p) + 1]);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
           asm volatile("" : "+v"(kf[p][tb]));   // products wait here, not between the reads
-          KS[tb] = mfma16(kf[p][tb], sb, KS[tb]);
+          KS[0][tb] = mfma16(kf[p][tb], sb0, KS[0][tb]);
+          KS[1][tb] = mfma16(kf[p][tb], sb1, KS[1][tb]);
         }
       }
+    };
+    KFrag kf_lo, kf_hi;     // columns 0-63 / 64-127 of the next chunk's K
+    auto zero_ks = [&]() {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) KS[u][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
     if (n_chunks > 0) {           // prologue: the preparation waves build chunk 0
       lds_barrier();
       lds_barrier();
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      k_times_s_half(0, 0);
+      zero_ks();
+      load_kf(0, 0, kf_lo);
+      load_kf(0, 2, kf_hi);
+      asm volatile("" ::: "memory");
+      mul_kf(0, kf_lo);
       lds_barrier();
     }
     for (int ch = 0; ch < n_chunks; ++ch) {
-      // Opaque refresh of the lane indices: lane-dependent LDS and HBM offsets
-      // are recomputed in every iteration instead of being hoisted out of the
-      // loop into registers that would not fit.
-      asm volatile("" : "+v"(g), "+v"(c));
       const int L = chunk_len(ch);
       const int kb_buf = ch & 1;
       const float* gd = gbuf[ch & 1];
-      const int vrow = v0 + c;
 
-      // ---- P1: rest of K S^T (columns 64-127), X = beta (V - e^gam K S^T) in place of KS
-      // V[t][vrow] for t = 16 tb + 4 g + i: rows with t % 16 = 4 g + i share
-      // the swizzle, so 4 lane offsets serve the 16 reads.
-      uint16_t vv[4][4];
+      // ---- P1: rest of K S^T (columns 64-127), X = beta (V - e^gam K S^T) in place of KS.
+      //      V and gate reads go first (independent of K S^T); at the end, the
+      //      A_ba tiles and the Q fragments of column block 0 are read for P2.
       {
-        const uint16_t* vbase = &rawV[(4 * g) * D + (vrow & 7)];
+        // V[t][v0 + 16 u + c] for t = 16 tb + 4 g + i: rows with t % 16 = 4 g + i
+        // share the swizzle, so 4 lane offsets serve the reads of a tile.
+        uint16_t vv[2][4][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint16_t* vrow_i = vbase + i * D + 8 * ((vrow >> 3) ^ (4 * g + i));
+        for (int u = 0; u < 2; ++u) {
+          const int col = v0 + 16 * u + c;
+          const uint16_t* vbase = &rawV[(4 * g) * D + (col & 7)];
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) vv[tb][i] = vrow_i[16 * tb * D];
+          for (int i = 0; i < 4; ++i) {
+            const uint16_t* vrow_i = vbase + i * D + 8 * ((col >> 3) ^ (4 * g + i));
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) vv[u][tb][i] = vrow_i[16 * tb * D];
+          }
         }
-      }
-      k_times_s_half(kb_buf, 2);
+        f32x4 eg[4], bt[4];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const int t4 = 16 * tb + 4 * g;
-        const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + t4]);
-        const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + t4]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) KS[tb][i] = bt[i] * (bf16_bits_to_f32(vv[tb][i]) - eg[i] * KS[tb][i]);
-      }
-      lds_barrier();
-
-      // ---- P2: Vn = Tm X, Vd; scale e^gam Q S^T
-      asm volatile("" : "+v"(g), "+v"(c));
-      f16x8 Vdb[2], Vnb[2];
-      {
-        // Tm = [[T_a, 0], [-T_b A_ba T_a, T_b]] in 32-row blocks, so
-        // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).
-        // the 6 operand tiles are read up front: one LDS latency for the chain
-        f16x8 ta[2], ab[2], tb2[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          ta[j] = ld16(&sm.Tm[(16 * j + c) * TLD + 8 * g]);
-          ab[j] = ld16(&sm.Aba[(16 * j + c) * BLD + 8 * g]);
-          tb2[j] = ld16(&sm.Tm[(16 * (j + 2) + c) * TLD + 32 + 8 * g]);
+        for (int tb = 0; tb < 4; ++tb) {
+          eg[tb] = *reinterpret_cast<const f32x4*>(&gd[G_EG + 16 * tb + 4 * g]);
+          bt[tb] = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * tb + 4 * g]);
         }
         asm volatile("" ::: "memory");
-        f32x4 Vn[4];
-        const f16x8 Xtop = pack2(KS[0], KS[1]);
+        mul_kf(2, kf_hi);       // read in P3b of the previous chunk (or the prologue)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) Vn[tb] = mfma16(ta[tb], Xtop, f32x4{0.f, 0.f, 0.f, 0.f});
-        Vnb[0] = pack2(Vn[0], Vn[1]);
-        // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
-        auto decayed = [&](int tb0) {
-          const f32x4 e0 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 4 * g]);
-          const f32x4 e1 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 16 + 4 * g]);
-          return pack2(Vn[tb0] * e0, Vn[tb0 + 1] * e1);
-        };
-        Vdb[0] = decayed(0);
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-          const f32x4 y = mfma16(ab[tb], Vnb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+          for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) KS[2 + tb][i] -= y[i];
-        }
-        const f16x8 Xbot = pack2(KS[2], KS[3]);
+            for (int i = 0; i < 4; ++i)
+              KS[u][tb][i] = bt[tb][i] * (bf16_bits_to_f32(vv[u][tb][i]) - eg[tb][i] * KS[u][tb][i]);
+        // X is formed here, so the V rows (overwritten in P2) have been read
 #pragma unroll
-        for (int tb = 2; tb < 4; ++tb) Vn[tb] = mfma16(tb2[tb - 2], Xbot, f32x4{0.f, 0.f, 0.f, 0.f});
-        Vnb[1] = pack2(Vn[2], Vn[3]);
-        Vdb[1] = decayed(2);
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(KS[u][tb]));
       }
-      asm volatile("" ::: "memory");    // Q S^T reads start after Tm X (register pressure)
-      asm volatile("" : "+v"(g), "+v"(c));
-      f32x4 QS[4];
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) QS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      {
+      f16x8 ab[2];
+      bf16x8_t qf[2][4];      // Q fragments of column blocks p, p + 1 (double-buffered)
+      auto load_qf = [&](int p, bf16x8_t(&dst)[4]) {
         // Element offsets, in a raw Q row t with t % 16 == c, of the two
         // 4-column pieces lane group g feeds as k-slots 0-3 / 4-7 of the
         // MFMA over column block p: columns 32 p + 4 g .. +3 and
@@ -701,118 +707,205 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         const int sw = (g >> 1) ^ c;
         const uint16_t* qraw = &raw.q[kb_buf][c * D + 4 * (g & 1)];
 #pragma unroll
-        for (int pp = 0; pp < 4; pp += 2) {     // 8 fragments read, then 8 products
-          bf16x8_t qf[2][4];
+        for (int tb = 0; tb < 4; ++tb) {
+          const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p) ^ sw)]);
+          const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * p + 2) ^ sw)]);
+          // keeps the two reads of one fragment next to each other: paired with
+          // reads of other fragments they would land in registers that need moves
+          asm volatile("" ::: "memory");
+          dst[tb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      };
+      {
 #pragma unroll
-          for (int p = 0; p < 2; ++p)
+        for (int j = 0; j < 2; ++j) ab[j] = ld16(&sm.Aba[(16 * j + c) * BLD + 8 * g]);
+        load_qf(0, qf[0]);
+      }
+      lds_barrier_keep<15>();   // A_ba and Q stay untouched in P2
+
+      // ---- P2: Vn = Tm X, Vd; scale e^gam Q S^T
+      f16x8 Vdb[2][2], Vnb[2][2];
+      {
+        // Tm = [[T_a, 0], [-T_b A_ba T_a, T_b]] in 32-row blocks, so
+        // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).  The 6
+        // operand tiles are read up front and serve both column tiles.
+        f16x8 ta[2], tb2[2];
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-              const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * (pp + p)) ^ sw)]);
-              const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qraw[16 * tb * D + 8 * ((4 * (pp + p) + 2) ^ sw)]);
-              // keeps the two reads of one fragment next to each other: paired with
-              // reads of other fragments they would land in registers that need moves
-              asm volatile("" ::: "memory");
-              qf[p][tb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
+        for (int j = 0; j < 2; ++j) {
+          ta[j] = ld16(&sm.Tm[(16 * j + c) * TLD + 8 * g]);
+          tb2[j] = ld16(&sm.Tm[(16 * (j + 2) + c) * TLD + 32 + 8 * g]);
+        }
+        asm volatile("" ::: "memory");
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          f32x4 Vn[4];
+          const f16x8 Xtop = pack2(KS[u][0], KS[u][1]);
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) Vn[tb] = mfma16(ta[tb], Xtop, z);
+          Vnb[u][0] = pack2(Vn[0], Vn[1]);
+          // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
+          auto decayed = [&](int tb0) {
+            const f32x4 e0 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 4 * g]);
+            const f32x4 e1 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 16 + 4 * g]);
+            return pack2(Vn[tb0] * e0, Vn[tb0 + 1] * e1);
+          };
+          Vdb[u][0] = decayed(0);
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) {
+            const f32x4 y = mfma16(ab[tb], Vnb[u][0], z);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) KS[u][2 + tb][i] -= y[i];
+          }
+          const f16x8 Xbot = pack2(KS[u][2], KS[u][3]);
+#pragma unroll
+          for (int tb = 2; tb < 4; ++tb) Vn[tb] = mfma16(tb2[tb - 2], Xbot, z);
+          Vnb[u][1] = pack2(Vn[2], Vn[3]);
+          Vdb[u][1] = decayed(2);
+        }
+        // Tm and A_ba (overwritten in P3a) have been read once Vn and Vd exist
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(Vnb[u][j]), "+v"(Vdb[u][j]));
+      }
+      asm volatile("" ::: "memory");    // Q S^T reads start after Tm X (register pressure)
+      f32x4 QS[2][4];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) QS[u][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      f16x8 pf[6];              // P tiles (t-block, k-block): 00 10 20 21 30 31, read for P3a
+      f16x8 fa[2][2];           // K^T fragments of k-blocks 0, 1, read for P3a
+      auto load_fa = [&](int kb0, f16x8(&dst)[2][2]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int kq = p32(16 * (kb0 + j) + 4 * (c & 3));    // this lane's quad of columns
 #pragma unroll
           for (int p = 0; p < 2; ++p) {
-            const bf16x8_t sb = pack2_bf(Sacc[2 * (pp + p)], Sacc[2 * (pp + p) + 1]);
+            const int tr0 = 32 * p + 4 * g + (c >> 2);
+            const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
+            const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
+            dst[j][p] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          }
+        }
+      };
+      {
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-              asm volatile("" : "+v"(qf[p][tb]));
-              QS[tb] = mfma16_bf(qf[p][tb], sb, QS[tb]);
-            }
+        for (int p = 0; p < 4; ++p) {     // Q fragments of block p + 1 are read before the 8 products of block p
+          if (p + 1 < 4) load_qf(p + 1, qf[(p + 1) & 1]);
+          const bf16x8_t sb0 = pack2_bf(Sacc[0][2 * p], Sacc[0][2 * p + 1]);
+          const bf16x8_t sb1 = pack2_bf(Sacc[1][2 * p], Sacc[1][2 * p + 1]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            asm volatile("" : "+v"(qf[p & 1][tb]));
+            QS[0][tb] = mfma16_bf(qf[p & 1][tb], sb0, QS[0][tb]);
+            QS[1][tb] = mfma16_bf(qf[p & 1][tb], sb1, QS[1][tb]);
           }
         }
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
           const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) QS[tb][i] *= egs[i];
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) QS[u][tb][i] *= egs[i];
         }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int tb = 0, j = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int p = 0; p <= (tb >> 1); ++p, ++j) pf[j] = ld16(&sm.P[(16 * tb + c) * TLD + 8 * g + 32 * p]);
+        load_fa(0, fa);
       }
       const float egL = gd[G_EG + L - 1];
-      lds_barrier();
+      lds_barrier_keep<15>();   // P, K and the gate data stay untouched in P3a
 
       // ---- P3a / P3b: state update, S = e^{gam_L} S + K^T Vd, in two halves of
       //      k.  Before it, in P3a, O = scale e^gam Q S^T + P Vn goes to HBM;
       //      after it, in P3b, K S^T of chunk ch+1 over columns 0-63.
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        asm volatile("" : "+v"(g), "+v"(c));
         if (half == 0) {
-          f16x8 pf[6];              // P tiles (t-block, k-block): 00 10 20 21 30 31
-#pragma unroll
-          for (int tb = 0, j = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int p = 0; p <= (tb >> 1); ++p, ++j) pf[j] = ld16(&sm.P[(16 * tb + c) * TLD + 8 * g + 32 * p]);
-          asm volatile("" ::: "memory");
 #pragma unroll
           for (int tb = 0, j = 0; tb < 4; ++tb)
 #pragma unroll
             for (int p = 0; p <= (tb >> 1); ++p, ++j) {
               asm volatile("" : "+v"(pf[j]));
-              QS[tb] = mfma16(pf[j], Vnb[p], QS[tb]);
+              QS[0][tb] = mfma16(pf[j], Vnb[0][p], QS[0][tb]);
+              QS[1][tb] = mfma16(pf[j], Vnb[1][p], QS[1][tb]);
             }
+          // P (overwritten in P3b) has been read once O exists
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(QS[0][tb]), "+v"(QS[1][tb]));
           // Row t of the chunk's output at obase + t row_bytes + this lane's
           // column: a uniform row address plus a 32-bit lane offset.
           char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
           const size_t row_bytes = v_stride * sizeof(uint16_t);
-          const uint32_t olane = uint32_t(4 * g) * uint32_t(row_bytes) + uint32_t(v0 + c) * 2u;
-          if (L == C) {
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
+          for (int u = 0; u < 2; ++u) {
+            const uint32_t olane = uint32_t(4 * g) * uint32_t(row_bytes) + uint32_t(v0 + 16 * u + c) * 2u;
+            if (L == C) {
 #pragma unroll
-              for (int i = 0; i < 4; i += 2)
-                store_bf16x2_saddr(obase + size_t(16 * tb + i) * row_bytes, obase + size_t(16 * tb + i + 1) * row_bytes,
-                                   olane, cvt_pk_bf16(QS[tb][i], QS[tb][i + 1]));
-          } else {
+              for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
+                for (int i = 0; i < 4; i += 2)
+                  store_bf16x2_saddr(obase + size_t(16 * tb + i) * row_bytes,
+                                     obase + size_t(16 * tb + i + 1) * row_bytes, olane,
+                                     cvt_pk_bf16(QS[u][tb][i], QS[u][tb][i + 1]));
+            } else {
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                if (16 * tb + 4 * g + i < L)
-                  *reinterpret_cast<uint16_t*>(obase + size_t(16 * tb + i) * row_bytes + olane) =
-                      f32_to_bf16_bits(QS[tb][i]);
-          }
-        }
+              for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int kb0 = 4 * half; kb0 < 4 * half + 4; kb0 += 2) {   // 4 K^T fragments read, then 4 products
-          f16x8 fa[2][2];
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int kq = p32(16 * (kb0 + j) + 4 * (c & 3));    // this lane's quad of columns
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-              const int tr0 = 32 * p + 4 * g + (c >> 2);
-              const f16x4_t lo = ld_tr16(&sm.Kc[kb_buf][tr0 * KCLD + kq]);
-              const f16x4_t hi = ld_tr16(&sm.Kc[kb_buf][(tr0 + 16) * KCLD + kq]);
-              fa[j][p] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                for (int i = 0; i < 4; ++i)
+                  if (16 * tb + 4 * g + i < L)
+                    *reinterpret_cast<uint16_t*>(obase + size_t(16 * tb + i) * row_bytes + olane) =
+                        f32_to_bf16_bits(QS[u][tb][i]);
             }
           }
-          asm volatile("" ::: "memory");
+        }
+        // K^T fragments of the next k-block pair are read before the products of
+        // this pair (the first pair was read in P2, the third at the end of P3a)
+#pragma unroll
+        for (int kb0 = 4 * half; kb0 < 4 * half + 4; kb0 += 2) {
+          f16x8 fn[2][2];
+          if (kb0 + 2 < 8 && kb0 != 2) load_fa(kb0 + 2, fn);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            Sacc[kb0 + j] *= egL;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) Sacc[u][kb0 + j] *= egL;
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
               asm volatile("" : "+v"(fa[j][p]));
-              Sacc[kb0 + j] = mfma16(fa[j][p], Vdb[p], Sacc[kb0 + j]);
+#pragma unroll
+              for (int u = 0; u < 2; ++u) Sacc[u][kb0 + j] = mfma16(fa[j][p], Vdb[u][p], Sacc[u][kb0 + j]);
             }
+          }
+          if (kb0 == 2) load_fa(4, fa);     // for P3b
+          else if (kb0 + 2 < 8) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int p = 0; p < 2; ++p) fa[j][p] = fn[j][p];
           }
         }
         if (half == 1) {    // after the last chunk this reads stale rows and is never used
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-          k_times_s_half(kb_buf ^ 1, 0);
+          zero_ks();
+          load_kf(kb_buf ^ 1, 0, kf_lo);
+          load_kf(kb_buf ^ 1, 2, kf_hi);
+          asm volatile("" ::: "memory");
+          mul_kf(0, kf_lo);
         }
-        lds_barrier();
+        lds_barrier_keep<15>();   // K (both buffers) stays untouched in P3b and P1
       }
     }
     asm volatile("" : "+v"(g), "+v"(c));
     float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb)
+        *reinterpret_cast<f32x4*>(dst + size_t(16 * u) * D + 16 * kb + 4 * g) = Sacc[u][kb];
   } else {
     // ================= preparation waves
     // The preparation waves run single-wave dependency chains (Tm inverse and
@@ -839,7 +932,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         diag_rows(IC<0>{}, IC<12>{}, dx);
         diag_rows(IC<12>{}, IC<16>{}, dx);
       } else {
-        tiles_P(gbuf[0], 0);
+        tiles_P1(gbuf[0], 0);
       }
       lds_barrier();
     }
@@ -847,10 +940,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g), "+v"(c), "+v"(ptid));
       const int nb = (ch + 1) & 1;          // parity of chunk ch+1
       const bool more = ch + 1 < n_chunks;
-      // ---- P1: 16-row Tm merges of chunk ch (waves 6, 7); K/Q rows of chunk
+      // ---- P1: 16-row Tm merges of chunk ch (prep waves 2, 3); K/Q rows of chunk
       //      ch+1 landed (copied in P3b of ch-1); gate data of ch+1 from a and b
-      //      loaded in P1 of ch-1, then the loads of a and b of ch+2 (wave 0)
+      //      loaded in P1 of ch-1, then the loads of a and b of ch+2 (prep wave 0)
       if (pw >= kPrepWaves - 2) merge16(32 * (pw - (kPrepWaves - 2)));
+      tiles_P2(gbuf[ch & 1], ch & 1);   // the rest of P of chunk ch (read by the chain in P3a)
       if (more) {
         wait_vm<0>();
         if (pw == 0) {
@@ -865,30 +959,31 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         tiles_A(gbuf[nb], nb);
       }
       lds_barrier();
-      // ---- P3a: rows 0-11 of the Tm diagonal blocks (wave 0), the lower-left A
-      //      tiles and the fp16 K rows (waves 1-7) of chunk ch+1; the chain has
-      //      read Tm and Aba of ch in P2
+      // ---- P3a: rows 0-11 of the Tm diagonal blocks (prep wave 0), the lower-left
+      //      A tiles and the fp16 K rows (prep waves 1-3) of chunk ch+1; the chain has
+      //      read Aba of ch in P1 and Tm of ch in P2
       if (more) {
         if (pw == 0) {
           diag_rows(IC<0>{}, IC<12>{}, dx);
         } else {
-          tiles_Aba(gbuf[nb], nb);   // the chain read Aba of chunk ch in P2
+          tiles_Aba(gbuf[nb], nb);   // the chain read Aba of chunk ch in P1
           convert_k(ch + 1);
         }
       }
       lds_barrier();
-      // ---- P3b: rows 12-15 of the Tm diagonal blocks (wave 0) and the P tiles
-      //      (waves 1-7) of chunk ch+1, the chain having read P of ch in P3a;
+      // ---- P3b: rows 12-15 of the Tm diagonal blocks (prep wave 0) and the P tiles
+      //      (prep waves 1-3) of chunk ch+1, the chain having read P of ch in P3a;
       //      copies of chunk ch+2 into the raw buffers of ch; V of chunk ch+1
-      //      landed (only those 4 copies, 8 on wave 7, remain)
+      //      landed (only the new K/Q copies, 12 on prep wave 1 and 10 on prep
+      //      waves 2 and 3, remain outstanding)
       if (more) {
         if (pw == 0) diag_rows(IC<12>{}, IC<16>{}, dx);
-        else tiles_P(gbuf[nb], nb);
+        else tiles_P1(gbuf[nb], nb);
       }
       if (pw > 0) {
         if (ch + 2 < n_chunks) {
           copy_kq(ch + 2);
-          if (pw == kPrepWaves - 1) wait_vm<8>(); else wait_vm<4>();
+          if (pw == 1) wait_vm<12>(); else wait_vm<10>();
         } else if (more) {
           wait_vm<0>();
         }
