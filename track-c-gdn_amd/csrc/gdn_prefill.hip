@@ -91,7 +91,7 @@ struct __align__(16) Smem {
   _Float16 Tm[C * TLD];        // diagonal 32-row blocks of (I + A)^-1 [t][p32(t')]
   _Float16 P[C * TLD];         // decayed causal Q K^T [t][p32(t')]
   float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32), diagonal 32-row blocks
-  _Float16 Aba[(C / 2) * BLD]; // its lower-left 32x32 block in fp16 [t - 32][p32(t')]
+  _Float16 Aba[(C / 2) * BLD]; // its lower-left 32x32 block, negated, in fp16 [t - 32][p32(t')]
 };
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
@@ -242,7 +242,7 @@ using IC = std::integral_constant<int, N>;
 // chunks and issue every copy into LDS.  In iteration i the chain works on
 // chunk i while the preparation waves build chunk i+1, in four phases
 // separated by LDS barriers:
-//   P1   chain : K S^T (columns 64-127), X  prep : 16-row merges of Tm_i (prep waves 2, 3);
+//   P1   chain : X = beta (V - e^gam K S^T) prep : 16-row merges of Tm_i (prep waves 2, 3);
 //                                                  rest of P_i; gate data of chunk i+1
 //                                                  (prep wave 0)
 //   P2   chain : Vn = Tm X, Vd,             prep : copy of V_{i+1}; A_{i+1} tiles of
@@ -252,7 +252,7 @@ using IC = std::integral_constant<int, N>;
 //                first half of k                   A_{i+1} tiles; fp16 K_{i+1}
 //   P3b  chain : S update, second half;     prep : rows 12-15 of those blocks (prep
 //                K S^T of chunk i+1                wave 0); P_{i+1} tiles; copies of
-//                (columns 0-63)                    K/Q of chunk i+2
+//                                                  K/Q of chunk i+2
 // The 32-row merge of Tm is left to the chain: Vn = Tm X is applied as
 // Vn_top = T_a X_top, Vn_bot = T_b (X_bot - A_ba Vn_top).
 // Raw K and Q rows are double-buffered by chunk parity, so the chain reads the
@@ -363,10 +363,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
     }
   };
-  auto copy_kq = [&](int ch) {
-    copy_rows(k, qk_stride, size_t(hq) * D, dma_qk, ch, raw.k[ch & 1]);
-    copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1]);
-  };
+  auto copy_k = [&](int ch) { copy_rows(k, qk_stride, size_t(hq) * D, dma_qk, ch, raw.k[ch & 1]); };
+  auto copy_q = [&](int ch) { copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1]); };
+  auto copy_kq = [&](int ch) { copy_k(ch); copy_q(ch); };
   auto copy_v = [&](int ch) { copy_rows(v, v_stride, size_t(hv) * D, dma_v, ch, rawV); };
   auto load_ab = [&](int ch) {      // a, b of the chunk's tokens for gate_compute (wave 0)
     const int L = chunk_len(ch);
@@ -468,9 +467,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       val[i] = br * __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
       if (ti == tj) val[i] = (c > 4 * g + i) ? val[i] : 0.f;
     }
-    if (ti >= 2 && tj <= 1) {     // lower-left 32x32 block: an MFMA operand of the chain
+    if (ti >= 2 && tj <= 1) {     // lower-left 32x32 block, negated: an MFMA operand of the chain
       *reinterpret_cast<f16x4_t*>(&sm.Aba[(16 * (ti - 2) + c) * BLD + 8 * g + 4 * tj]) =
-          f16x4_t{(_Float16)val[0], (_Float16)val[1], (_Float16)val[2], (_Float16)val[3]};
+          f16x4_t{(_Float16)-val[0], (_Float16)-val[1], (_Float16)-val[2], (_Float16)-val[3]};
     } else {
       *reinterpret_cast<f32x4*>(&sm.A[(16 * ti + c) * ALD + 16 * tj + 4 * g]) = val;
     }
@@ -650,6 +649,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       load_kf(0, 2, kf_hi);
       asm volatile("" ::: "memory");
       mul_kf(0, kf_lo);
+      mul_kf(2, kf_hi);
       lds_barrier();
     }
     for (int ch = 0; ch < n_chunks; ++ch) {
@@ -657,22 +657,24 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       const int kb_buf = ch & 1;
       const float* gd = gbuf[ch & 1];
 
-      // ---- P1: rest of K S^T (columns 64-127), X = beta (V - e^gam K S^T) in place of KS.
-      //      V and gate reads go first (independent of K S^T); at the end, the
-      //      A_ba tiles and the Q fragments of column block 0 are read for P2.
+      // ---- P1: X = beta (V - e^gam K S^T) in place of KS; at the end, the A_ba
+      //      tiles and the Q fragments of column block 0 are read for P2.
       {
-        // V[t][v0 + 16 u + c] for t = 16 tb + 4 g + i: rows with t % 16 = 4 g + i
-        // share the swizzle, so 4 lane offsets serve the reads of a tile.
-        uint16_t vv[2][4][4];
+        // V[16 tb + 4 g + i][v0 + 16 u + c], i = 0..3, by one transposing read per
+        // (u, tb): lane 4 m + j of group g reads columns v0 + 16 u + 4 j .. +3 of
+        // row 16 tb + 4 g + m (8 contiguous bytes of a swizzled 16-byte slot).
+        i16x4_t vv[2][4];
+        {
+          const int m = c >> 2, j = c & 3;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int col = v0 + 16 * u + c;
-          const uint16_t* vbase = &rawV[(4 * g) * D + (col & 7)];
+          for (int u = 0; u < 2; ++u) {
+            const int col = v0 + 16 * u + 4 * j;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint16_t* vrow_i = vbase + i * D + 8 * ((col >> 3) ^ (4 * g + i));
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) vv[u][tb][i] = vrow_i[16 * tb * D];
+            for (int tb = 0; tb < 4; ++tb) {
+              const int t = 16 * tb + 4 * g + m;
+              vv[u][tb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) i16x4_t*)&rawV[t * D + 8 * ((col >> 3) ^ (t & 15)) + (col & 7)]);
+            }
           }
         }
         f32x4 eg[4], bt[4];
@@ -681,15 +683,14 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           eg[tb] = *reinterpret_cast<const f32x4*>(&gd[G_EG + 16 * tb + 4 * g]);
           bt[tb] = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * tb + 4 * g]);
         }
-        asm volatile("" ::: "memory");
-        mul_kf(2, kf_hi);       // read in P3b of the previous chunk (or the prologue)
+        asm volatile("" ::: "memory");    // every read issued before the first use
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              KS[u][tb][i] = bt[tb][i] * (bf16_bits_to_f32(vv[u][tb][i]) - eg[tb][i] * KS[u][tb][i]);
+              KS[u][tb][i] = bt[tb][i] * (bf16_bits_to_f32(uint16_t(vv[u][tb][i])) - eg[tb][i] * KS[u][tb][i]);
         // X is formed here, so the V rows (overwritten in P2) have been read
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -727,41 +728,49 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       f16x8 Vdb[2][2], Vnb[2][2];
       {
         // Tm = [[T_a, 0], [-T_b A_ba T_a, T_b]] in 32-row blocks, so
-        // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).  The 6
-        // operand tiles are read up front and serve both column tiles.
+        // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).  The
+        // operand tiles are read up front and serve both column tiles, whose
+        // products are interleaved stage by stage; the preparation stores
+        // -A_ba, so X_bot - A_ba Vn_top accumulates in the MFMA.
         f16x8 ta[2], tb2[2];
+        f32x4 ed[4];            // e^{gam_L - gam} of this lane's rows, for Vd
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           ta[j] = ld16(&sm.Tm[(16 * j + c) * TLD + 8 * g]);
           tb2[j] = ld16(&sm.Tm[(16 * (j + 2) + c) * TLD + 32 + 8 * g]);
         }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) ed[tb] = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb + 4 * g]);
+        load_qf(1, qf[1]);      // Q S^T operands of column block 1, used after Tm X
         asm volatile("" ::: "memory");
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        f32x4 Vn[2][4];
+        f16x8 xb[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) xb[u] = pack2(KS[u][0], KS[u][1]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) Vn[u][tb] = mfma16(ta[tb], xb[u], z);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) Vnb[u][0] = pack2(Vn[u][0], Vn[u][1]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) KS[u][2 + tb] = mfma16(ab[tb], Vnb[u][0], KS[u][2 + tb]);
+        // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
+#pragma unroll
+        for (int u = 0; u < 2; ++u) Vdb[u][0] = pack2(Vn[u][0] * ed[0], Vn[u][1] * ed[1]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) xb[u] = pack2(KS[u][2], KS[u][3]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int tb = 2; tb < 4; ++tb) Vn[u][tb] = mfma16(tb2[tb - 2], xb[u], z);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          f32x4 Vn[4];
-          const f16x8 Xtop = pack2(KS[u][0], KS[u][1]);
-#pragma unroll
-          for (int tb = 0; tb < 2; ++tb) Vn[tb] = mfma16(ta[tb], Xtop, z);
-          Vnb[u][0] = pack2(Vn[0], Vn[1]);
-          // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
-          auto decayed = [&](int tb0) {
-            const f32x4 e0 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 4 * g]);
-            const f32x4 e1 = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb0 + 16 + 4 * g]);
-            return pack2(Vn[tb0] * e0, Vn[tb0 + 1] * e1);
-          };
-          Vdb[u][0] = decayed(0);
-#pragma unroll
-          for (int tb = 0; tb < 2; ++tb) {
-            const f32x4 y = mfma16(ab[tb], Vnb[u][0], z);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) KS[u][2 + tb][i] -= y[i];
-          }
-          const f16x8 Xbot = pack2(KS[u][2], KS[u][3]);
-#pragma unroll
-          for (int tb = 2; tb < 4; ++tb) Vn[tb] = mfma16(tb2[tb - 2], Xbot, z);
-          Vnb[u][1] = pack2(Vn[2], Vn[3]);
-          Vdb[u][1] = decayed(2);
+          Vnb[u][1] = pack2(Vn[u][2], Vn[u][3]);
+          Vdb[u][1] = pack2(Vn[u][2] * ed[2], Vn[u][3] * ed[3]);
         }
         // Tm and A_ba (overwritten in P3a) have been read once Vn and Vd exist
 #pragma unroll
@@ -769,7 +778,6 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
           for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(Vnb[u][j]), "+v"(Vdb[u][j]));
       }
-      asm volatile("" ::: "memory");    // Q S^T reads start after Tm X (register pressure)
       f32x4 QS[2][4];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -792,8 +800,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       };
       {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {     // Q fragments of block p + 1 are read before the 8 products of block p
-          if (p + 1 < 4) load_qf(p + 1, qf[(p + 1) & 1]);
+        for (int p = 0; p < 4; ++p) {     // the 8 products of block p, then the reads of block p + 2
           const bf16x8_t sb0 = pack2_bf(Sacc[0][2 * p], Sacc[0][2 * p + 1]);
           const bf16x8_t sb1 = pack2_bf(Sacc[1][2 * p], Sacc[1][2 * p + 1]);
 #pragma unroll
@@ -802,6 +809,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
             QS[0][tb] = mfma16_bf(qf[p & 1][tb], sb0, QS[0][tb]);
             QS[1][tb] = mfma16_bf(qf[p & 1][tb], sb1, QS[1][tb]);
           }
+          if (p + 2 < 4) load_qf(p + 2, qf[p & 1]);
         }
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
@@ -823,7 +831,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 
       // ---- P3a / P3b: state update, S = e^{gam_L} S + K^T Vd, in two halves of
       //      k.  Before it, in P3a, O = scale e^gam Q S^T + P Vn goes to HBM;
-      //      after it, in P3b, K S^T of chunk ch+1 over columns 0-63.
+      //      after it, in P3b, K S^T of chunk ch+1.
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         if (half == 0) {
@@ -895,6 +903,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           load_kf(kb_buf ^ 1, 2, kf_hi);
           asm volatile("" ::: "memory");
           mul_kf(0, kf_lo);
+          mul_kf(2, kf_hi);
         }
         lds_barrier_keep<15>();   // K (both buffers) stays untouched in P3b and P1
       }
@@ -958,6 +967,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         copy_v(ch + 1);           // every chain wave has read V of chunk ch
         tiles_A(gbuf[nb], nb);
       }
+      if (pw > 0 && ch + 2 < n_chunks) copy_k(ch + 2);   // raw K of chunk ch was last read in P1
       lds_barrier();
       // ---- P3a: rows 0-11 of the Tm diagonal blocks (prep wave 0), the lower-left
       //      A tiles and the fp16 K rows (prep waves 1-3) of chunk ch+1; the chain has
@@ -982,7 +992,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
       if (pw > 0) {
         if (ch + 2 < n_chunks) {
-          copy_kq(ch + 2);
+          copy_q(ch + 2);
           if (pw == 1) wait_vm<12>(); else wait_vm<10>();
         } else if (more) {
           wait_vm<0>();
