@@ -207,13 +207,10 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
 }
 
-// The two bf16 halves of a dword to base0 + off and base1 + off: bases uniform
-// (SGPR pairs), off a 32-bit lane offset, so no 64-bit address arithmetic per
-// store.  Nothing in the kernel reads what these stores write.
-__device__ __forceinline__ void store_bf16x2_saddr(const char* base0, const char* base1, uint32_t off,
-                                                   uint32_t two) {
-  asm volatile("global_store_short %0, %1, %2\n\tglobal_store_short_d16_hi %0, %1, %3"
-               :: "v"(off), "v"(two), "s"(base0), "s"(base1) : "memory");
+// 8 bytes to base + off: base uniform (an SGPR pair), off a 32-bit lane offset.
+// Nothing in the kernel reads what these stores write.
+__device__ __forceinline__ void store_b64_saddr(char* base, uint32_t off, uint32_t lo, uint32_t hi) {
+  asm volatile("global_store_dwordx2 %0, %1, %2" :: "v"(off), "v"(uint2{lo, hi}), "s"(base) : "memory");
 }
 
 // Tokens [bos, bos + len) of sequence n, clamped into [0, T].
@@ -328,7 +325,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // Preparation wave 0 issues no copies, only its loads of a and b, so the
   // waits the compiler places for those count nothing else.
   constexpr int kMaxGroups = 6;
-  const int n_groups = pw == 0 ? 0 : (pw == 1 ? 6 : 5);
+  const int n_groups = (is_chain || pw == 0) ? 0 : (pw == 1 ? 6 : 5);
   const int group0 = pw == 1 ? 0 : (pw == 2 ? 6 : 11);
   auto group_row0 = [&](int j) { return 4 * (group0 + j); };
   // Byte offsets, from a chunk's first row, of the 16 bytes this lane copies
@@ -516,10 +513,10 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // preparation waves 1-3, in a phase in which the chain does not read Aba.
   auto tiles_Aba = [&](const float* gd, int pb) {
     switch (pw) {
-      case 1: tile_A(IC<3>{}, gd, pb); tile_A(IC<4>{}, gd, pb); break;
+      case 0: tile_A(IC<4>{}, gd, pb); break;
+      case 1: tile_A(IC<3>{}, gd, pb); break;
       case 2: tile_A(IC<6>{}, gd, pb); break;
-      case 3: tile_A(IC<7>{}, gd, pb); break;
-      default: break;
+      default: tile_A(IC<7>{}, gd, pb); break;
     }
   };
   // Rows [I0, I1) of the diagonal 16x16 blocks of Tm: lane group g inverts
@@ -778,11 +775,15 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
           for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(Vnb[u][j]), "+v"(Vdb[u][j]));
       }
-      f32x4 QS[2][4];
+      // The output tiles are formed transposed, O^T = S Q^T + Vn^T P^T: lane
+      // (g, c) of OT[u][tb] holds token 16 tb + c, state rows (output columns)
+      // v0 + 16 u + 4 g .. +3, 8 contiguous bytes of an output row.  The
+      // operand registers are those of the untransposed products, swapped.
+      f32x4 OT[2][4];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) QS[u][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; ++tb) OT[u][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
       f16x8 pf[6];              // P tiles (t-block, k-block): 00 10 20 21 30 31, read for P3a
       f16x8 fa[2][2];           // K^T fragments of k-blocks 0, 1, read for P3a
       auto load_fa = [&](int kb0, f16x8(&dst)[2][2]) {
@@ -806,18 +807,16 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
             asm volatile("" : "+v"(qf[p & 1][tb]));
-            QS[0][tb] = mfma16_bf(qf[p & 1][tb], sb0, QS[0][tb]);
-            QS[1][tb] = mfma16_bf(qf[p & 1][tb], sb1, QS[1][tb]);
+            OT[0][tb] = mfma16_bf(sb0, qf[p & 1][tb], OT[0][tb]);
+            OT[1][tb] = mfma16_bf(sb1, qf[p & 1][tb], OT[1][tb]);
           }
           if (p + 2 < 4) load_qf(p + 2, qf[p & 1]);
         }
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-          const f32x4 egs = *reinterpret_cast<const f32x4*>(&gd[G_EGS + 16 * tb + 4 * g]);
+          const float egs = gd[G_EGS + 16 * tb + c];    // scale e^gam of this lane's token
 #pragma unroll
-          for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) QS[u][tb][i] *= egs[i];
+          for (int u = 0; u < 2; ++u) OT[u][tb] *= egs;
         }
         asm volatile("" ::: "memory");
 #pragma unroll
@@ -840,35 +839,24 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
             for (int p = 0; p <= (tb >> 1); ++p, ++j) {
               asm volatile("" : "+v"(pf[j]));
-              QS[0][tb] = mfma16(pf[j], Vnb[0][p], QS[0][tb]);
-              QS[1][tb] = mfma16(pf[j], Vnb[1][p], QS[1][tb]);
+              OT[0][tb] = mfma16(Vnb[0][p], pf[j], OT[0][tb]);
+              OT[1][tb] = mfma16(Vnb[1][p], pf[j], OT[1][tb]);
             }
           // P (overwritten in P3b) has been read once O exists
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(QS[0][tb]), "+v"(QS[1][tb]));
-          // Row t of the chunk's output at obase + t row_bytes + this lane's
-          // column: a uniform row address plus a 32-bit lane offset.
-          char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
+          for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(OT[0][tb]), "+v"(OT[1][tb]));
+          // Token t of the chunk at obase + t row_bytes, this lane's 4 columns at
+          // 8 g bytes from the tile's first: a uniform base plus a 32-bit lane offset.
           const size_t row_bytes = v_stride * sizeof(uint16_t);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const uint32_t olane = uint32_t(4 * g) * uint32_t(row_bytes) + uint32_t(v0 + 16 * u + c) * 2u;
-            if (L == C) {
+            char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D + v0 + 16 * u);
 #pragma unroll
-              for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-                for (int i = 0; i < 4; i += 2)
-                  store_bf16x2_saddr(obase + size_t(16 * tb + i) * row_bytes,
-                                     obase + size_t(16 * tb + i + 1) * row_bytes, olane,
-                                     cvt_pk_bf16(QS[u][tb][i], QS[u][tb][i + 1]));
-            } else {
-#pragma unroll
-              for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                  if (16 * tb + 4 * g + i < L)
-                    *reinterpret_cast<uint16_t*>(obase + size_t(16 * tb + i) * row_bytes + olane) =
-                        f32_to_bf16_bits(QS[u][tb][i]);
+            for (int tb = 0; tb < 4; ++tb) {
+              const uint32_t olane = uint32_t(16 * tb + c) * uint32_t(row_bytes) + uint32_t(8 * g);
+              if (L == C || 16 * tb + c < L)
+                store_b64_saddr(obase, olane, cvt_pk_bf16(OT[u][tb][0], OT[u][tb][1]),
+                                cvt_pk_bf16(OT[u][tb][2], OT[u][tb][3]));
             }
           }
         }
@@ -949,13 +937,13 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g), "+v"(c), "+v"(ptid));
       const int nb = (ch + 1) & 1;          // parity of chunk ch+1
       const bool more = ch + 1 < n_chunks;
-      // ---- P1: 16-row Tm merges of chunk ch (prep waves 2, 3); K/Q rows of chunk
-      //      ch+1 landed (copied in P3b of ch-1); gate data of ch+1 from a and b
+      // ---- P1: 16-row Tm merges of chunk ch (prep waves 2, 3); K rows of chunk
+      //      ch+1 landed (copied in P2 of ch-1); gate data of ch+1 from a and b
       //      loaded in P1 of ch-1, then the loads of a and b of ch+2 (prep wave 0)
       if (pw >= kPrepWaves - 2) merge16(32 * (pw - (kPrepWaves - 2)));
       tiles_P2(gbuf[ch & 1], ch & 1);   // the rest of P of chunk ch (read by the chain in P3a)
       if (more) {
-        wait_vm<0>();
+        if (pw == 1) wait_vm<6>(); else wait_vm<5>();   // K of ch+1 landed; its Q copies may remain
         if (pw == 0) {
           gate_compute(ch + 1);
           if (ch + 2 < n_chunks) load_ab(ch + 2);
@@ -967,17 +955,21 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         copy_v(ch + 1);           // every chain wave has read V of chunk ch
         tiles_A(gbuf[nb], nb);
       }
-      if (pw > 0 && ch + 2 < n_chunks) copy_k(ch + 2);   // raw K of chunk ch was last read in P1
+      if (ch + 2 < n_chunks) copy_k(ch + 2);   // raw K of chunk ch was last read in P1
       lds_barrier();
       // ---- P3a: rows 0-11 of the Tm diagonal blocks (prep wave 0), the lower-left
       //      A tiles and the fp16 K rows (prep waves 1-3) of chunk ch+1; the chain has
       //      read Aba of ch in P1 and Tm of ch in P2
       if (more) {
-        if (pw == 0) {
-          diag_rows(IC<0>{}, IC<12>{}, dx);
+        tiles_Aba(gbuf[nb], nb);     // the chain read Aba of chunk ch in P1
+        if (pw == 0) diag_rows(IC<0>{}, IC<12>{}, dx);
+        else convert_k(ch + 1);
+        // Q of chunk ch+1 landed (read from P3b on); the V and K copies issued
+        // in P2 may remain
+        if (ch + 2 < n_chunks) {
+          if (pw == 1) wait_vm<12>(); else wait_vm<10>();
         } else {
-          tiles_Aba(gbuf[nb], nb);   // the chain read Aba of chunk ch in P1
-          convert_k(ch + 1);
+          if (pw == 1) wait_vm<6>(); else wait_vm<5>();
         }
       }
       lds_barrier();
@@ -990,13 +982,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         if (pw == 0) diag_rows(IC<12>{}, IC<16>{}, dx);
         else tiles_P1(gbuf[nb], nb);
       }
-      if (pw > 0) {
-        if (ch + 2 < n_chunks) {
-          copy_q(ch + 2);
-          if (pw == 1) wait_vm<12>(); else wait_vm<10>();
-        } else if (more) {
-          wait_vm<0>();
-        }
+      if (ch + 2 < n_chunks) {
+        copy_q(ch + 2);
+        if (pw == 1) wait_vm<12>(); else wait_vm<10>();   // the K and Q copies of chunk ch+2 may remain
+      } else if (more) {
+        wait_vm<0>();
       }
       lds_barrier();
     }
