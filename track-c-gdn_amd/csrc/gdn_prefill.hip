@@ -60,7 +60,8 @@ constexpr int kPrepWaves = 4;               // preparation / copy waves, one per
 constexpr int kWaves = kChainWaves + kPrepWaves;
 constexpr int kThreads = kWaves * 64;
 constexpr int kPrepThreads = kPrepWaves * 64;
-constexpr int kRowsPerWave = D / kChainWaves;   // 32 state rows (v) per chain wave: two 16-column tiles
+constexpr int kRowsPerWave = D / kChainWaves;   // state rows (v) per chain wave
+constexpr int kTiles = kRowsPerWave / 16;        // 16-row column tiles per chain wave
 
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -207,10 +208,12 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
 }
 
-// 8 bytes to base + off: base uniform (an SGPR pair), off a 32-bit lane offset.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16 bytes to base + off: base uniform (an SGPR pair), off a 32-bit lane offset.
 // Nothing in the kernel reads what these stores write.
-__device__ __forceinline__ void store_b64_saddr(char* base, uint32_t off, uint32_t lo, uint32_t hi) {
-  asm volatile("global_store_dwordx2 %0, %1, %2" :: "v"(off), "v"(uint2{lo, hi}), "s"(base) : "memory");
+__device__ __forceinline__ void store_b128_saddr(char* base, uint32_t off, u32x4_t data) {
+  asm volatile("global_store_dwordx4 %0, %1, %2" :: "v"(off), "v"(data), "s"(base) : "memory");
 }
 
 // Tokens [bos, bos + len) of sequence n, clamped into [0, T].
@@ -590,15 +593,15 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     // ================= chain waves
     // Column tile u (0, 1) of this wave holds state rows v = v0 + 16 u + c.
     // initial state: Sacc[u][kb][i] = S[v0 + 16 u + c][16 kb + 4 g + i]
-    f32x4 Sacc[2][8];
+    f32x4 Sacc[kTiles][8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < kTiles; ++u)
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb) Sacc[u][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (h0 != nullptr) {
       const float* src = h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < kTiles; ++u)
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb)
           Sacc[u][kb] = *reinterpret_cast<const f32x4*>(src + size_t(16 * u) * D + 16 * kb + 4 * g);
@@ -607,7 +610,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     // fp16 K rows are in Kc[kb_buf]; columns 0-63 use state entries k < 64,
     // updated in the first half of the state update.  The 8 K fragments are
     // read before the first product and serve both column tiles.
-    f32x4 KS[2][4];
+    f32x4 KS[kTiles][4];
     // K fragments of column blocks p0, p0 + 1 of Kc[kb_buf]: issued ahead of
     // their products (LDS reads wait behind the other waves' traffic).
     typedef f16x8 KFrag[2][4];
@@ -621,20 +624,21 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     auto mul_kf = [&](int p0, KFrag& kf) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const f16x8 sb0 = pack2(Sacc[0][2 * (p0 + p)], Sacc[0][2 * (p0 + p) + 1]);
-        const f16x8 sb1 = pack2(Sacc[1][2 * (p0 + p)], Sacc[1][2 * (p0 + p) + 1]);
+        f16x8 sb[kTiles];
+#pragma unroll
+        for (int u = 0; u < kTiles; ++u) sb[u] = pack2(Sacc[u][2 * (p0 + p)], Sacc[u][2 * (p0 + p) + 1]);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
           asm volatile("" : "+v"(kf[p][tb]));   // products wait here, not between the reads
-          KS[0][tb] = mfma16(kf[p][tb], sb0, KS[0][tb]);
-          KS[1][tb] = mfma16(kf[p][tb], sb1, KS[1][tb]);
+#pragma unroll
+          for (int u = 0; u < kTiles; ++u) KS[u][tb] = mfma16(kf[p][tb], sb[u], KS[u][tb]);
         }
       }
     };
     KFrag kf_lo, kf_hi;     // columns 0-63 / 64-127 of the next chunk's K
     auto zero_ks = [&]() {
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < kTiles; ++u)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) KS[u][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
@@ -660,11 +664,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         // V[16 tb + 4 g + i][v0 + 16 u + c], i = 0..3, by one transposing read per
         // (u, tb): lane 4 m + j of group g reads columns v0 + 16 u + 4 j .. +3 of
         // row 16 tb + 4 g + m (8 contiguous bytes of a swizzled 16-byte slot).
-        i16x4_t vv[2][4];
+        i16x4_t vv[kTiles][4];
         {
           const int m = c >> 2, j = c & 3;
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
+          for (int u = 0; u < kTiles; ++u) {
             const int col = v0 + 16 * u + 4 * j;
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
@@ -680,9 +684,15 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           eg[tb] = *reinterpret_cast<const f32x4*>(&gd[G_EG + 16 * tb + 4 * g]);
           bt[tb] = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * tb + 4 * g]);
         }
-        asm volatile("" ::: "memory");    // every read issued before the first use
+        // every read issued before the first use (the asm operands keep the
+        // conversions of V below this point)
+        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kTiles; ++u)
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(vv[u][tb]));
+#pragma unroll
+        for (int u = 0; u < kTiles; ++u)
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
@@ -690,7 +700,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
               KS[u][tb][i] = bt[tb][i] * (bf16_bits_to_f32(uint16_t(vv[u][tb][i])) - eg[tb][i] * KS[u][tb][i]);
         // X is formed here, so the V rows (overwritten in P2) have been read
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kTiles; ++u)
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(KS[u][tb]));
       }
@@ -722,7 +732,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       lds_barrier_keep<15>();   // A_ba and Q stay untouched in P2
 
       // ---- P2: Vn = Tm X, Vd; scale e^gam Q S^T
-      f16x8 Vdb[2][2], Vnb[2][2];
+      f16x8 Vdb[kTiles][2], Vnb[kTiles][2];
       {
         // Tm = [[T_a, 0], [-T_b A_ba T_a, T_b]] in 32-row blocks, so
         // Vn_top = T_a X_top and Vn_bot = T_b (X_bot - A_ba Vn_top).  The
@@ -741,37 +751,37 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         load_qf(1, qf[1]);      // Q S^T operands of column block 1, used after Tm X
         asm volatile("" ::: "memory");
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        f32x4 Vn[2][4];
-        f16x8 xb[2];
+        f32x4 Vn[kTiles][4];
+        f16x8 xb[kTiles];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) xb[u] = pack2(KS[u][0], KS[u][1]);
+        for (int u = 0; u < kTiles; ++u) xb[u] = pack2(KS[u][0], KS[u][1]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kTiles; ++u)
 #pragma unroll
           for (int tb = 0; tb < 2; ++tb) Vn[u][tb] = mfma16(ta[tb], xb[u], z);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) Vnb[u][0] = pack2(Vn[u][0], Vn[u][1]);
+        for (int u = 0; u < kTiles; ++u) Vnb[u][0] = pack2(Vn[u][0], Vn[u][1]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kTiles; ++u)
 #pragma unroll
           for (int tb = 0; tb < 2; ++tb) KS[u][2 + tb] = mfma16(ab[tb], Vnb[u][0], KS[u][2 + tb]);
         // decayed copy for the state update: Vd = e^{gam_L - gam} Vn
 #pragma unroll
-        for (int u = 0; u < 2; ++u) Vdb[u][0] = pack2(Vn[u][0] * ed[0], Vn[u][1] * ed[1]);
+        for (int u = 0; u < kTiles; ++u) Vdb[u][0] = pack2(Vn[u][0] * ed[0], Vn[u][1] * ed[1]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) xb[u] = pack2(KS[u][2], KS[u][3]);
+        for (int u = 0; u < kTiles; ++u) xb[u] = pack2(KS[u][2], KS[u][3]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kTiles; ++u)
 #pragma unroll
           for (int tb = 2; tb < 4; ++tb) Vn[u][tb] = mfma16(tb2[tb - 2], xb[u], z);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kTiles; ++u) {
           Vnb[u][1] = pack2(Vn[u][2], Vn[u][3]);
           Vdb[u][1] = pack2(Vn[u][2] * ed[2], Vn[u][3] * ed[3]);
         }
         // Tm and A_ba (overwritten in P3a) have been read once Vn and Vd exist
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kTiles; ++u)
 #pragma unroll
           for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(Vnb[u][j]), "+v"(Vdb[u][j]));
       }
@@ -779,9 +789,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       // (g, c) of OT[u][tb] holds token 16 tb + c, state rows (output columns)
       // v0 + 16 u + 4 g .. +3, 8 contiguous bytes of an output row.  The
       // operand registers are those of the untransposed products, swapped.
-      f32x4 OT[2][4];
+      f32x4 OT[kTiles][4];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < kTiles; ++u)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) OT[u][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
       f16x8 pf[6];              // P tiles (t-block, k-block): 00 10 20 21 30 31, read for P3a
@@ -800,23 +810,20 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         }
       };
       {
+        // Column blocks 0, 1 of S Q^T here, blocks 2, 3 in P3a (their Q fragments
+        // read here, before other chain waves stage outputs in the raw Q buffer)
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {     // the 8 products of block p, then the reads of block p + 2
-          const bf16x8_t sb0 = pack2_bf(Sacc[0][2 * p], Sacc[0][2 * p + 1]);
-          const bf16x8_t sb1 = pack2_bf(Sacc[1][2 * p], Sacc[1][2 * p + 1]);
+        for (int p = 0; p < 2; ++p) {     // the 8 products of block p, then the reads of block p + 2
+          bf16x8_t sb[kTiles];
+#pragma unroll
+          for (int u = 0; u < kTiles; ++u) sb[u] = pack2_bf(Sacc[u][2 * p], Sacc[u][2 * p + 1]);
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
             asm volatile("" : "+v"(qf[p & 1][tb]));
-            OT[0][tb] = mfma16_bf(sb0, qf[p & 1][tb], OT[0][tb]);
-            OT[1][tb] = mfma16_bf(sb1, qf[p & 1][tb], OT[1][tb]);
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16_bf(sb[u], qf[p & 1][tb], OT[u][tb]);
           }
-          if (p + 2 < 4) load_qf(p + 2, qf[p & 1]);
-        }
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const float egs = gd[G_EGS + 16 * tb + c];    // scale e^gam of this lane's token
-#pragma unroll
-          for (int u = 0; u < 2; ++u) OT[u][tb] *= egs;
+          load_qf(p + 2, qf[p & 1]);
         }
         asm volatile("" ::: "memory");
 #pragma unroll
@@ -835,29 +842,60 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       for (int half = 0; half < 2; ++half) {
         if (half == 0) {
 #pragma unroll
+          for (int p = 2; p < 4; ++p) {   // the rest of S Q^T (S before this chunk's update)
+            bf16x8_t sb[kTiles];
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) sb[u] = pack2_bf(Sacc[u][2 * p], Sacc[u][2 * p + 1]);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+              asm volatile("" : "+v"(qf[p & 1][tb]));
+#pragma unroll
+              for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16_bf(sb[u], qf[p & 1][tb], OT[u][tb]);
+            }
+          }
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const float egs = gd[G_EGS + 16 * tb + c];    // scale e^gam of this lane's token
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) OT[u][tb] *= egs;
+          }
+#pragma unroll
           for (int tb = 0, j = 0; tb < 4; ++tb)
 #pragma unroll
             for (int p = 0; p <= (tb >> 1); ++p, ++j) {
               asm volatile("" : "+v"(pf[j]));
-              OT[0][tb] = mfma16(Vnb[0][p], pf[j], OT[0][tb]);
-              OT[1][tb] = mfma16(Vnb[1][p], pf[j], OT[1][tb]);
+#pragma unroll
+              for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16(Vnb[u][p], pf[j], OT[u][tb]);
             }
           // P (overwritten in P3b) has been read once O exists
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(OT[0][tb]), "+v"(OT[1][tb]));
-          // Token t of the chunk at obase + t row_bytes, this lane's 4 columns at
-          // 8 g bytes from the tile's first: a uniform base plus a 32-bit lane offset.
+          for (int u = 0; u < kTiles; ++u)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(OT[u][tb]));
+          // The chunk's output tile is staged in the raw Q buffer of this chunk
+          // (last read in P2; the Q copy of chunk ch+2 goes there in P1 of the
+          // next iteration), in the raw row layout: token t, 4 columns per lane
+          // (one 8-byte write); P3b stores whole rows from it.
+#pragma unroll
+          for (int u = 0; u < kTiles; ++u)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+              *reinterpret_cast<uint2*>(&raw.q[kb_buf][raw_off(16 * tb + c, v0 + 16 * u + 4 * g)]) =
+                  uint2{cvt_pk_bf16(OT[u][tb][0], OT[u][tb][1]), cvt_pk_bf16(OT[u][tb][2], OT[u][tb][3])};
+          asm volatile("" ::: "memory");
+        }
+        if (half == 1) {
+          // Rows kOutRows w .. kOutRows (w + 1) - 1 of the staged output tile
+          // (w = this chain wave), 4 rows per instruction, to HBM as whole
+          // 256-byte rows.
+          constexpr int kOutRows = C / kChainWaves;
           const size_t row_bytes = v_stride * sizeof(uint16_t);
+          char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D + v0 + 16 * u);
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-              const uint32_t olane = uint32_t(16 * tb + c) * uint32_t(row_bytes) + uint32_t(8 * g);
-              if (L == C || 16 * tb + c < L)
-                store_b64_saddr(obase, olane, cvt_pk_bf16(OT[u][tb][0], OT[u][tb][1]),
-                                cvt_pk_bf16(OT[u][tb][2], OT[u][tb][3]));
-            }
+          for (int q4 = 0; q4 < kOutRows / 4; ++q4) {
+            const int row = kOutRows * (v0 / kRowsPerWave) + 4 * q4 + (lane >> 4);
+            const u32x4_t d = *reinterpret_cast<const u32x4_t*>(&raw.q[kb_buf][raw_off(row, 8 * c)]);
+            if (L == C || row < L) store_b128_saddr(obase, uint32_t(row) * uint32_t(row_bytes) + uint32_t(16 * c), d);
           }
         }
         // K^T fragments of the next k-block pair are read before the products of
@@ -869,12 +907,12 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) Sacc[u][kb0 + j] *= egL;
+            for (int u = 0; u < kTiles; ++u) Sacc[u][kb0 + j] *= egL;
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
               asm volatile("" : "+v"(fa[j][p]));
 #pragma unroll
-              for (int u = 0; u < 2; ++u) Sacc[u][kb0 + j] = mfma16(fa[j][p], Vdb[u][p], Sacc[u][kb0 + j]);
+              for (int u = 0; u < kTiles; ++u) Sacc[u][kb0 + j] = mfma16(fa[j][p], Vdb[u][p], Sacc[u][kb0 + j]);
             }
           }
           if (kb0 == 2) load_fa(4, fa);     // for P3b
@@ -893,13 +931,16 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           mul_kf(0, kf_lo);
           mul_kf(2, kf_hi);
         }
-        lds_barrier_keep<15>();   // K (both buffers) stays untouched in P3b and P1
+        // K (both buffers) stays untouched in P3b and P1; the staged output
+        // tile written in P3a is older than the 8 reads that may stay in flight
+        if (half == 0) lds_barrier_keep<8>();
+        else lds_barrier_keep<15>();
       }
     }
     asm volatile("" : "+v"(g), "+v"(c));
     float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < kTiles; ++u)
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb)
         *reinterpret_cast<f32x4*>(dst + size_t(16 * u) * D + 16 * kb + 4 * g) = Sacc[u][kb];
@@ -919,7 +960,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         gate_compute(0);
         if (n_chunks > 1) load_ab(1);
       }
-      if (n_chunks > 1) copy_kq(1);
+      if (n_chunks > 1) copy_k(1);   // Q of chunk 1 is copied in P1 of chunk 0
       lds_barrier();
       tiles_A(gbuf[0], 0);
       tiles_Aba(gbuf[0], 0);
@@ -942,6 +983,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       //      loaded in P1 of ch-1, then the loads of a and b of ch+2 (prep wave 0)
       if (pw >= kPrepWaves - 2) merge16(32 * (pw - (kPrepWaves - 2)));
       tiles_P2(gbuf[ch & 1], ch & 1);   // the rest of P of chunk ch (read by the chain in P3a)
+      // Q rows of chunk ch+1 into the raw buffer of chunk ch-1 (its output tile
+      // was stored from there in P3b), first read in P3b
+      if (more) copy_q(ch + 1);
       if (more) {
         if (pw == 1) wait_vm<6>(); else wait_vm<5>();   // K of ch+1 landed; its Q copies may remain
         if (pw == 0) {
@@ -961,7 +1005,6 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       //      A tiles and the fp16 K rows (prep waves 1-3) of chunk ch+1; the chain has
       //      read Aba of ch in P1 and Tm of ch in P2
       if (more) {
-        tiles_Aba(gbuf[nb], nb);     // the chain read Aba of chunk ch in P1
         if (pw == 0) diag_rows(IC<0>{}, IC<12>{}, dx);
         else convert_k(ch + 1);
         // Q of chunk ch+1 landed (read from P3b on); the V and K copies issued
@@ -979,12 +1022,12 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       //      landed (only the new K/Q copies, 12 on prep wave 1 and 10 on prep
       //      waves 2 and 3, remain outstanding)
       if (more) {
+        tiles_Aba(gbuf[nb], nb);     // the chain read Aba of chunk ch by P2
         if (pw == 0) diag_rows(IC<12>{}, IC<16>{}, dx);
         else tiles_P1(gbuf[nb], nb);
       }
       if (ch + 2 < n_chunks) {
-        copy_q(ch + 2);
-        if (pw == 1) wait_vm<12>(); else wait_vm<10>();   // the K and Q copies of chunk ch+2 may remain
+        if (pw == 1) wait_vm<6>(); else wait_vm<5>();   // the K copies of chunk ch+2 may remain
       } else if (more) {
         wait_vm<0>();
       }
