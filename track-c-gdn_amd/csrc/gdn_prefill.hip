@@ -533,9 +533,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     int cid = c;
     asm volatile("" : "+v"(cid));
 #pragma unroll
-    for (int i = I0; i < I1; ++i) {
-      // bound the live A rows: loads of rows 4b.. are not hoisted above row 4b
-      if ((i & 3) == 0) asm volatile("" ::: "memory");
+    for (int i = I0; i < I1; ++i) {   // the A rows of the whole range are read up front
       // two partial sums (alternate 4-column blocks) halve the dependent chain
       float s0 = (i == cid) ? 1.f : 0.f, s1 = 0.f;
 #pragma unroll
