@@ -120,6 +120,29 @@ def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4):
     return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=nbytes)
 
 
+def decode_multi_bytes(B: int, T: int, HQ: int, HV: int) -> int:
+    """State read + write once, per-token inputs and outputs T times."""
+    return B * HV * 2 * D * D * 4 + T * B * (HV * (2 * D * 2 + 4) + HQ * 2 * D * 2)
+
+
+def bench_decode_multi(dev, steps, warmup, B=256, T=4, HQ=4, HV=8, sets=4):
+    x = ginp.decode_multi_inputs(B, T, HQ, HV, seed=1006)
+    g = _to(x, dev)
+    states = [g["state"]] + [g["state"].clone() for _ in range(sets - 1)]
+    outs = [torch.empty_like(g["state"]) for _ in range(sets)]
+    o = torch.empty(B, T, HV, D, dtype=torch.bfloat16, device=dev)
+    calls = [gdec.PreparedDecodeMulti(g["q"], g["k"], g["v"], states[j], g["A_log"], g["a"],
+                                      g["dt_bias"], g["b"], g["scale"], o, outs[j])
+             for j in range(sets)]
+
+    def launch(i):
+        calls[i % sets]()
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=decode_multi_bytes(B, T, HQ, HV), B=B,
+                T=T)
+
+
 def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     w = ginp.WORKLOADS[name]
     lens = ginp.workload_lengths(name)
@@ -224,6 +247,20 @@ def main():
                             "kernel_us": round(r["kernel_ms"] * 1e3, 2)}
         print(f"# decode B=256: {ms*1e3:.2f} us/step, kernel {r['kernel_ms']*1e3:.2f} us, "
               f"{kgbs:.0f} GB/s ({kgbs/HBM_PEAK_GBS*100:.1f}% of HBM peak)",
+              file=sys.stderr, flush=True)
+        # multi-token decode (4 tokens per sequence per launch; an extension)
+        r = bench_decode_multi(dev, args.steps // 2, args.warmup)
+        kus = r["kernel_ms"] * 1e3
+        mgbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+        line["decode_multi"] = {
+            "workload": "decode_multi_b256_t4_qk4_v8", "batch": r["B"], "tokens_per_seq": r["T"],
+            "kernel_us": round(kus, 2), "tokens_per_s": round(r["B"] * r["T"] / (kus * 1e-6), 1),
+            "single_step_us_x4": round(4 * line["roofline"]["kernel_us"], 2),
+            "roofline": {"bound": "hbm", "achieved": round(mgbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(mgbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_launch": r["bytes"]}}
+        print(f"# decode multi B=256 T=4: kernel {kus:.2f} us ({mgbs:.0f} GB/s of algorithmic "
+              f"bytes) vs 4 single steps {4 * line['roofline']['kernel_us']:.1f} us",
               file=sys.stderr, flush=True)
 
     if args.only in ("all", "prefill"):

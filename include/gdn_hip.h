@@ -76,6 +76,25 @@ int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         int B, int HQ, int HV, float scale, void* stream);
 
 /*
+ * T consecutive decode steps per sequence (multi-token / speculative decode):
+ * for t = 0..T-1 in order, the step of gdn_decode_fwd with token t's inputs,
+ * the state kept on chip in between (read once, written once).
+ * No reference counterpart: the reference decode asserts one token per call
+ * (gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py:117-119); this
+ * serves callers that verify several draft tokens per sequence.
+ *   q, k : [B, T, HQ, D] bf16;  v : [B, T, HV, D] bf16;  a, b : [B, T, HV] bf16;
+ *   out  : [B, T, HV, D] bf16;  state / new_state : [B, HV, V, K] fp32 as in
+ *   gdn_decode_fwd (state NULL = zeros; new_state may equal state).
+ * T must be >= 1.  The result equals T successive gdn_decode_fwd calls bit
+ * for bit.
+ */
+int gdn_decode_multi_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const float* state, float* new_state,
+                         const float* A_log, const uint16_t* a, const float* dt_bias,
+                         const uint16_t* b, uint16_t* out,
+                         int B, int T, int HQ, int HV, float scale, void* stream);
+
+/*
  * Workspace bytes gdn_prefill_fwd needs for this problem (may be 0).
  */
 size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV);

@@ -29,6 +29,7 @@ SIGNATURES = {
     "gdn_error_string": (ctypes.c_char_p, [_I]),
     "gdn_decode_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "gdn_decode_pool_fwd": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
+    "gdn_decode_multi_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
     "gdn_prefill_workspace_bytes": (_S, [_I, _I, _I, _I]),
     "gdn_prefill_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                              _P, _P, _P, _S, _P]),

@@ -34,6 +34,7 @@ constexpr int kRowsPerWave = D / kWavesPerHead;   // 16
 constexpr int kRowsPerLane = kRowsPerWave / 4;    // 4 (4 DPP rows per wave)
 constexpr int kThreadsPerHead = kWavesPerHead * kWave;
 static_assert(kRowsPerLane == 4, "v is read and o written as 4 bf16 per lane");
+constexpr int kTokBlock = 16;     // tokens staged in LDS at a time (multi-token decode)
 
 template <bool kNonTemporal>
 __device__ __forceinline__ f32x4 load_state(const f32x4* p) {
@@ -161,6 +162,130 @@ __global__ __launch_bounds__(kThreadsPerHead, 8) void gdn_decode_kernel(
   }
 }
 
+// Multi-token decode: T tokens of each sequence applied in order with the
+// state held in registers in between (one state read and one state write for
+// the T steps).  Token t of sequence n uses q, k [n, t, hq], v [n, t, hv] and
+// a, b [n, t, hv]; its output goes to out [n, t, hv].  The per-token
+// arithmetic is the single-step kernel's, in the same order, so T steps here
+// give the same bits as T launches of gdn_decode_kernel.
+template <bool kNonTemporal>
+__global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* state_in, float* state_out,
+    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
+    uint16_t* __restrict__ out, int T, int HQ, int HV, float scale) {
+  const int ratio = HV / HQ;
+  const int n = blockIdx.x / HV;
+  const int hv = blockIdx.x - n * HV;
+  const int hq = hv / ratio;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row0 = (wave % kWavesPerHead) * kRowsPerWave;
+  const int rsub = lane >> 4;
+  const int c = lane & 15;
+  const int rbase = row0 + rsub * kRowsPerLane;
+  const size_t sbase = (size_t(n) * HV + hv) * size_t(D) * D;
+
+  f32x4 s[kRowsPerLane][2];
+  if (state_in != nullptr) {
+    const float* sp = state_in + sbase + size_t(rbase) * D;
+#pragma unroll
+    for (int j = 0; j < kRowsPerLane; ++j) {
+      s[j][0] = load_state<kNonTemporal>(reinterpret_cast<const f32x4*>(sp + j * D + 4 * c));
+      s[j][1] = load_state<kNonTemporal>(reinterpret_cast<const f32x4*>(sp + j * D + 64 + 4 * c));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowsPerLane; ++j) {
+      s[j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  const float a_log_exp = expf(A_log[hv]);
+  const float dtb = dt_bias[hv];
+
+  // Token inputs go through LDS in blocks of kTokBlock tokens: k, q and this
+  // head's v rows (256 B each per token) and a, b, copied by the whole
+  // workgroup with 16-byte loads, so the serial token loop reads LDS, not HBM.
+  __shared__ __align__(16) uint16_t tk[kTokBlock][3][D];   // k | q | v
+  __shared__ float tab[kTokBlock][2];                       // a, b (as fp32)
+  for (int t0 = 0; t0 < T; t0 += kTokBlock) {
+    const int nt = min(kTokBlock, T - t0);
+    __syncthreads();     // the previous block's reads are done
+    for (int e = threadIdx.x; e < nt * 3 * (D / 8); e += kThreadsPerHead) {
+      const int t = e / (3 * (D / 8)), r = e - t * (3 * (D / 8));
+      const int which = r / (D / 8), chunk = r - which * (D / 8);
+      const size_t tok = size_t(n) * T + t0 + t;
+      const uint16_t* src = which == 0 ? k + (tok * HQ + hq) * D
+                          : which == 1 ? q + (tok * HQ + hq) * D
+                                       : v + (tok * HV + hv) * D;
+      *reinterpret_cast<uint4*>(&tk[t][which][8 * chunk]) = *reinterpret_cast<const uint4*>(src + 8 * chunk);
+    }
+    if (threadIdx.x < 2 * nt) {
+      const int t = threadIdx.x >> 1;
+      const size_t tok = size_t(n) * T + t0 + t;
+      tab[t][threadIdx.x & 1] = bf16_bits_to_f32((threadIdx.x & 1) ? b[tok * HV + hv] : a[tok * HV + hv]);
+    }
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+      float kk[8], qq[8], vv[kRowsPerLane];
+      {
+        const uint2 klo = *reinterpret_cast<const uint2*>(&tk[t][0][4 * c]);
+        const uint2 khi = *reinterpret_cast<const uint2*>(&tk[t][0][64 + 4 * c]);
+        const uint2 qlo = *reinterpret_cast<const uint2*>(&tk[t][1][4 * c]);
+        const uint2 qhi = *reinterpret_cast<const uint2*>(&tk[t][1][64 + 4 * c]);
+        const uint2 vw = *reinterpret_cast<const uint2*>(&tk[t][2][rbase]);
+        unpack_bf16x2(klo.x, kk[0], kk[1]); unpack_bf16x2(klo.y, kk[2], kk[3]);
+        unpack_bf16x2(khi.x, kk[4], kk[5]); unpack_bf16x2(khi.y, kk[6], kk[7]);
+        unpack_bf16x2(qlo.x, qq[0], qq[1]); unpack_bf16x2(qlo.y, qq[2], qq[3]);
+        unpack_bf16x2(qhi.x, qq[4], qq[5]); unpack_bf16x2(qhi.y, qq[6], qq[7]);
+        unpack_bf16x2(vw.x, vv[0], vv[1]); unpack_bf16x2(vw.y, vv[2], vv[3]);
+      }
+      // gates (reference DEC:59-65), uniform per wave
+      const float g = expf(-a_log_exp * softplus_thresh20(tab[t][0] + dtb));
+      const float beta = 1.0f / (1.0f + expf(-tab[t][1]));
+      float kq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kq = fmaf(kk[e], qq[e], kq);
+      kq = row16_sum(kq);
+      float o_out[kRowsPerLane];
+#pragma unroll
+      for (int j = 0; j < kRowsPerLane; ++j) {
+        float x[8] = {s[j][0].x, s[j][0].y, s[j][0].z, s[j][0].w,
+                      s[j][1].x, s[j][1].y, s[j][1].z, s[j][1].w};
+        float pk = 0.f, pq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[e] *= g;
+          pk = fmaf(x[e], kk[e], pk);
+          pq = fmaf(x[e], qq[e], pq);
+        }
+        pk = row16_sum(pk);
+        pq = row16_sum(pq);
+        const float delta = beta * (vv[j] - pk);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = fmaf(delta, kk[e], x[e]);
+        o_out[j] = scale * fmaf(delta, kq, pq);
+        s[j][0] = f32x4{x[0], x[1], x[2], x[3]};
+        s[j][1] = f32x4{x[4], x[5], x[6], x[7]};
+      }
+      if (c == 0) {
+        uint2 w;
+        w.x = pack_bf16x2(o_out[0], o_out[1]);
+        w.y = pack_bf16x2(o_out[2], o_out[3]);
+        *reinterpret_cast<uint2*>(out + ((size_t(n) * T + t0 + t) * HV + hv) * D + rbase) = w;
+      }
+    }
+  }
+  float* dst = state_out + sbase + size_t(rbase) * D;
+#pragma unroll
+  for (int j = 0; j < kRowsPerLane; ++j) {
+    store_state<kNonTemporal>(reinterpret_cast<f32x4*>(dst + j * D + 4 * c), s[j][0]);
+    store_state<kNonTemporal>(reinterpret_cast<f32x4*>(dst + j * D + 64 + 4 * c), s[j][1]);
+  }
+}
+
 int check_decode_args(const void* q, const void* k, const void* v, const void* state_out,
                       const void* A_log, const void* a, const void* dt_bias, const void* b,
                       const void* out, int B, int HQ, int HV) {
@@ -183,7 +308,32 @@ int launch_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
   return err == hipSuccess ? GDN_OK : -int(err);
 }
 
+int launch_decode_multi(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        const float* state_in, float* state_out, const float* A_log,
+                        const uint16_t* a, const float* dt_bias, const uint16_t* b, uint16_t* out,
+                        int B, int T, int HQ, int HV, float scale, void* stream) {
+  if (B == 0) return GDN_OK;
+  const dim3 grid(unsigned(B) * unsigned(HV));
+  const dim3 block(kThreadsPerHead);
+  hipLaunchKernelGGL(gdn_decode_multi_kernel<true>, grid, block, 0, static_cast<hipStream_t>(stream),
+                     q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, T, HQ, HV, scale);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? GDN_OK : -int(err);
+}
+
 }  // namespace
+
+extern "C" int gdn_decode_multi_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    const float* state, float* new_state, const float* A_log,
+                                    const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                                    uint16_t* out, int B, int T, int HQ, int HV, float scale,
+                                    void* stream) {
+  const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (T < 1) return GDN_ERR_SHAPE;
+  return launch_decode_multi(q, k, v, state, new_state, A_log, a, dt_bias, b, out, B, T, HQ, HV,
+                             scale, stream);
+}
 
 extern "C" int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               const float* state, float* new_state, const float* A_log,

@@ -10,6 +10,9 @@ Host-side mirror of the reference decode entry point
 * :func:`gdn_decode` -- the same step for any head layout with
   ``HV % HQ == 0`` (e.g. 16 qk-heads / 32 v-heads).
 * :func:`decode_pool_` -- in-place step against a slot-indexed state pool.
+* :func:`gdn_decode_multi` -- T consecutive steps per sequence in one launch
+  (multi-token / speculative decode; the reference accepts one token per
+  call, DEC:117-119).
 
 All compute runs in the HIP kernel of libgdn_hip.so on torch's current
 stream; there is no CPU path.
@@ -123,6 +126,51 @@ def run_dps(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
 
 
 @torch.no_grad()
+def gdn_decode_multi(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
+                     new_state=None):
+    """T decode steps per sequence, applied in token order, in one launch.
+
+    ``q, k [B, T, HQ, 128]``, ``v [B, T, HV, 128]`` bf16; ``a, b [B, T, HV]``
+    bf16; ``state [B, HV, 128, 128]`` fp32 or ``None``; ``A_log, dt_bias
+    [HV]``.  Returns ``(output [B, T, HV, 128] bf16, new_state)``, equal bit
+    for bit to T successive :func:`gdn_decode` calls; ``new_state`` may be the
+    ``state`` tensor itself.
+    """
+    assert q.is_cuda and k.is_cuda and v.is_cuda, "decode inputs must be GPU tensors"
+    assert q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+    assert a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
+    assert q.dim() == 4 and q.shape[3] == D and k.shape == q.shape
+    B, T, nq, _ = q.shape
+    assert T >= 1, "at least one token per sequence"
+    assert v.dim() == 4 and v.shape[:2] == (B, T) and v.shape[3] == D
+    nv = v.shape[2]
+    assert nv % nq == 0, "v-heads must be a multiple of qk-heads"
+    assert A_log.numel() == nv and dt_bias.numel() == nv
+    assert a.numel() == B * T * nv and b.numel() == B * T * nv
+    scale = _resolve_scale(scale, D)
+    if state is not None:
+        assert state.is_cuda and state.dtype == torch.float32 and state.shape == (B, nv, D, D)
+        if not state.is_contiguous():
+            state = state.contiguous()
+    if output is None:
+        output = torch.empty(B, T, nv, D, dtype=q.dtype, device=q.device)
+    if new_state is None:
+        new_state = torch.empty(B, nv, D, D, dtype=torch.float32, device=q.device)
+    assert output.dtype == torch.bfloat16 and output.is_contiguous()
+    assert output.numel() == B * T * nv * D
+    assert new_state.dtype == torch.float32 and new_state.is_contiguous()
+    assert new_state.shape == (B, nv, D, D)
+    A_log, dt_bias = _gates(A_log, dt_bias)
+    q, k, v, a, b = (t.contiguous() for t in (q, k, v, a, b))
+    rc = _capi.lib().gdn_decode_multi_fwd(
+        _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
+        _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
+        B, T, nq, nv, float(scale), _capi.stream_handle(q.device))
+    _capi.check(rc, "gdn_decode_multi_fwd")
+    return output, new_state
+
+
+@torch.no_grad()
 def decode_pool_(q, k, v, state_pool, slot_ids, A_log, a, dt_bias, b, scale=None, *,
                  output=None):
     """One decode step against ``state_pool[slot_ids[n]]``, updated in place.
@@ -180,3 +228,38 @@ class PreparedDecode:
         rc = self._fn(*self._args)
         if rc:
             _capi.check(rc, "gdn_decode_fwd")
+
+
+class PreparedDecodeMulti:
+    """T decode steps per sequence on fixed buffers, launched by one C call.
+
+    The multi-token counterpart of :class:`PreparedDecode` (same contract:
+    validated once, ``__call__`` only enqueues the kernel).
+    """
+
+    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
+        assert q.dim() == 4 and q.shape[3] == D and k.shape == q.shape
+        B, T, nq, _ = q.shape
+        assert T >= 1 and v.dim() == 4 and v.shape[:2] == (B, T) and v.shape[3] == D
+        nv = v.shape[2]
+        assert nv % nq == 0 and a.numel() == B * T * nv and b.numel() == B * T * nv
+        assert state is None or (state.is_contiguous() and state.dtype == torch.float32
+                                 and state.shape == (B, nv, D, D))
+        assert output.dtype == torch.bfloat16 and output.is_contiguous()
+        assert output.numel() == B * T * nv * D
+        assert new_state.dtype == torch.float32 and new_state.is_contiguous()
+        assert new_state.shape == (B, nv, D, D)
+        for t in (q, k, v, a, b):
+            assert t.is_contiguous() and t.dtype == torch.bfloat16
+        A_log, dt_bias = _gates(A_log, dt_bias)
+        self._keep = (q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+        self._fn = _capi.lib().gdn_decode_multi_fwd
+        self._args = (
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
+            _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
+            B, T, nq, nv, float(_resolve_scale(scale, D)), _capi.stream_handle(q.device))
+
+    def __call__(self) -> None:
+        rc = self._fn(*self._args)
+        if rc:
+            _capi.check(rc, "gdn_decode_multi_fwd")

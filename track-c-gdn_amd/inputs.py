@@ -52,6 +52,21 @@ def decode_inputs(B: int, HQ: int = 4, HV: int = 8, seed: int = 1001,
                 scale=1.0 / math.sqrt(head_dim))
 
 
+def decode_multi_inputs(B: int, T: int, HQ: int = 4, HV: int = 8, seed: int = 1005,
+                        with_state: bool = True, head_dim: int = D) -> Dict[str, torch.Tensor]:
+    """Inputs of T consecutive decode steps per sequence at batch ``B`` (CPU tensors)."""
+    gen = torch.Generator().manual_seed(seed)
+    q = _unit_rows(torch.randn(B, T, HQ, head_dim, generator=gen)).to(torch.bfloat16)
+    k = _unit_rows(torch.randn(B, T, HQ, head_dim, generator=gen)).to(torch.bfloat16)
+    v = torch.randn(B, T, HV, head_dim, generator=gen).to(torch.bfloat16)
+    state = (torch.randn(B, HV, head_dim, head_dim, generator=gen) * 0.02) if with_state else None
+    A_log, dt_bias = _common_gates(gen, HV)
+    a = torch.randn(B, T, HV, generator=gen).to(torch.bfloat16)
+    b = torch.randn(B, T, HV, generator=gen).to(torch.bfloat16)
+    return dict(q=q, k=k, v=v, state=state, A_log=A_log, a=a, dt_bias=dt_bias, b=b,
+                scale=1.0 / math.sqrt(head_dim))
+
+
 def prefill_inputs(lengths: Sequence[int], HQ: int = 4, HV: int = 8, seed: int = 1002,
                    with_state: bool = False, cu_dtype=torch.int64,
                    head_dim: int = D) -> Dict[str, torch.Tensor]:
