@@ -135,7 +135,8 @@ def test_prefill_weak_decay_precision(device):
     _check(o, s, *_oracle(x))
 
 
-@pytest.mark.parametrize("name", ["prefill_t4096_n1_qk4_v8", "prefill_varlen16_qk4_v8"])
+@pytest.mark.parametrize("name", ["prefill_t4096_n1_qk4_v8", "prefill_varlen16_qk4_v8",
+                                  "prefill_varlen8_t32768_qk16_v32"])
 def test_prefill_benchmark_workloads(device, name):
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
