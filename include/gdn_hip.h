@@ -37,6 +37,14 @@ extern "C" {
 #define GDN_ERR_SHAPE (-1002)     /* an unsupported size or head configuration */
 #define GDN_ERR_WORKSPACE (-1003) /* workspace missing or too small */
 
+/* Option bits of the *_ex entry points and gdn_decode_multi_fwd.
+ * GDN_QK_L2NORM: every q and k row (128 elements) is used L2-normalised,
+ *   x (sum x^2 + 1e-6)^(-1/2), computed in fp32 inside the kernel.  The
+ *   reference expects normalised inputs from its caller and has no such
+ *   option. */
+#define GDN_QK_L2NORM 1
+#define GDN_FLAGS_ALL 1
+
 /* ABI version of the loaded library (GDN_ABI_VERSION). */
 int gdn_abi_version(void);
 
@@ -59,6 +67,16 @@ int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                    const float* A_log, const uint16_t* a, const float* dt_bias,
                    const uint16_t* b, uint16_t* out,
                    int B, int HQ, int HV, float scale, void* stream);
+
+/*
+ * gdn_decode_fwd with option bits (GDN_QK_L2NORM); flags = 0 is
+ * gdn_decode_fwd.  Unknown bits: GDN_ERR_SHAPE.
+ */
+int gdn_decode_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                      const float* state, float* new_state,
+                      const float* A_log, const uint16_t* a, const float* dt_bias,
+                      const uint16_t* b, uint16_t* out,
+                      int B, int HQ, int HV, float scale, int flags, void* stream);
 
 /*
  * One decode step against a state pool, updated in place:
@@ -85,14 +103,14 @@ int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
  *   q, k : [B, T, HQ, D] bf16;  v : [B, T, HV, D] bf16;  a, b : [B, T, HV] bf16;
  *   out  : [B, T, HV, D] bf16;  state / new_state : [B, HV, V, K] fp32 as in
  *   gdn_decode_fwd (state NULL = zeros; new_state may equal state).
- * T must be >= 1.  The result equals T successive gdn_decode_fwd calls bit
- * for bit.
+ * T must be >= 1; flags as for gdn_decode_ex_fwd.  The result equals T
+ * successive gdn_decode_ex_fwd calls with the same flags bit for bit.
  */
 int gdn_decode_multi_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                          const float* state, float* new_state,
                          const float* A_log, const uint16_t* a, const float* dt_bias,
                          const uint16_t* b, uint16_t* out,
-                         int B, int T, int HQ, int HV, float scale, void* stream);
+                         int B, int T, int HQ, int HV, float scale, int flags, void* stream);
 
 /*
  * Workspace bytes gdn_prefill_fwd needs for this problem (may be 0).
@@ -122,6 +140,18 @@ int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     int HQ, int HV, float scale,
                     uint16_t* out, float* final_state,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * gdn_prefill_fwd with option bits (GDN_QK_L2NORM); flags = 0 is
+ * gdn_prefill_fwd.  Unknown bits: GDN_ERR_SHAPE.
+ */
+int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                       const float* state, const float* A_log, const uint16_t* a,
+                       const float* dt_bias, const uint16_t* b,
+                       const void* cu_seqlens, int cu_is_int32, int N, int T,
+                       int HQ, int HV, float scale,
+                       uint16_t* out, float* final_state,
+                       void* workspace, size_t workspace_bytes, int flags, void* stream);
 
 #ifdef __cplusplus
 }

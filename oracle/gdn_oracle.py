@@ -29,6 +29,9 @@ How each function is pinned (tests/test_oracle.py):
                       closed forms at T = 1, split / varlen invariances.
 * prefill_chunked  -- equals prefill_recurrent in float64 at chunk sizes
                       1, 16, 32, 64, 128 including ragged tails.
+* qk_l2norm        -- torch.nn.functional.normalize where eps is negligible,
+                      the closed form c/sqrt(c^2 + eps) on scaled unit vectors,
+                      zero maps to zero, sign/permutation equivariance.
 """
 
 from __future__ import annotations
@@ -50,6 +53,7 @@ __all__ = [
     "prefill_recurrent",
     "prefill_chunked",
     "default_scale",
+    "qk_l2norm",
 ]
 
 
@@ -58,6 +62,22 @@ def default_scale(scale: Optional[float], head_dim: int) -> float:
     if scale is None or float(scale) == 0.0:
         return 1.0 / math.sqrt(head_dim)
     return float(scale)
+
+
+L2NORM_EPS = 1e-6
+
+
+def qk_l2norm(x: torch.Tensor, eps: float = L2NORM_EPS, dtype=torch.float64) -> torch.Tensor:
+    """``x * (sum_d x_d^2 + eps)^(-1/2)`` over the last (head) dimension.
+
+    The reference has no counterpart: its operators take q and k already
+    L2-normalised by the caller (the benchmark inputs are drawn that way).
+    This is the normalisation the ``qk_l2norm`` option applies inside the
+    kernels to raw bf16 q/k before the decode step (DEC:72-76) or the chunked
+    prefill (PRE:1049-1129); the result is not rounded back to bf16.
+    """
+    x = x.to(dtype)
+    return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
 
 
 # ----------------------------------------------------------------------------

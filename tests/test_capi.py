@@ -21,7 +21,8 @@ def declared_functions():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "gdn_abi_version", "gdn_error_string", "gdn_decode_fwd", "gdn_decode_pool_fwd",
-        "gdn_decode_multi_fwd", "gdn_prefill_workspace_bytes", "gdn_prefill_fwd"])
+        "gdn_decode_multi_fwd", "gdn_decode_ex_fwd", "gdn_prefill_workspace_bytes",
+        "gdn_prefill_fwd", "gdn_prefill_ex_fwd"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -52,8 +53,12 @@ def test_argument_errors_return_before_launch():
     assert lib.gdn_decode_fwd(P, P, P, P, P, P, P, P, P, P, -1, 4, 8, 1.0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_decode_fwd(P, P, P, P, P, P, P, P, P, P, 1, 0, 8, 1.0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_decode_pool_fwd(P, P, P, P, 4, None, P, P, P, P, P, 1, 4, 8, 1.0, None) == capi.GDN_ERR_NULL
-    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, None, 1, 2, 4, 8, 1.0, None) == capi.GDN_ERR_NULL
-    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, P, 1, 0, 4, 8, 1.0, None) == capi.GDN_ERR_SHAPE
-    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, P, 1, 2, 4, 6, 1.0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, None, 1, 2, 4, 8, 1.0, 0, None) == capi.GDN_ERR_NULL
+    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, P, 1, 0, 4, 8, 1.0, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, P, 1, 2, 4, 6, 1.0, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_multi_fwd(P, P, P, P, P, P, P, P, P, P, 1, 2, 4, 8, 1.0, 2, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_ex_fwd(P, P, P, P, P, P, P, P, P, P, 1, 4, 8, 1.0, 4, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_decode_ex_fwd(None, P, P, P, P, P, P, P, P, P, 1, 4, 8, 1.0, 1, None) == capi.GDN_ERR_NULL
+    assert lib.gdn_prefill_ex_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 0, 8, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_fwd(None, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 0, None) == capi.GDN_ERR_NULL
     assert lib.gdn_prefill_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 7, 1.0, P, P, None, 0, None) == capi.GDN_ERR_SHAPE

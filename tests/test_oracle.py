@@ -269,3 +269,45 @@ def test_prefill_reference_storage_error_is_bf16_sized():
     _, S_bf = O.prefill_chunked(q, k, v, S, A_log, a, dt_bias, b, cu, None, reference_storage=True)
     rel = float((S_bf - S_ex).norm() / S_ex.norm())
     assert 1e-4 < rel < 1e-2
+
+
+# --------------------------------------------------------------------------- q/k L2-norm
+
+def test_qk_l2norm_matches_normalize_when_eps_negligible():
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(5, 3, 128, generator=g, dtype=DT) * 7.0      # |x|^2 ~ 6e3 >> eps
+    ref = F.normalize(x, dim=-1)
+    out = O.qk_l2norm(x)
+    # relative effect of eps on the norm is eps / (2 |x|^2) < 1e-9
+    torch.testing.assert_close(out, ref, atol=1e-9, rtol=1e-9)
+    assert out.dtype == DT and out.shape == x.shape
+
+
+@pytest.mark.parametrize("c", [0.0, 1e-4, 1e-3, 0.5, 1.0, 3.0])
+def test_qk_l2norm_closed_form_on_scaled_unit_vectors(c):
+    D = 128
+    for i in (0, 17, 127):
+        x = torch.zeros(D, dtype=DT)
+        x[i] = -c if i == 17 else c
+        out = O.qk_l2norm(x)
+        expect = torch.zeros(D, dtype=DT)
+        expect[i] = x[i] / math.sqrt(c * c + 1e-6)
+        torch.testing.assert_close(out, expect, atol=0.0, rtol=1e-14)
+
+
+def test_qk_l2norm_equivariance_and_eps_argument():
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(4, 128, generator=g, dtype=DT) * 0.01       # eps matters at this size
+    perm = torch.randperm(128, generator=g)
+    sign = torch.where(torch.rand(128, generator=g) < 0.5, -1.0, 1.0).to(DT)
+    out = O.qk_l2norm(x)
+    torch.testing.assert_close(O.qk_l2norm(x[:, perm] * sign), out[:, perm] * sign,
+                               atol=1e-15, rtol=1e-13)
+    # the output norm is |x| / sqrt(|x|^2 + eps), strictly below 1
+    n2 = (x * x).sum(-1)
+    torch.testing.assert_close(out.norm(dim=-1), torch.sqrt(n2 / (n2 + 1e-6)), atol=0, rtol=1e-13)
+    assert bool((out.norm(dim=-1) < 1).all())
+    # eps = 0 is plain normalisation; bf16 input is widened, not rounded
+    torch.testing.assert_close(O.qk_l2norm(x, eps=0.0), F.normalize(x, dim=-1), atol=0, rtol=1e-14)
+    xb = x.to(torch.bfloat16)
+    assert O.qk_l2norm(xb).dtype == DT

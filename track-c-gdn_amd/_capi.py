@@ -18,6 +18,7 @@ GDN_OK = 0
 GDN_ERR_NULL = -1001
 GDN_ERR_SHAPE = -1002
 GDN_ERR_WORKSPACE = -1003
+GDN_QK_L2NORM = 1
 
 # Every symbol include/gdn_hip.h declares, with (restype, argtypes).
 _P = ctypes.c_void_p
@@ -29,10 +30,13 @@ SIGNATURES = {
     "gdn_error_string": (ctypes.c_char_p, [_I]),
     "gdn_decode_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "gdn_decode_pool_fwd": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
-    "gdn_decode_multi_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
+    "gdn_decode_ex_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P]),
+    "gdn_decode_multi_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P]),
     "gdn_prefill_workspace_bytes": (_S, [_I, _I, _I, _I]),
     "gdn_prefill_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                              _P, _P, _P, _S, _P]),
+    "gdn_prefill_ex_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
+                                _P, _P, _P, _S, _I, _P]),
 }
 
 _lib = None

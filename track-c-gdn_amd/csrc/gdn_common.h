@@ -80,4 +80,43 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// q / k L2 normalisation (optional, GDN_QK_L2NORM): a row x of 128 elements
+// is used as x (sum x^2 + 1e-6)^(-1/2), all in fp32 (no intermediate rounding;
+// the bf16 squares are exact in fp32, v_rsq_f32 is within 1 ulp).
+constexpr float kL2NormEps = 1e-6f;
+
+__device__ __forceinline__ float l2norm_rsqrt(float sum_sq) {
+  return __builtin_amdgcn_rsqf(sum_sq + kL2NormEps);
+}
+
+// The factor (sum x^2 + 1e-6)^(-1/2) of a row held 8 per lane by the 16 lanes
+// of a DPP row (every lane of the row receives it).
+__device__ __forceinline__ float l2norm_factor_row16(const float (&x)[8]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+  return l2norm_rsqrt(row16_sum(ss));
+}
+
+// Sum of squares of 8 packed bf16 values (two per dword), one v_dot2 each.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float sum_sq_bf16x8(uint4 w) {
+  float s = 0.f;
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x),
+                                      __builtin_bit_cast(bf16x2_t, w.x), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y),
+                                      __builtin_bit_cast(bf16x2_t, w.y), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z),
+                                      __builtin_bit_cast(bf16x2_t, w.z), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w),
+                                      __builtin_bit_cast(bf16x2_t, w.w), s, false);
+  return s;
+}
+
+__device__ __forceinline__ void l2norm_row16(float (&x)[8]) {
+  const float r = l2norm_factor_row16(x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= r;
+}
+
 }  // namespace gdn

@@ -58,8 +58,8 @@ __device__ __forceinline__ void load_bf16x8_split(const uint16_t* base, int c, f
   unpack_bf16x2(hi.y, x[6], x[7]);
 }
 
-template <bool kNonTemporal>
-__global__ __launch_bounds__(kThreadsPerHead, 8) void gdn_decode_kernel(
+template <bool kNonTemporal, bool kL2>
+__global__ __launch_bounds__(kThreadsPerHead, kL2 ? 6 : 8) void gdn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* state_in, float* state_out,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
@@ -112,6 +112,10 @@ __global__ __launch_bounds__(kThreadsPerHead, 8) void gdn_decode_kernel(
   float kk[8], qq[8];
   load_bf16x8_split(k + qk_off, c, kk);
   load_bf16x8_split(q + qk_off, c, qq);
+  if constexpr (kL2) {      // option GDN_QK_L2NORM
+    l2norm_row16(kk);
+    l2norm_row16(qq);
+  }
   float vv[kRowsPerLane];
   {
     const uint2 vw = *reinterpret_cast<const uint2*>(v + nh * D + rbase);
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
     const uint16_t* __restrict__ v, const float* state_in, float* state_out,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
-    uint16_t* __restrict__ out, int T, int HQ, int HV, float scale) {
+    uint16_t* __restrict__ out, int T, int HQ, int HV, float scale, int flags) {
   const int ratio = HV / HQ;
   const int n = blockIdx.x / HV;
   const int hv = blockIdx.x - n * HV;
@@ -242,6 +246,10 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
         unpack_bf16x2(qhi.x, qq[4], qq[5]); unpack_bf16x2(qhi.y, qq[6], qq[7]);
         unpack_bf16x2(vw.x, vv[0], vv[1]); unpack_bf16x2(vw.y, vv[2], vv[3]);
       }
+      if (flags & GDN_QK_L2NORM) {
+        l2norm_row16(kk);
+        l2norm_row16(qq);
+      }
       // gates (reference DEC:59-65), uniform per wave
       const float g = expf(-a_log_exp * softplus_thresh20(tab[t][0] + dtb));
       const float beta = 1.0f / (1.0f + expf(-tab[t][1]));
@@ -297,13 +305,18 @@ int check_decode_args(const void* q, const void* k, const void* v, const void* s
 int launch_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state_in,
                   float* state_out, const float* A_log, const uint16_t* a, const float* dt_bias,
                   const uint16_t* b, uint16_t* out, const int32_t* slot_ids, int B, int HQ, int HV,
-                  int pool_size, float scale, void* stream) {
+                  int pool_size, float scale, int flags, void* stream) {
   if (B == 0) return GDN_OK;
   const dim3 grid(unsigned(B) * unsigned(HV));
   const dim3 block(kThreadsPerHead);
-  hipLaunchKernelGGL(gdn_decode_kernel<true>, grid, block, 0, static_cast<hipStream_t>(stream),
-                     q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, slot_ids, HQ, HV,
-                     pool_size, scale);
+  if (flags & GDN_QK_L2NORM)
+    hipLaunchKernelGGL((gdn_decode_kernel<true, true>), grid, block, 0, static_cast<hipStream_t>(stream),
+                       q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, slot_ids, HQ, HV,
+                       pool_size, scale);
+  else
+    hipLaunchKernelGGL((gdn_decode_kernel<true, false>), grid, block, 0, static_cast<hipStream_t>(stream),
+                       q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, slot_ids, HQ, HV,
+                       pool_size, scale);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : -int(err);
 }
@@ -311,12 +324,13 @@ int launch_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
 int launch_decode_multi(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         const float* state_in, float* state_out, const float* A_log,
                         const uint16_t* a, const float* dt_bias, const uint16_t* b, uint16_t* out,
-                        int B, int T, int HQ, int HV, float scale, void* stream) {
+                        int B, int T, int HQ, int HV, float scale, int flags, void* stream) {
   if (B == 0) return GDN_OK;
   const dim3 grid(unsigned(B) * unsigned(HV));
   const dim3 block(kThreadsPerHead);
   hipLaunchKernelGGL(gdn_decode_multi_kernel<true>, grid, block, 0, static_cast<hipStream_t>(stream),
-                     q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, T, HQ, HV, scale);
+                     q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, T, HQ, HV, scale,
+                     flags);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : -int(err);
 }
@@ -327,12 +341,13 @@ extern "C" int gdn_decode_multi_fwd(const uint16_t* q, const uint16_t* k, const 
                                     const float* state, float* new_state, const float* A_log,
                                     const uint16_t* a, const float* dt_bias, const uint16_t* b,
                                     uint16_t* out, int B, int T, int HQ, int HV, float scale,
-                                    void* stream) {
+                                    int flags, void* stream) {
   const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
   if (rc != GDN_OK) return rc;
   if (T < 1) return GDN_ERR_SHAPE;
+  if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
   return launch_decode_multi(q, k, v, state, new_state, A_log, a, dt_bias, b, out, B, T, HQ, HV,
-                             scale, stream);
+                             scale, flags, stream);
 }
 
 extern "C" int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -342,7 +357,19 @@ extern "C" int gdn_decode_fwd(const uint16_t* q, const uint16_t* k, const uint16
   const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
   if (rc != GDN_OK) return rc;
   return launch_decode(q, k, v, state, new_state, A_log, a, dt_bias, b, out, nullptr, B, HQ, HV,
-                       B, scale, stream);
+                       B, scale, 0, stream);
+}
+
+extern "C" int gdn_decode_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const float* state, float* new_state, const float* A_log,
+                                 const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                                 uint16_t* out, int B, int HQ, int HV, float scale, int flags,
+                                 void* stream) {
+  const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
+  return launch_decode(q, k, v, state, new_state, A_log, a, dt_bias, b, out, nullptr, B, HQ, HV,
+                       B, scale, flags, stream);
 }
 
 extern "C" int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -355,5 +382,5 @@ extern "C" int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const u
   if (!slot_ids) return GDN_ERR_NULL;
   if (pool_size < 0) return GDN_ERR_SHAPE;
   return launch_decode(q, k, v, state_pool, state_pool, A_log, a, dt_bias, b, out, slot_ids, B,
-                       HQ, HV, pool_size, scale, stream);
+                       HQ, HV, pool_size, scale, 0, stream);
 }

@@ -263,7 +263,12 @@ using IC = std::integral_constant<int, N>;
 // phase at the end of the phase before whenever no wave overwrites them in
 // between, and its barriers leave those reads in flight.  Which wave computes
 // which tile is fixed at compile time, so tile offsets are immediates.
-template <typename CuT>
+// kL2 (option GDN_QK_L2NORM): the q and k rows are used L2-normalised.  The
+// copying waves compute each row's factor (sum x^2 + 1e-6)^(-1/2) from the
+// rows they copied, right after their wait for them, and the factors scale
+// the products: the fp16 K rows (so K S^T and the state update see k-hat),
+// the A and P tiles (row and column factors) and the e^gam factor of S Q^T.
+template <typename CuT, bool kL2>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ h0,
@@ -275,6 +280,10 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   __shared__ SmemRaw raw;
   __shared__ __align__(16) uint16_t rawV[C * D];     // V chunk (bf16, swizzled), DMA target
   __shared__ __align__(16) float gbuf[2][GSZ];       // gate data, DMA target, double-buffered
+  // L2-norm factors of the K / Q rows of the chunks of parity 0 / 1 (kL2 only)
+  __shared__ __align__(16) float nrm[kL2 ? 2 * 2 * C : 4];
+  auto nk = [&](int pb) { return &nrm[(2 * pb + 0) * C]; };
+  auto nq = [&](int pb) { return &nrm[(2 * pb + 1) * C]; };
 
   // Workgroup -> (sequence n, v-head hv).  The G = HV/HQ v-heads that share a
   // qk-head read the same K/Q rows; they get workgroup ids 8 apart, which the
@@ -367,6 +376,29 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   auto copy_q = [&](int ch) { copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1]); };
   auto copy_kq = [&](int ch) { copy_k(ch); copy_q(ch); };
   auto copy_v = [&](int ch) { copy_rows(v, v_stride, size_t(hv) * D, dma_v, ch, rawV); };
+  // L2-norm factors of the 4 n_groups rows this wave copied into buf, from the
+  // diagonal of their Gram matrix: two 16-row tiles, each one bf16 MFMA chain
+  // with the same registers as both operands (squares exact, fp32 sums).  Tile
+  // lane (g, c) supplies row c and holds Gram entries (4 g + e, c), so the
+  // diagonal entry of row c sits in lane (c / 4, c), element c % 4.  Rows past
+  // the wave's last repeat it.  Call after the wait for those copies.
+  auto norm_rows = [&](const uint16_t* buf, float* dstf) {
+    if (n_groups == 0) return;
+    const int nrows = 4 * n_groups;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int i = min(16 * tt + c, nrows - 1);
+      const int r = group_row0(0) + i;
+      bf16x8_t f[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) f[ks] = ld16_bf(&buf[raw_off(r, 32 * ks + 8 * g)]);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(f[ks], f[ks], acc);
+      const float d = (c & 2) ? ((c & 1) ? acc[3] : acc[2]) : ((c & 1) ? acc[1] : acc[0]);
+      if ((c >> 2) == g && 16 * tt + c < nrows) dstf[r] = l2norm_rsqrt(d);
+    }
+  };
   auto load_ab = [&](int ch) {      // a, b of the chunk's tokens for gate_compute (wave 0)
     const int L = chunk_len(ch);
     const size_t gi = size_t(bos + ch * C + min(lane, L - 1)) * HV + hv;
@@ -431,6 +463,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       float f[8];
       unpack_bf16x2(w.x, f[0], f[1]); unpack_bf16x2(w.y, f[2], f[3]);
       unpack_bf16x2(w.z, f[4], f[5]); unpack_bf16x2(w.w, f[6], f[7]);
+      if constexpr (kL2) {
+        const float r = nk(ch & 1)[((ptid - 64) + kCvThreads * j) / 16];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] *= r;
+      }
       _Float16* d = reinterpret_cast<_Float16*>(dst + cv_dst[j]);
       *reinterpret_cast<f16x4_t*>(d) = f16x4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
       *reinterpret_cast<f16x4_t*>(d + 8) = f16x4_t{(_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
@@ -459,8 +496,12 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
     const float gr = gd[G_L2 + 16 * ti + c];
-    const float br = gd[G_BETA + 16 * ti + c];
+    float br = gd[G_BETA + 16 * ti + c];
     const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
+    if constexpr (kL2) {
+      br *= nk(pb)[16 * ti + c];
+      acc *= *reinterpret_cast<const f32x4*>(&nk(pb)[16 * tj + 4 * g]);
+    }
     f32x4 val;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -493,6 +534,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
     const float gr = gd[G_L2 + 16 * ti + c] + scale_l2;
     const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
+    if constexpr (kL2) acc *= nq(pb)[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk(pb)[16 * tj + 4 * g]);
     f16x4_t val;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -853,7 +895,8 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           }
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
-            const float egs = gd[G_EGS + 16 * tb + c];    // scale e^gam of this lane's token
+            float egs = gd[G_EGS + 16 * tb + c];    // scale e^gam of this lane's token
+            if constexpr (kL2) egs *= nq(kb_buf)[16 * tb + c];
 #pragma unroll
             for (int u = 0; u < kTiles; ++u) OT[u][tb] *= egs;
           }
@@ -954,6 +997,10 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       copy_v(0);
       if (pw == 0) load_ab(0);
       wait_vm<0>();
+      if constexpr (kL2) {
+        norm_rows(raw.k[0], nk(0));
+        norm_rows(raw.q[0], nq(0));
+      }
       if (pw == 0) {
         gate_compute(0);
         if (n_chunks > 1) load_ab(1);
@@ -986,6 +1033,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       if (more) copy_q(ch + 1);
       if (more) {
         if (pw == 1) wait_vm<6>(); else wait_vm<5>();   // K of ch+1 landed; its Q copies may remain
+        if constexpr (kL2) norm_rows(raw.k[nb], nk(nb));
         if (pw == 0) {
           gate_compute(ch + 1);
           if (ch + 2 < n_chunks) load_ab(ch + 2);
@@ -1012,6 +1060,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         } else {
           if (pw == 1) wait_vm<6>(); else wait_vm<5>();
         }
+        if constexpr (kL2) norm_rows(raw.q[nb], nq(nb));
       }
       lds_barrier();
       // ---- P3b: rows 12-15 of the Tm diagonal blocks (prep wave 0) and the P tiles
@@ -1043,6 +1092,28 @@ int check_prefill_args(const void* q, const void* k, const void* v, const void* 
   return GDN_OK;
 }
 
+
+template <bool kL2>
+int launch_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
+                   const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                   const void* cu_seqlens, int cu_is_int32, int N, int T, int HQ, int HV,
+                   float scale, uint16_t* out, float* final_state, hipStream_t st) {
+  const unsigned units = unsigned(N) * unsigned(HQ);
+  const dim3 grid{8u * unsigned(HV / HQ) * ((units + 7u) / 8u), 1u, 1u};
+  const dim3 block(kThreads);
+  if (cu_is_int32) {
+    hipLaunchKernelGGL((gdn_prefill_chain_kernel<int32_t, kL2>), grid, block, 0, st, q, k, v, state,
+                       A_log, a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), N, T, HQ, HV,
+                       scale, out, final_state);
+  } else {
+    hipLaunchKernelGGL((gdn_prefill_chain_kernel<int64_t, kL2>), grid, block, 0, st, q, k, v, state,
+                       A_log, a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), N, T, HQ, HV,
+                       scale, out, final_state);
+  }
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? GDN_OK : -int(err);
+}
+
 }  // namespace
 
 extern "C" size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV) {
@@ -1053,31 +1124,33 @@ extern "C" size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV) {
   return 0;
 }
 
+extern "C" int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                  const float* state, const float* A_log, const uint16_t* a,
+                                  const float* dt_bias, const uint16_t* b, const void* cu_seqlens,
+                                  int cu_is_int32, int N, int T, int HQ, int HV, float scale,
+                                  uint16_t* out, float* final_state, void* workspace,
+                                  size_t workspace_bytes, int flags, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
+                                    N, T, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
+  if (N == 0) return GDN_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (flags & GDN_QK_L2NORM)
+    return launch_prefill<true>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
+                                T, HQ, HV, scale, out, final_state, st);
+  return launch_prefill<false>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T,
+                               HQ, HV, scale, out, final_state, st);
+}
+
 extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                const float* state, const float* A_log, const uint16_t* a,
                                const float* dt_bias, const uint16_t* b, const void* cu_seqlens,
                                int cu_is_int32, int N, int T, int HQ, int HV, float scale,
                                uint16_t* out, float* final_state, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
-  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
-                                    N, T, HQ, HV);
-  if (rc != GDN_OK) return rc;
-  if (N == 0) return GDN_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned units = unsigned(N) * unsigned(HQ);
-  const dim3 grid{8u * unsigned(HV / HQ) * ((units + 7u) / 8u), 1u, 1u};
-  const dim3 block(kThreads);
-  if (cu_is_int32) {
-    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int32_t>, grid, block, 0, st, q, k, v, state, A_log,
-                       a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), N, T, HQ, HV, scale,
-                       out, final_state);
-  } else {
-    hipLaunchKernelGGL(gdn_prefill_chain_kernel<int64_t>, grid, block, 0, st, q, k, v, state, A_log,
-                       a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), N, T, HQ, HV, scale,
-                       out, final_state);
-  }
-  const hipError_t err = hipGetLastError();
-  return err == hipSuccess ? GDN_OK : -int(err);
+  return gdn_prefill_ex_fwd(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ,
+                            HV, scale, out, final_state, workspace, workspace_bytes, 0, stream);
 }

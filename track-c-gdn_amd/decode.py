@@ -59,29 +59,32 @@ def _gates(A_log, dt_bias):
     return A_log.float().contiguous(), dt_bias.float().contiguous()
 
 
-def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, nq, nv):
+def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, nq, nv,
+            flags=0):
     A_log, dt_bias = _gates(A_log, dt_bias)
     q = q.contiguous()
     k = k.contiguous()
     v = v.contiguous()
     a = a.contiguous()
     b = b.contiguous()
-    rc = _capi.lib().gdn_decode_fwd(
+    rc = _capi.lib().gdn_decode_ex_fwd(
         _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
         _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
-        B, nq, nv, float(scale), _capi.stream_handle(q.device))
-    _capi.check(rc, "gdn_decode_fwd")
+        B, nq, nv, float(scale), flags, _capi.stream_handle(q.device))
+    _capi.check(rc, "gdn_decode_ex_fwd")
 
 
 @torch.no_grad()
 def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
-               new_state=None):
+               new_state=None, qk_l2norm: bool = False):
     """One decode step for any ``HV % HQ == 0`` head layout.
 
     ``q, k [B, 1, HQ, 128]``, ``v [B, 1, HV, 128]`` bf16; ``state
     [B, HV, 128, 128]`` fp32 or ``None``; ``a, b [B, 1, HV]`` bf16; ``A_log,
     dt_bias [HV]``.  Returns ``(output [B, 1, HV, 128] bf16, new_state)``.
     ``new_state`` may be the ``state`` tensor itself (in-place update).
+    ``qk_l2norm=True`` uses q and k L2-normalised, ``x (sum x^2 + 1e-6)^-1/2``
+    in fp32 inside the kernel (an option the reference does not have).
     """
     B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
     scale = _resolve_scale(scale, q.shape[-1])
@@ -97,7 +100,8 @@ def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
     assert output.dtype == torch.bfloat16 and output.is_contiguous() and output.numel() == B * nv * D
     assert new_state.dtype == torch.float32 and new_state.is_contiguous()
     assert new_state.shape == (B, nv, D, D)
-    _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, nq, nv)
+    _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, nq, nv,
+            _capi.GDN_QK_L2NORM if qk_l2norm else 0)
     return output, new_state
 
 
@@ -127,7 +131,7 @@ def run_dps(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
 
 @torch.no_grad()
 def gdn_decode_multi(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
-                     new_state=None):
+                     new_state=None, qk_l2norm: bool = False):
     """T decode steps per sequence, applied in token order, in one launch.
 
     ``q, k [B, T, HQ, 128]``, ``v [B, T, HV, 128]`` bf16; ``a, b [B, T, HV]``
@@ -165,7 +169,8 @@ def gdn_decode_multi(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output
     rc = _capi.lib().gdn_decode_multi_fwd(
         _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
         _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
-        B, T, nq, nv, float(scale), _capi.stream_handle(q.device))
+        B, T, nq, nv, float(scale), _capi.GDN_QK_L2NORM if qk_l2norm else 0,
+        _capi.stream_handle(q.device))
     _capi.check(rc, "gdn_decode_multi_fwd")
     return output, new_state
 
@@ -257,7 +262,7 @@ class PreparedDecodeMulti:
         self._args = (
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
             _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
-            B, T, nq, nv, float(_resolve_scale(scale, D)), _capi.stream_handle(q.device))
+            B, T, nq, nv, float(_resolve_scale(scale, D)), 0, _capi.stream_handle(q.device))
 
     def __call__(self) -> None:
         rc = self._fn(*self._args)

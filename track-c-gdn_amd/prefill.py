@@ -80,14 +80,18 @@ def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
 
 @torch.no_grad()
 def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
-                output=None, final_state=None, workspace=None, validate: bool = True):
+                output=None, final_state=None, workspace=None, validate: bool = True,
+                qk_l2norm: bool = False):
     """Chunked GDN prefill over packed varlen sequences, any ``HV % HQ == 0``.
 
     ``q, k [T, HQ, 128]``, ``v [T, HV, 128]``, ``a, b [T, HV]`` bf16;
     ``state [N, HV, 128, 128]`` fp32 or ``None`` (zeros); ``cu_seqlens [N+1]``
     int64/int32.  Returns ``(output [T, HV, 128] bf16, final_state)``.
     ``validate=False`` skips the host read-back of ``cu_seqlens[-1]``; the
-    caller then guarantees ``cu_seqlens[N] == T``.
+    caller then guarantees ``cu_seqlens[N] == T``.  ``qk_l2norm=True`` uses
+    every q and k row L2-normalised, ``x (sum x^2 + 1e-6)^-1/2`` in fp32
+    inside the kernel (an option the reference does not have: it expects
+    normalised inputs).
     """
     T, nq, d = q.shape
     nv = v.shape[1]
@@ -115,13 +119,13 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
         workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    rc = _capi.lib().gdn_prefill_fwd(
+    rc = _capi.lib().gdn_prefill_ex_fwd(
         _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
         _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
         1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
         _capi.ptr(output), _capi.ptr(final_state), _capi.ptr(workspace), ws_bytes,
-        _capi.stream_handle(q.device))
-    _capi.check(rc, "gdn_prefill_fwd")
+        _capi.GDN_QK_L2NORM if qk_l2norm else 0, _capi.stream_handle(q.device))
+    _capi.check(rc, "gdn_prefill_ex_fwd")
     return output, final_state
 
 
