@@ -165,6 +165,27 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
                 flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True))
 
 
+def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
+    """The prefill that also writes the state entering every chunk (bf16 h)."""
+    w = ginp.WORKLOADS[name]
+    lens = ginp.workload_lengths(name)
+    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
+    g = _to(x, dev)
+    T = sum(lens)
+    N = len(lens)
+    out = torch.empty(T, w["HV"], D, dtype=torch.bfloat16, device=dev)
+    fs = torch.empty(N, w["HV"], D, D, dtype=torch.float32, device=dev)
+    NT = gpre.num_chunks(g["cu_seqlens"], T)
+    h = torch.empty(NT, w["HV"], D, D, dtype=torch.bfloat16, device=dev)
+    args = [g[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
+
+    def launch(i):
+        gpre.gdn_prefill(*args, g["scale"], output=out, final_state=fs, validate=False, h=h)
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    return dict(total_ms=total_ms, kernel_ms=kern_ms, chunks=NT, h_bytes=h.numel() * 2)
+
+
 def cpu_baseline_decode(budget_s=12.0, B=256):
     """Oracle decode step in fp32 on the host cores (bounded sample of B=256)."""
     from oracle import gdn_oracle as O
@@ -289,6 +310,18 @@ def main():
         except Exception as e:  # prefill not available: say so in the line
             line["prefill"] = {"error": f"{type(e).__name__}: {e}"}
             print(f"# prefill failed: {e}", file=sys.stderr, flush=True)
+        if "error" not in line["prefill"]:
+            # per-chunk states as well (the h a training backward reads; an option)
+            r = bench_prefill_h(dev, args.prefill_steps, PREFILL_WARMUP)
+            kus = r["kernel_ms"] * 1e3
+            line["prefill_h"] = {
+                "workload": "prefill_varlen8_t32768_qk16_v32", "chunks": r["chunks"],
+                "h_bytes": r["h_bytes"], "kernel_us": round(kus, 2),
+                "prefill_kernel_us": line["prefill"]["roofline"]["kernel_us"],
+                "h_write_GBs": round(r["h_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9, 1)}
+            print(f"# prefill with h (bf16, {r['chunks']} chunks, {r['h_bytes'] / 1e6:.0f} MB): "
+                  f"{kus:.1f} us against {line['prefill']['roofline']['kernel_us']:.1f} us without",
+                  file=sys.stderr, flush=True)
 
     if args.copy_calibration:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)

@@ -153,6 +153,39 @@ int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                        uint16_t* out, float* final_state,
                        void* workspace, size_t workspace_bytes, int flags, void* stream);
 
+/*
+ * Number of 64-token chunks of a varlen batch, sum over n of
+ * ceil(len_n / 64) with len_n from cu_seqlens clamped into [0, T] as the
+ * kernels clamp it: the first dimension of the h output below.  Reads a HOST
+ * copy of cu_seqlens (N+1 entries).  Returns -1 on a NULL pointer or
+ * negative N / T.  Counterpart of the chunk count `NT = len(chunk_indices)`
+ * and of `prepare_chunk_offsets` (gdn_prefill_qk4_v8_d128_k_last/solution/
+ * triton/kernel.py:1358-1361, 172-209).
+ */
+long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, int N, int T);
+
+/*
+ * gdn_prefill_ex_fwd that also writes the state entering every chunk:
+ * h[chunk_offset(n) + i][hv][v][k], bf16 (round to nearest even), with
+ * chunk_offset(n) the chunks of sequences 0 .. n-1 and i the chunk within
+ * sequence n; h[chunk_offset(n)] is the initial state (zeros without one).
+ * Replaces `chunk_gated_delta_rule_fwd_h`'s h output, `h = k.new_empty(B, NT,
+ * H, V, K)` stored before each chunk's update
+ * (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:1341-1398,
+ * 1153-1160), the per-chunk states a training backward reads.
+ *   h        : device [h_chunks, HV, 128, 128] bf16.
+ *   h_chunks : capacity of h in chunks; gdn_prefill_chunk_count(...) gives
+ *              the number written.  Slots at or past h_chunks are skipped.
+ * out / final_state are those of gdn_prefill_ex_fwd, bit for bit.
+ */
+int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                      const float* state, const float* A_log, const uint16_t* a,
+                      const float* dt_bias, const uint16_t* b,
+                      const void* cu_seqlens, int cu_is_int32, int N, int T,
+                      int HQ, int HV, float scale,
+                      uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
+                      void* workspace, size_t workspace_bytes, int flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,10 @@ How each function is pinned (tests/test_oracle.py):
                       closed forms at T = 1, split / varlen invariances.
 * prefill_chunked  -- equals prefill_recurrent in float64 at chunk sizes
                       1, 16, 32, 64, 128 including ragged tails.
+* prefill_chunk_states -- the first state of each sequence is its initial
+                      state; state i equals prefill_recurrent's final state
+                      over the first 64 i tokens; the count and order follow
+                      chunk_offsets.
 * qk_l2norm        -- torch.nn.functional.normalize where eps is negligible,
                       the closed form c/sqrt(c^2 + eps) on scaled unit vectors,
                       zero maps to zero, sign/permutation equivariance.
@@ -52,6 +56,7 @@ __all__ = [
     "unit_lower_inverse_blocked",
     "prefill_recurrent",
     "prefill_chunked",
+    "prefill_chunk_states",
     "default_scale",
     "qk_l2norm",
 ]
@@ -281,6 +286,35 @@ def prefill_recurrent(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=No
             o[t] = scale * torch.einsum("hvk,hk->hv", S, qh[t])
         final[n] = S
     return o, final
+
+
+def prefill_chunk_states(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, chunk_size: int = 64,
+                         dtype=torch.float64):
+    """States entering every chunk, ``h [NT, HV, V, K]`` (PRE:1341-1398).
+
+    ``chunk_gated_delta_rule_fwd_h`` stores the running state of sequence
+    ``n`` into ``h[chunk_offsets[n] + i]`` before it applies chunk ``i``
+    (PRE:1153-1160), starting from the initial state (zeros if ``None``);
+    ``chunk_offsets`` counts the chunks of the earlier sequences (PRE:172-209).
+    The states come from the token recurrence of :func:`prefill_recurrent`.
+    """
+    T, HQ, HV, D, N = _check_prefill_shapes(q, k, v, state, a, b, cu_seqlens)
+    ld, beta = prefill_log_decay_beta(a, b, A_log, dt_bias, dtype)
+    kh = _expand_heads(k.to(dtype), HV)
+    vh = v.to(dtype)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    hs = []
+    for n in range(N):
+        S = torch.zeros(HV, D, D, dtype=dtype) if state is None else state[n].to(dtype).clone()
+        for t in range(cu[n], cu[n + 1]):
+            if (t - cu[n]) % chunk_size == 0:
+                hs.append(S.clone())
+            S = torch.exp(ld[t])[:, None, None] * S
+            sk = torch.einsum("hvk,hk->hv", S, kh[t])
+            S = S + (beta[t][:, None] * (vh[t] - sk))[:, :, None] * kh[t][:, None, :]
+    if not hs:
+        return torch.zeros(0, HV, D, D, dtype=dtype)
+    return torch.stack(hs)
 
 
 def _round_bf16(x: torch.Tensor) -> torch.Tensor:

@@ -22,7 +22,7 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "gdn_abi_version", "gdn_error_string", "gdn_decode_fwd", "gdn_decode_pool_fwd",
         "gdn_decode_multi_fwd", "gdn_decode_ex_fwd", "gdn_prefill_workspace_bytes",
-        "gdn_prefill_fwd", "gdn_prefill_ex_fwd"])
+        "gdn_prefill_fwd", "gdn_prefill_ex_fwd", "gdn_prefill_chunk_count", "gdn_prefill_h_fwd"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -62,3 +62,36 @@ def test_argument_errors_return_before_launch():
     assert lib.gdn_prefill_ex_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 0, 8, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_fwd(None, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 0, None) == capi.GDN_ERR_NULL
     assert lib.gdn_prefill_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 7, 1.0, P, P, None, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 1, None, 0, 0, None) == capi.GDN_ERR_NULL
+    assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, -1, None, 0, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, None, 0, 2, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 6, 1.0, P, P, P, 1, None, 0, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_chunk_count(None, 0, 1, 1) == -1
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_chunk_count_matches_chunk_offsets(seed):
+    """Host chunk counter (the h output's first dimension) against the oracle's
+    chunk_offsets, int64 and int32, including the kernels' clamping of
+    out-of-range and decreasing entries into [0, T]."""
+    import torch
+    from oracle import gdn_oracle as O
+
+    lib = pkg_module("_capi").lib()
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, 300, (int(torch.randint(1, 12, (1,), generator=g)),), generator=g)
+    lens[0] = 0 if seed == 1 else lens[0]
+    cu = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(lens, 0)])
+    T = int(cu[-1])
+    for dt in (torch.int64, torch.int32):
+        c = cu.to(dt).contiguous()
+        n = lib.gdn_prefill_chunk_count(c.data_ptr(), int(dt == torch.int32), c.numel() - 1, T)
+        assert n == int(O.chunk_offsets(cu, 64)[-1])
+    bad = cu.clone()
+    bad[-1] = T + 500                      # past T: clamped to T
+    if bad.numel() > 2:
+        bad[1] = -7                        # negative: clamped to 0
+    expect = sum((int(min(max(int(bad[i + 1]), max(int(bad[i]), 0)), T)) - min(max(int(bad[i]), 0), T) + 63) // 64
+                 for i in range(bad.numel() - 1))
+    n = lib.gdn_prefill_chunk_count(bad.data_ptr(), 0, bad.numel() - 1, T)
+    assert n == expect

@@ -311,3 +311,37 @@ def test_qk_l2norm_equivariance_and_eps_argument():
     torch.testing.assert_close(O.qk_l2norm(x, eps=0.0), F.normalize(x, dim=-1), atol=0, rtol=1e-14)
     xb = x.to(torch.bfloat16)
     assert O.qk_l2norm(xb).dtype == DT
+
+
+# --------------------------------------------------------------------------- per-chunk states
+
+@pytest.mark.parametrize("lens,C", [([150, 0, 64, 1, 129], 64), ([40, 33], 16)])
+def test_prefill_chunk_states_against_prefix_runs(lens, C):
+    g = torch.Generator().manual_seed(sum(lens) + C)
+    HQ, HV, D = 2, 4, 8
+    T = sum(lens)
+    q = F.normalize(torch.randn(T, HQ, D, generator=g, dtype=DT), dim=-1)
+    k = F.normalize(torch.randn(T, HQ, D, generator=g, dtype=DT), dim=-1)
+    v = torch.randn(T, HV, D, generator=g, dtype=DT)
+    a = torch.randn(T, HV, generator=g, dtype=DT)
+    b = torch.randn(T, HV, generator=g, dtype=DT)
+    A_log = torch.rand(HV, generator=g, dtype=DT) * 2 - 2
+    dt_bias = torch.randn(HV, generator=g, dtype=DT) * 0.1
+    S0 = torch.randn(len(lens), HV, D, D, generator=g, dtype=DT) * 0.3
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int64)
+    h = O.prefill_chunk_states(q, k, v, S0, A_log, a, dt_bias, b, cu, chunk_size=C)
+    offs = O.chunk_offsets(cu, C)
+    assert h.shape == (int(offs[-1]), HV, D, D)
+    for n, L in enumerate(lens):
+        bos = int(cu[n])
+        for i in range((L + C - 1) // C):
+            slot = int(offs[n]) + i
+            if i == 0:
+                torch.testing.assert_close(h[slot], S0[n], atol=0, rtol=0)
+                continue
+            sl = slice(bos, bos + C * i)
+            _, s_ref = O.prefill_recurrent(q[sl], k[sl], v[sl], S0[n:n + 1], A_log, a[sl], dt_bias,
+                                           b[sl], torch.tensor([0, C * i]), 1.0)
+            torch.testing.assert_close(h[slot], s_ref[0], atol=1e-12, rtol=1e-12)
+    h0 = O.prefill_chunk_states(q, k, v, None, A_log, a, dt_bias, b, cu, chunk_size=C)
+    assert float(h0[0].abs().max()) == 0.0

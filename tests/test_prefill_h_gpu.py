@@ -1,0 +1,115 @@
+"""GPU checks of the per-chunk state output (``gdn_prefill_h_fwd``): the state
+entering every 64-token chunk, bf16, as ``chunk_gated_delta_rule_fwd_h``
+stores its ``h`` (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:
+1341-1398, stored before each chunk's update at 1153-1160).
+
+Bars:
+* the first slot of each sequence is the initial state rounded to bf16, bit
+  for bit (torch's round to nearest even);
+* every other slot within 3e-3 relative (Frobenius) of the fp64 oracle: bf16
+  storage alone is up to 2^-9 = 1.95e-3 per element;
+* output and final state identical bit for bit to the prefill without h;
+* slots at or past the capacity passed in are never written.
+At the 32 768-token benchmark size, where the oracle is too slow, each
+sequence's chain is checked for consistency instead: the prefill restarted
+from a stored slot (widened to fp32) over the rest of the sequence reproduces
+the final state within the bf16 bar.
+"""
+
+import pytest
+import torch
+
+from conftest import pkg_module
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+H_REL_BAR = 3e-3
+
+
+def _to(x, dev):
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in x.items()}
+
+
+def _rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+@pytest.mark.parametrize("lens,HQ,HV,with_state,l2", [
+    ([1, 63, 64, 65, 129], 4, 8, True, False), ([0, 300], 4, 8, False, False),
+    ([130, 0, 70], 16, 32, True, False), ([200, 64], 4, 8, True, True)])
+def test_prefill_h_matches_oracle(device, lens, HQ, HV, with_state, l2):
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    print(f"prefill h lens={lens} HQ={HQ} HV={HV} l2={l2}", flush=True)
+    x = inp.prefill_inputs(lens, HQ=HQ, HV=HV, seed=4100 + sum(lens), with_state=with_state)
+    g = _to(x, device)
+    o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2)
+    o0, s0 = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o0) and torch.equal(s, s0)
+    offs = O.chunk_offsets(x["cu_seqlens"], 64)
+    assert h.shape == (int(offs[-1]), HV, 128, 128) and h.dtype == torch.bfloat16
+    xo = dict(x)
+    if l2:
+        xo["q"], xo["k"] = O.qk_l2norm(x["q"]), O.qk_l2norm(x["k"])
+    h_ref = O.prefill_chunk_states(*[xo[n] for n in NAMES])
+    h_cpu = h.cpu()
+    for n, L in enumerate(lens):
+        for i in range((L + 63) // 64):
+            slot = int(offs[n]) + i
+            if i == 0:
+                first = (x["state"][n] if with_state else torch.zeros(HV, 128, 128)).to(torch.bfloat16)
+                assert torch.equal(h_cpu[slot], first), (n, slot)
+            else:
+                rel = _rel(h_cpu[slot], h_ref[slot])
+                assert rel <= H_REL_BAR, (n, i, rel)
+
+
+def test_prefill_h_capacity_guard_and_int32(device):
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    lens = [150, 90, 64]
+    x = inp.prefill_inputs(lens, seed=4200, with_state=True, cu_dtype=torch.int32)
+    g = _to(x, device)
+    NT = pre.num_chunks(g["cu_seqlens"], sum(lens))
+    assert NT == 3 + 2 + 1
+    big = torch.full((NT + 2, 8, 128, 128), 7.0, dtype=torch.bfloat16, device=device)
+    o_full, s_full, h_full = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"])
+    small = big[:NT - 2]                      # the last sequence's slots and one more are cut
+    o, s = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], h=small)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_full) and torch.equal(s, s_full)
+    assert torch.equal(big[:NT - 2], h_full[:NT - 2])
+    assert bool((big[NT - 2:] == 7.0).all())  # never written
+
+
+def test_prefill_h_benchmark_workload_chain_consistency(device):
+    """32 768 tokens, 8 sequences, qk16/v32: restarting from stored slots."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    name = "prefill_varlen8_t32768_qk16_v32"
+    w = inp.WORKLOADS[name]
+    lens = inp.workload_lengths(name)
+    print(f"prefill h {name}", flush=True)
+    x = inp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
+    g = _to(x, device)
+    o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"])
+    torch.cuda.synchronize()
+    offs = O.chunk_offsets(x["cu_seqlens"], 64)
+    cu = [int(c) for c in x["cu_seqlens"]]
+    for n, L in enumerate(lens):
+        assert torch.equal(h[int(offs[n])], g["state"][n].to(torch.bfloat16))
+        nch = (L + 63) // 64
+        for i in (1, nch // 2, nch - 1):
+            t0 = cu[n] + 64 * i
+            sl = slice(t0, cu[n + 1])
+            sub_cu = torch.tensor([0, cu[n + 1] - t0], dtype=torch.int64, device=device)
+            _, s_re = pre.gdn_prefill(g["q"][sl], g["k"][sl], g["v"][sl],
+                                      h[int(offs[n]) + i][None].float(), g["A_log"], g["a"][sl],
+                                      g["dt_bias"], g["b"][sl], sub_cu, g["scale"])
+            torch.cuda.synchronize()
+            rel = _rel(s_re[0], s[n])
+            assert rel <= H_REL_BAR, (n, i, rel)

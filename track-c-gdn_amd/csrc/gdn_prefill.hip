@@ -212,13 +212,17 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // 16 bytes to base + off: base uniform (an SGPR pair), off a 32-bit lane offset.
 // Nothing in the kernel reads what these stores write.
+// A store of more than 8 bytes keeps reading its data VGPRs after issue: a
+// VALU write to them needs 2 wait states first (the compiler counts them for
+// its own stores, not for this asm), hence the s_nop.
 __device__ __forceinline__ void store_b128_saddr(char* base, uint32_t off, u32x4_t data) {
-  asm volatile("global_store_dwordx4 %0, %1, %2" :: "v"(off), "v"(data), "s"(base) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, %2\n\ts_nop 1" :: "v"(off), "v"(data), "s"(base)
+               : "memory");
 }
 
 // Tokens [bos, bos + len) of sequence n, clamped into [0, T].
 template <typename CuT>
-__device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {
+__host__ __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {
   long long b0 = (long long)cu[n], e0 = (long long)cu[n + 1];
   b0 = b0 < 0 ? 0 : (b0 > T ? T : b0);
   e0 = e0 < b0 ? b0 : (e0 > T ? T : e0);
@@ -268,14 +272,20 @@ using IC = std::integral_constant<int, N>;
 // rows they copied, right after their wait for them, and the factors scale
 // the products: the fp16 K rows (so K S^T and the state update see k-hat),
 // the A and P tiles (row and column factors) and the e^gam factor of S Q^T.
-template <typename CuT, bool kL2>
+//
+// kH: the state entering every chunk is also written, bf16, to
+// hout[chunk_offset(n) + ch][hv][v][k] (chunk_offset(n) = the chunks of the
+// sequences before n), skipping slots at or past h_chunks.  The values are
+// the bf16 fragments the chain forms anyway for S Q^T.
+template <typename CuT, bool kL2, bool kH>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ h0,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV,
-    float scale, uint16_t* __restrict__ out, float* __restrict__ ht) {
+    float scale, uint16_t* __restrict__ out, float* __restrict__ ht,
+    uint16_t* __restrict__ hout, int h_chunks) {
   __shared__ Smem sm;
   __shared__ SmemRaw raw;
   __shared__ __align__(16) uint16_t rawV[C * D];     // V chunk (bf16, swizzled), DMA target
@@ -319,6 +329,14 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   const size_t qk_stride = size_t(HQ) * D;   // elements per token in q / k
   const size_t v_stride = size_t(HV) * D;    // elements per token in v / out
   const int n_chunks = (len + C - 1) / C;
+  int h_base = 0;                   // kH: chunks of the sequences before n
+  if constexpr (kH) {
+    for (int m = 0; m < n; ++m) {
+      int bm, lm;
+      seq_bounds(cu_seqlens, m, T, bm, lm);
+      h_base += (lm + C - 1) / C;
+    }
+  }
   auto chunk_len = [&](int ch) { return min(C, len - ch * C); };
 
   // Upper 16x16 tiles inside the diagonal 32x32 blocks of Tm / P are read by
@@ -646,6 +664,30 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         for (int kb = 0; kb < 8; ++kb)
           Sacc[u][kb] = *reinterpret_cast<const f32x4*>(src + size_t(16 * u) * D + 16 * kb + 4 * g);
     }
+    // kH: the bf16 fragments sb[u] of column block p of the state entering chunk
+    // ch go to its h slot.  Lane (g, c) holds row v0 + 16 u + c, 4-column
+    // pieces g and g + 4 of the block (columns 32 p + 4 g .., 32 p + 16 + 4 g ..).
+    // v_permlane16_swap trades the odd 16-lane rows' first piece for the even
+    // rows' second piece, which leaves every lane two adjacent pieces: pieces
+    // g, g + 1 (g even) or g + 3, g + 4 (g odd), 16 contiguous bytes, so one
+    // 16-byte store per lane writes the block's 64 bytes of each of 16 rows.
+    const uint32_t h_lane = uint32_t(vrow * D + ((g & 1) ? 4 * (g + 3) : 4 * g)) * 2u;
+    auto store_h = [&](int ch, int p, const bf16x8_t (&sb)[kTiles]) {
+      if constexpr (kH) {
+        const int slot = h_base + ch;
+        if (slot < h_chunks) {
+          char* base = reinterpret_cast<char*>(hout) + (size_t(slot) * HV + hv) * size_t(D * D * 2);
+#pragma unroll
+          for (int u = 0; u < kTiles; ++u) {
+            const u32x4_t w = __builtin_bit_cast(u32x4_t, sb[u]);
+            const auto lo = __builtin_amdgcn_permlane16_swap(w[0], w[2], false, false);
+            const auto hi = __builtin_amdgcn_permlane16_swap(w[1], w[3], false, false);
+            store_b128_saddr(base + u * (16 * D * 2), h_lane + uint32_t(64 * p),
+                             u32x4_t{lo[0], hi[0], lo[1], hi[1]});
+          }
+        }
+      }
+    };
     // KS[u] += K[:, 32 p0 .. 32 p0 + 63] S^T[32 p0 .., tile u] for the chunk whose
     // fp16 K rows are in Kc[kb_buf]; columns 0-63 use state entries k < 64,
     // updated in the first half of the state update.  The 8 K fragments are
@@ -863,6 +905,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
             for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16_bf(sb[u], qf[p & 1][tb], OT[u][tb]);
           }
+          store_h(ch, p, sb);
           load_qf(p + 2, qf[p & 1]);
         }
         asm volatile("" ::: "memory");
@@ -892,6 +935,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
               for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16_bf(sb[u], qf[p & 1][tb], OT[u][tb]);
             }
+            store_h(ch, p, sb);
           }
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
@@ -1093,25 +1137,48 @@ int check_prefill_args(const void* q, const void* k, const void* v, const void* 
 }
 
 
-template <bool kL2>
+template <bool kL2, bool kH>
 int launch_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                    const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
                    const void* cu_seqlens, int cu_is_int32, int N, int T, int HQ, int HV,
-                   float scale, uint16_t* out, float* final_state, hipStream_t st) {
+                   float scale, uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
+                   hipStream_t st) {
   const unsigned units = unsigned(N) * unsigned(HQ);
   const dim3 grid{8u * unsigned(HV / HQ) * ((units + 7u) / 8u), 1u, 1u};
   const dim3 block(kThreads);
   if (cu_is_int32) {
-    hipLaunchKernelGGL((gdn_prefill_chain_kernel<int32_t, kL2>), grid, block, 0, st, q, k, v, state,
-                       A_log, a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), N, T, HQ, HV,
-                       scale, out, final_state);
+    hipLaunchKernelGGL((gdn_prefill_chain_kernel<int32_t, kL2, kH>), grid, block, 0, st, q, k, v,
+                       state, A_log, a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), N, T,
+                       HQ, HV, scale, out, final_state, h, h_chunks);
   } else {
-    hipLaunchKernelGGL((gdn_prefill_chain_kernel<int64_t, kL2>), grid, block, 0, st, q, k, v, state,
-                       A_log, a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), N, T, HQ, HV,
-                       scale, out, final_state);
+    hipLaunchKernelGGL((gdn_prefill_chain_kernel<int64_t, kL2, kH>), grid, block, 0, st, q, k, v,
+                       state, A_log, a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), N, T,
+                       HQ, HV, scale, out, final_state, h, h_chunks);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : -int(err);
+}
+
+int prefill_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
+                     const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                     const void* cu_seqlens, int cu_is_int32, int N, int T, int HQ, int HV,
+                     float scale, uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
+                     int flags, hipStream_t st) {
+  const bool l2 = (flags & GDN_QK_L2NORM) != 0;
+  if (h != nullptr) {
+    return l2 ? launch_prefill<true, true>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                           cu_is_int32, N, T, HQ, HV, scale, out, final_state, h,
+                                           h_chunks, st)
+              : launch_prefill<false, true>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                            cu_is_int32, N, T, HQ, HV, scale, out, final_state, h,
+                                            h_chunks, st);
+  }
+  return l2 ? launch_prefill<true, false>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                          cu_is_int32, N, T, HQ, HV, scale, out, final_state,
+                                          nullptr, 0, st)
+            : launch_prefill<false, false>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                           cu_is_int32, N, T, HQ, HV, scale, out, final_state,
+                                           nullptr, 0, st);
 }
 
 }  // namespace
@@ -1137,12 +1204,41 @@ extern "C" int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const ui
   if (rc != GDN_OK) return rc;
   if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
   if (N == 0) return GDN_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (flags & GDN_QK_L2NORM)
-    return launch_prefill<true>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
-                                T, HQ, HV, scale, out, final_state, st);
-  return launch_prefill<false>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T,
-                               HQ, HV, scale, out, final_state, st);
+  return prefill_dispatch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ,
+                          HV, scale, out, final_state, nullptr, 0, flags,
+                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, int N,
+                                             int T) {
+  if (!cu_seqlens_host || N < 0 || T < 0) return -1;
+  long long total = 0;
+  for (int m = 0; m < N; ++m) {
+    int bm, lm;
+    if (cu_is_int32) seq_bounds(static_cast<const int32_t*>(cu_seqlens_host), m, T, bm, lm);
+    else seq_bounds(static_cast<const int64_t*>(cu_seqlens_host), m, T, bm, lm);
+    total += (lm + C - 1) / C;
+  }
+  return total;
+}
+
+extern "C" int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const float* state, const float* A_log, const uint16_t* a,
+                                 const float* dt_bias, const uint16_t* b, const void* cu_seqlens,
+                                 int cu_is_int32, int N, int T, int HQ, int HV, float scale,
+                                 uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
+                                 void* workspace, size_t workspace_bytes, int flags, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
+                                    N, T, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (!h) return GDN_ERR_NULL;
+  if (h_chunks < 0 || (flags & ~GDN_FLAGS_ALL)) return GDN_ERR_SHAPE;
+  if (N == 0) return GDN_OK;
+  return prefill_dispatch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ,
+                          HV, scale, out, final_state, h, h_chunks, flags,
+                          static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,

@@ -12,6 +12,9 @@ Host-side mirror of the reference prefill entry point
   ``final_state`` appended).
 * :func:`gdn_prefill` -- any ``HV % HQ == 0`` head layout, optional
   validation, caller-provided outputs.
+* :func:`gdn_prefill_h` -- also returns ``h``, the state entering every
+  64-token chunk (the h output of ``chunk_gated_delta_rule_fwd_h``,
+  PRE:1341-1398).
 
 All compute runs in the HIP kernels of libgdn_hip.so on torch's current
 stream.
@@ -78,10 +81,22 @@ def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
     return int(_capi.lib().gdn_prefill_workspace_bytes(N, T, HQ, HV))
 
 
+def num_chunks(cu_seqlens: torch.Tensor, T: int) -> int:
+    """64-token chunks of the batch, ``sum ceil(len_n / 64)`` (the chunk count
+    of PRE:1358-1361): the first dimension of ``h``.  Reads ``cu_seqlens``
+    on the host (a device-to-host copy when it lives on the GPU)."""
+    cu = cu_seqlens.detach().to("cpu").contiguous()
+    assert cu.dtype in (torch.int64, torch.int32) and cu.dim() == 1 and cu.numel() >= 1
+    n = _capi.lib().gdn_prefill_chunk_count(cu.data_ptr(), 1 if cu.dtype == torch.int32 else 0,
+                                            cu.numel() - 1, int(T))
+    assert n >= 0
+    return int(n)
+
+
 @torch.no_grad()
 def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
                 output=None, final_state=None, workspace=None, validate: bool = True,
-                qk_l2norm: bool = False):
+                qk_l2norm: bool = False, h=None):
     """Chunked GDN prefill over packed varlen sequences, any ``HV % HQ == 0``.
 
     ``q, k [T, HQ, 128]``, ``v [T, HV, 128]``, ``a, b [T, HV]`` bf16;
@@ -91,7 +106,9 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     caller then guarantees ``cu_seqlens[N] == T``.  ``qk_l2norm=True`` uses
     every q and k row L2-normalised, ``x (sum x^2 + 1e-6)^-1/2`` in fp32
     inside the kernel (an option the reference does not have: it expects
-    normalised inputs).
+    normalised inputs).  ``h``, a ``[NT, HV, 128, 128]`` bf16 buffer
+    (``NT = num_chunks(cu_seqlens, T)``), also receives the state entering
+    every chunk; the output and final state are the same bit for bit.
     """
     T, nq, d = q.shape
     nv = v.shape[1]
@@ -119,14 +136,48 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
         workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    flags = _capi.GDN_QK_L2NORM if qk_l2norm else 0
+    if h is not None:
+        assert h.dtype == torch.bfloat16 and h.is_contiguous() and h.device == q.device
+        assert h.dim() == 4 and h.shape[1:] == (nv, HEAD_SIZE, HEAD_SIZE)
+        rc = _capi.lib().gdn_prefill_h_fwd(
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
+            _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
+            1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
+            _capi.ptr(output), _capi.ptr(final_state), _capi.ptr(h), h.shape[0],
+            _capi.ptr(workspace), ws_bytes, flags, _capi.stream_handle(q.device))
+        _capi.check(rc, "gdn_prefill_h_fwd")
+        return output, final_state
     rc = _capi.lib().gdn_prefill_ex_fwd(
         _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
         _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
         1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
         _capi.ptr(output), _capi.ptr(final_state), _capi.ptr(workspace), ws_bytes,
-        _capi.GDN_QK_L2NORM if qk_l2norm else 0, _capi.stream_handle(q.device))
+        flags, _capi.stream_handle(q.device))
     _capi.check(rc, "gdn_prefill_ex_fwd")
     return output, final_state
+
+
+@torch.no_grad()
+def gdn_prefill_h(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
+                  output=None, final_state=None, h=None, workspace=None, qk_l2norm: bool = False):
+    """:func:`gdn_prefill` that also returns ``h [NT, HV, 128, 128]`` bf16, the
+    state entering every 64-token chunk: ``h[chunk_offset(n) + i]`` is the
+    state of sequence ``n`` before its chunk ``i`` (the initial state for
+    ``i = 0``), as ``chunk_gated_delta_rule_fwd_h`` stores it (PRE:1341-1398,
+    1153-1160; round to nearest even).  Returns ``(output, final_state, h)``.
+    Reads ``cu_seqlens`` on the host to size ``h`` (as the reference's chunk
+    index preparation does, PRE:175-209).
+    """
+    T = q.shape[0]
+    nv = v.shape[1]
+    NT = num_chunks(cu_seqlens, T)
+    if h is None:
+        h = torch.empty(NT, nv, HEAD_SIZE, HEAD_SIZE, dtype=torch.bfloat16, device=q.device)
+    assert h.shape[0] >= NT, (h.shape, NT)
+    o, s = gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
+                       final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h)
+    return o, s, h
 
 
 @torch.no_grad()
