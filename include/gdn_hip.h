@@ -10,6 +10,9 @@
  *     asynchronously, with no host synchronisation;
  *   - return 0 on success, a negative GDN_ERR_* code for an argument error
  *     (nothing launched), or -(hipError_t) if a launch failed;
+ *   - an array with no elements may be NULL: decode with B = 0 reads and
+ *     writes nothing; prefill with T = 0 needs only cu_seqlens and, when
+ *     N > 0, A_log, dt_bias and final_state (the initial states are copied);
  *   - no C++ exception crosses the ABI.
  *
  * Layouts (D = 128 = K = V; qk-head of v-head h is h / (HV/HQ)):

@@ -297,8 +297,10 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
 int check_decode_args(const void* q, const void* k, const void* v, const void* state_out,
                       const void* A_log, const void* a, const void* dt_bias, const void* b,
                       const void* out, int B, int HQ, int HV) {
-  if (!q || !k || !v || !state_out || !A_log || !a || !dt_bias || !b || !out) return GDN_ERR_NULL;
   if (B < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return GDN_ERR_SHAPE;
+  // An empty batch reads and writes nothing; its tensors may have no storage.
+  if (B > 0 && (!q || !k || !v || !state_out || !A_log || !a || !dt_bias || !b || !out))
+    return GDN_ERR_NULL;
   return GDN_OK;
 }
 
@@ -379,7 +381,7 @@ extern "C" int gdn_decode_pool_fwd(const uint16_t* q, const uint16_t* k, const u
                                    float scale, void* stream) {
   const int rc = check_decode_args(q, k, v, state_pool, A_log, a, dt_bias, b, out, B, HQ, HV);
   if (rc != GDN_OK) return rc;
-  if (!slot_ids) return GDN_ERR_NULL;
+  if (!slot_ids && B > 0) return GDN_ERR_NULL;
   if (pool_size < 0) return GDN_ERR_SHAPE;
   return launch_decode(q, k, v, state_pool, state_pool, A_log, a, dt_bias, b, out, slot_ids, B,
                        HQ, HV, pool_size, scale, 0, stream);

@@ -1130,9 +1130,13 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 int check_prefill_args(const void* q, const void* k, const void* v, const void* A_log,
                        const void* a, const void* dt_bias, const void* b, const void* cu,
                        const void* out, const void* final_state, int N, int T, int HQ, int HV) {
-  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !cu || !out || !final_state)
-    return GDN_ERR_NULL;
   if (N < 0 || T < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return GDN_ERR_SHAPE;
+  // Empty tensors may have no storage: token arrays are only needed when
+  // T > 0, per-sequence arrays when N > 0 (a batch of empty sequences still
+  // copies its initial states to the final states).
+  if (!cu) return GDN_ERR_NULL;
+  if (N > 0 && (!A_log || !dt_bias || !final_state)) return GDN_ERR_NULL;
+  if (T > 0 && (!q || !k || !v || !a || !b || !out)) return GDN_ERR_NULL;
   return GDN_OK;
 }
 
@@ -1233,7 +1237,7 @@ extern "C" int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uin
   const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
                                     N, T, HQ, HV);
   if (rc != GDN_OK) return rc;
-  if (!h) return GDN_ERR_NULL;
+  if (!h && h_chunks > 0) return GDN_ERR_NULL;
   if (h_chunks < 0 || (flags & ~GDN_FLAGS_ALL)) return GDN_ERR_SHAPE;
   if (N == 0) return GDN_OK;
   return prefill_dispatch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ,
