@@ -113,3 +113,26 @@ def test_prefill_h_benchmark_workload_chain_consistency(device):
             torch.cuda.synchronize()
             rel = _rel(s_re[0], s[n])
             assert rel <= H_REL_BAR, (n, i, rel)
+
+
+def test_prefill_h_many_sequences(device):
+    """150 sequences (more than one per lane of the offset sum), lengths 0-140."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    g0 = torch.Generator().manual_seed(4400)
+    lens = torch.randint(0, 141, (150,), generator=g0).tolist()
+    lens[0], lens[77], lens[149] = 0, 64, 1
+    print(f"prefill h {len(lens)} sequences, {sum(lens)} tokens", flush=True)
+    x = inp.prefill_inputs(lens, seed=4401, with_state=True)
+    g = _to(x, device)
+    o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"])
+    torch.cuda.synchronize()
+    offs = O.chunk_offsets(x["cu_seqlens"], 64)
+    assert h.shape[0] == int(offs[-1])
+    h_ref = O.prefill_chunk_states(*[x[n] for n in NAMES])
+    h_cpu = h.cpu()
+    for n, L in enumerate(lens):
+        if L > 0:
+            assert torch.equal(h_cpu[int(offs[n])], x["state"][n].to(torch.bfloat16)), n
+    rel = _rel(h_cpu, h_ref)
+    assert rel <= H_REL_BAR, rel

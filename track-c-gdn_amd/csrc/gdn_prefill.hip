@@ -331,11 +331,15 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   const int n_chunks = (len + C - 1) / C;
   int h_base = 0;                   // kH: chunks of the sequences before n
   if constexpr (kH) {
-    for (int m = 0; m < n; ++m) {
+    int part = 0;                   // lanes take every 64th sequence, then a wave sum
+    for (int m = lane; m < n; m += 64) {
       int bm, lm;
       seq_bounds(cu_seqlens, m, T, bm, lm);
-      h_base += (lm + C - 1) / C;
+      part += (lm + C - 1) / C;
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+    h_base = __builtin_amdgcn_readfirstlane(part);
   }
   auto chunk_len = [&](int ch) { return min(C, len - ch * C); };
 
