@@ -210,10 +210,12 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
   const float dtb = dt_bias[hv];
 
   // Token inputs go through LDS in blocks of kTokBlock tokens: k, q and this
-  // head's v rows (256 B each per token) and a, b, copied by the whole
-  // workgroup with 16-byte loads, so the serial token loop reads LDS, not HBM.
+  // head's v rows (256 B each per token), copied by the whole workgroup with
+  // 16-byte loads, so the serial token loop reads LDS, not HBM; and each
+  // token's gates g, beta, computed once (by one thread per token) instead
+  // of by every wave.
   __shared__ __align__(16) uint16_t tk[kTokBlock][3][D];   // k | q | v
-  __shared__ float tab[kTokBlock][2];                       // a, b (as fp32)
+  __shared__ float tab[kTokBlock][2];                       // g, beta
   for (int t0 = 0; t0 < T; t0 += kTokBlock) {
     const int nt = min(kTokBlock, T - t0);
     __syncthreads();     // the previous block's reads are done
@@ -226,10 +228,11 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
                                        : v + (tok * HV + hv) * D;
       *reinterpret_cast<uint4*>(&tk[t][which][8 * chunk]) = *reinterpret_cast<const uint4*>(src + 8 * chunk);
     }
-    if (threadIdx.x < 2 * nt) {
-      const int t = threadIdx.x >> 1;
+    if (threadIdx.x < nt) {      // gates (reference DEC:59-65)
+      const int t = threadIdx.x;
       const size_t tok = size_t(n) * T + t0 + t;
-      tab[t][threadIdx.x & 1] = bf16_bits_to_f32((threadIdx.x & 1) ? b[tok * HV + hv] : a[tok * HV + hv]);
+      tab[t][0] = expf(-a_log_exp * softplus_thresh20(bf16_bits_to_f32(a[tok * HV + hv]) + dtb));
+      tab[t][1] = 1.0f / (1.0f + expf(-bf16_bits_to_f32(b[tok * HV + hv])));
     }
     __syncthreads();
     for (int t = 0; t < nt; ++t) {
@@ -250,9 +253,8 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
         l2norm_row16(kk);
         l2norm_row16(qq);
       }
-      // gates (reference DEC:59-65), uniform per wave
-      const float g = expf(-a_log_exp * softplus_thresh20(tab[t][0] + dtb));
-      const float beta = 1.0f / (1.0f + expf(-tab[t][1]));
+      const float g = tab[t][0];
+      const float beta = tab[t][1];
       float kq = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) kq = fmaf(kk[e], qq[e], kq);
