@@ -209,13 +209,15 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
   const float a_log_exp = expf(A_log[hv]);
   const float dtb = dt_bias[hv];
 
-  // Token inputs go through LDS in blocks of kTokBlock tokens: k, q and this
-  // head's v rows (256 B each per token), copied by the whole workgroup with
-  // 16-byte loads, so the serial token loop reads LDS, not HBM; and each
-  // token's gates g, beta, computed once (by one thread per token) instead
-  // of by every wave.
-  __shared__ __align__(16) uint16_t tk[kTokBlock][3][D];   // k | q | v
-  __shared__ float tab[kTokBlock][2];                       // g, beta
+  // Token inputs go through LDS in blocks of kTokBlock tokens, widened to
+  // fp32 once: k, q and this head's v row (128 values each per token),
+  // copied by the whole workgroup with 16-byte loads.  Then one 16-lane group
+  // per token normalises k and q (option GDN_QK_L2NORM) and forms k.q, with
+  // the lane layout and summation order of the single-step kernel (lane c:
+  // elements 4c .. 4c+3 and 64+4c .. 64+4c+3), and one thread per token forms
+  // the gates g, beta.  The serial token loop then only reads LDS.
+  __shared__ __align__(16) float tk[kTokBlock][3][D];   // k | q | v
+  __shared__ float tab[kTokBlock][3];                   // g, beta, k.q
   for (int t0 = 0; t0 < T; t0 += kTokBlock) {
     const int nt = min(kTokBlock, T - t0);
     __syncthreads();     // the previous block's reads are done
@@ -226,7 +228,12 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
       const uint16_t* src = which == 0 ? k + (tok * HQ + hq) * D
                           : which == 1 ? q + (tok * HQ + hq) * D
                                        : v + (tok * HV + hv) * D;
-      *reinterpret_cast<uint4*>(&tk[t][which][8 * chunk]) = *reinterpret_cast<const uint4*>(src + 8 * chunk);
+      const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * chunk);
+      float x[8];
+      unpack_bf16x2(w.x, x[0], x[1]); unpack_bf16x2(w.y, x[2], x[3]);
+      unpack_bf16x2(w.z, x[4], x[5]); unpack_bf16x2(w.w, x[6], x[7]);
+      *reinterpret_cast<f32x4*>(&tk[t][which][8 * chunk]) = f32x4{x[0], x[1], x[2], x[3]};
+      *reinterpret_cast<f32x4*>(&tk[t][which][8 * chunk + 4]) = f32x4{x[4], x[5], x[6], x[7]};
     }
     if (threadIdx.x < nt) {      // gates (reference DEC:59-65)
       const int t = threadIdx.x;
@@ -235,30 +242,52 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
       tab[t][1] = 1.0f / (1.0f + expf(-bf16_bits_to_f32(b[tok * HV + hv])));
     }
     __syncthreads();
-    for (int t = 0; t < nt; ++t) {
-      float kk[8], qq[8], vv[kRowsPerLane];
-      {
-        const uint2 klo = *reinterpret_cast<const uint2*>(&tk[t][0][4 * c]);
-        const uint2 khi = *reinterpret_cast<const uint2*>(&tk[t][0][64 + 4 * c]);
-        const uint2 qlo = *reinterpret_cast<const uint2*>(&tk[t][1][4 * c]);
-        const uint2 qhi = *reinterpret_cast<const uint2*>(&tk[t][1][64 + 4 * c]);
-        const uint2 vw = *reinterpret_cast<const uint2*>(&tk[t][2][rbase]);
-        unpack_bf16x2(klo.x, kk[0], kk[1]); unpack_bf16x2(klo.y, kk[2], kk[3]);
-        unpack_bf16x2(khi.x, kk[4], kk[5]); unpack_bf16x2(khi.y, kk[6], kk[7]);
-        unpack_bf16x2(qlo.x, qq[0], qq[1]); unpack_bf16x2(qlo.y, qq[2], qq[3]);
-        unpack_bf16x2(qhi.x, qq[4], qq[5]); unpack_bf16x2(qhi.y, qq[6], qq[7]);
-        unpack_bf16x2(vw.x, vv[0], vv[1]); unpack_bf16x2(vw.y, vv[2], vv[3]);
+    {
+      const int t = 4 * wave + rsub;          // one 16-lane group per token
+      if (t < nt) {
+        float kk[8], qq[8];
+        const f32x4 k0 = *reinterpret_cast<const f32x4*>(&tk[t][0][4 * c]);
+        const f32x4 k1 = *reinterpret_cast<const f32x4*>(&tk[t][0][64 + 4 * c]);
+        const f32x4 q0 = *reinterpret_cast<const f32x4*>(&tk[t][1][4 * c]);
+        const f32x4 q1 = *reinterpret_cast<const f32x4*>(&tk[t][1][64 + 4 * c]);
+        kk[0] = k0.x; kk[1] = k0.y; kk[2] = k0.z; kk[3] = k0.w;
+        kk[4] = k1.x; kk[5] = k1.y; kk[6] = k1.z; kk[7] = k1.w;
+        qq[0] = q0.x; qq[1] = q0.y; qq[2] = q0.z; qq[3] = q0.w;
+        qq[4] = q1.x; qq[5] = q1.y; qq[6] = q1.z; qq[7] = q1.w;
+        if (flags & GDN_QK_L2NORM) {
+          l2norm_row16(kk);
+          l2norm_row16(qq);
+          *reinterpret_cast<f32x4*>(&tk[t][0][4 * c]) = f32x4{kk[0], kk[1], kk[2], kk[3]};
+          *reinterpret_cast<f32x4*>(&tk[t][0][64 + 4 * c]) = f32x4{kk[4], kk[5], kk[6], kk[7]};
+          *reinterpret_cast<f32x4*>(&tk[t][1][4 * c]) = f32x4{qq[0], qq[1], qq[2], qq[3]};
+          *reinterpret_cast<f32x4*>(&tk[t][1][64 + 4 * c]) = f32x4{qq[4], qq[5], qq[6], qq[7]};
+        }
+        float kq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kq = fmaf(kk[e], qq[e], kq);
+        kq = row16_sum(kq);
+        if (c == 0) tab[t][2] = kq;
       }
-      if (flags & GDN_QK_L2NORM) {
-        l2norm_row16(kk);
-        l2norm_row16(qq);
+    }
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+      float kk[8], vv[kRowsPerLane];
+      float qq[8];
+      {
+        const f32x4 k0 = *reinterpret_cast<const f32x4*>(&tk[t][0][4 * c]);
+        const f32x4 k1 = *reinterpret_cast<const f32x4*>(&tk[t][0][64 + 4 * c]);
+        const f32x4 q0 = *reinterpret_cast<const f32x4*>(&tk[t][1][4 * c]);
+        const f32x4 q1 = *reinterpret_cast<const f32x4*>(&tk[t][1][64 + 4 * c]);
+        const f32x4 vw = *reinterpret_cast<const f32x4*>(&tk[t][2][rbase]);
+        kk[0] = k0.x; kk[1] = k0.y; kk[2] = k0.z; kk[3] = k0.w;
+        kk[4] = k1.x; kk[5] = k1.y; kk[6] = k1.z; kk[7] = k1.w;
+        qq[0] = q0.x; qq[1] = q0.y; qq[2] = q0.z; qq[3] = q0.w;
+        qq[4] = q1.x; qq[5] = q1.y; qq[6] = q1.z; qq[7] = q1.w;
+        vv[0] = vw.x; vv[1] = vw.y; vv[2] = vw.z; vv[3] = vw.w;
       }
       const float g = tab[t][0];
       const float beta = tab[t][1];
-      float kq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kq = fmaf(kk[e], qq[e], kq);
-      kq = row16_sum(kq);
+      const float kq = tab[t][2];
       float o_out[kRowsPerLane];
 #pragma unroll
       for (int j = 0; j < kRowsPerLane; ++j) {
