@@ -102,14 +102,15 @@ def timed_launches(launch, n_steps: int, warmup: int):
     return total, total / n_steps
 
 
-def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4):
+def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4, qk_l2norm=False):
     x = ginp.decode_inputs(B, HQ, HV, seed=1001)
     g = _to(x, dev)
     states = [g["state"]] + [g["state"].clone() for _ in range(sets - 1)]
     outs = [torch.empty_like(g["state"]) for _ in range(sets)]
     o = torch.empty(B, 1, HV, D, dtype=torch.bfloat16, device=dev)
     steps_ = [gdec.PreparedDecode(g["q"], g["k"], g["v"], states[j], g["A_log"], g["a"],
-                                  g["dt_bias"], g["b"], g["scale"], o, outs[j])
+                                  g["dt_bias"], g["b"], g["scale"], o, outs[j],
+                                  qk_l2norm=qk_l2norm)
               for j in range(sets)]
 
     def launch(i):
@@ -143,7 +144,7 @@ def bench_decode_multi(dev, steps, warmup, B=256, T=4, HQ=4, HV=8, sets=4):
                 T=T)
 
 
-def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
+def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk_l2norm=False):
     w = ginp.WORKLOADS[name]
     lens = ginp.workload_lengths(name)
     x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
@@ -154,7 +155,8 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     fs = torch.empty(N, w["HV"], D, D, dtype=torch.float32, device=dev)
 
     call = gpre.PreparedPrefill(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
-                                g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"], out, fs)
+                                g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"], out, fs,
+                                qk_l2norm=qk_l2norm)
 
     def launch(i):
         call()
@@ -283,6 +285,13 @@ def main():
         print(f"# decode multi B=256 T=4: kernel {kus:.2f} us ({mgbs:.0f} GB/s of algorithmic "
               f"bytes) vs 4 single steps {4 * line['roofline']['kernel_us']:.1f} us",
               file=sys.stderr, flush=True)
+        # the in-kernel q/k L2-normalisation option on the same inputs
+        r = bench_decode(dev, args.steps // 2, args.warmup, qk_l2norm=True)
+        line["decode_qk_l2norm"] = {"workload": "decode_b256_qk4_v8",
+                                    "kernel_us": round(r["kernel_ms"] * 1e3, 2),
+                                    "decode_kernel_us": line["roofline"]["kernel_us"]}
+        print(f"# decode with q/k L2-norm: {r['kernel_ms'] * 1e3:.2f} us", file=sys.stderr,
+              flush=True)
 
     if args.only in ("all", "prefill"):
         try:
@@ -322,6 +331,13 @@ def main():
             print(f"# prefill with h (bf16, {r['chunks']} chunks, {r['h_bytes'] / 1e6:.0f} MB): "
                   f"{kus:.1f} us against {line['prefill']['roofline']['kernel_us']:.1f} us without",
                   file=sys.stderr, flush=True)
+            # the in-kernel q/k L2-normalisation option on the same inputs
+            r = bench_prefill(dev, args.prefill_steps, PREFILL_WARMUP, qk_l2norm=True)
+            line["prefill_qk_l2norm"] = {
+                "workload": "prefill_varlen8_t32768_qk16_v32", "kernel_us": round(r["kernel_ms"] * 1e3, 2),
+                "prefill_kernel_us": line["prefill"]["roofline"]["kernel_us"]}
+            print(f"# prefill with q/k L2-norm: {r['kernel_ms'] * 1e3:.1f} us", file=sys.stderr,
+                  flush=True)
 
     if args.copy_calibration:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)

@@ -209,9 +209,11 @@ class PreparedDecode:
     repeatedly: arguments are checked and resolved to device pointers at
     construction, the stream is torch's current stream at that time, and
     ``__call__`` only enqueues the kernel.  ``new_state`` may be ``state``.
+    ``qk_l2norm`` as for :func:`gdn_decode`.
     """
 
-    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
+    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *,
+                 qk_l2norm: bool = False):
         B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
         assert state is None or (state.is_contiguous() and state.dtype == torch.float32
                                  and state.shape == (B, nv, D, D))
@@ -223,16 +225,17 @@ class PreparedDecode:
             assert t.is_contiguous()
         A_log, dt_bias = _gates(A_log, dt_bias)
         self._keep = (q, k, v, state, A_log, a, dt_bias, b, output, new_state)
-        self._fn = _capi.lib().gdn_decode_fwd
+        self._fn = _capi.lib().gdn_decode_ex_fwd
         self._args = (
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
             _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
-            B, nq, nv, float(_resolve_scale(scale, q.shape[-1])), _capi.stream_handle(q.device))
+            B, nq, nv, float(_resolve_scale(scale, q.shape[-1])),
+            _capi.GDN_QK_L2NORM if qk_l2norm else 0, _capi.stream_handle(q.device))
 
     def __call__(self) -> None:
         rc = self._fn(*self._args)
         if rc:
-            _capi.check(rc, "gdn_decode_fwd")
+            _capi.check(rc, "gdn_decode_ex_fwd")
 
 
 class PreparedDecodeMulti:
@@ -242,7 +245,8 @@ class PreparedDecodeMulti:
     validated once, ``__call__`` only enqueues the kernel).
     """
 
-    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
+    def __init__(self, q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *,
+                 qk_l2norm: bool = False):
         assert q.dim() == 4 and q.shape[3] == D and k.shape == q.shape
         B, T, nq, _ = q.shape
         assert T >= 1 and v.dim() == 4 and v.shape[:2] == (B, T) and v.shape[3] == D
@@ -262,7 +266,8 @@ class PreparedDecodeMulti:
         self._args = (
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(new_state),
             _capi.ptr(A_log), _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(output),
-            B, T, nq, nv, float(_resolve_scale(scale, D)), 0, _capi.stream_handle(q.device))
+            B, T, nq, nv, float(_resolve_scale(scale, D)), _capi.GDN_QK_L2NORM if qk_l2norm else 0,
+            _capi.stream_handle(q.device))
 
     def __call__(self) -> None:
         rc = self._fn(*self._args)

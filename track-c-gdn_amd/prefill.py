@@ -200,11 +200,11 @@ class PreparedPrefill:
 
     ``cu_seqlens`` is read back once here (the reference's ``cu_seqlens[-1]
     == T`` check); ``__call__`` only enqueues the kernel on the stream that
-    was current at construction.
+    was current at construction.  ``qk_l2norm`` as for :func:`gdn_prefill`.
     """
 
     def __init__(self, q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
-                 final_state):
+                 final_state, *, qk_l2norm: bool = False):
         T, nq, _ = q.shape
         nv = v.shape[1]
         validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv)
@@ -219,15 +219,16 @@ class PreparedPrefill:
         ws = workspace_bytes(N, T, nq, nv)
         self._ws = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
         self._keep = (q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, final_state)
-        self._fn = _capi.lib().gdn_prefill_fwd
+        self._fn = _capi.lib().gdn_prefill_ex_fwd
         self._args = (
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
             _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu_seqlens),
             1 if cu_seqlens.dtype == torch.int32 else 0, N, T, nq, nv,
             float(_resolve_scale(scale)), _capi.ptr(output), _capi.ptr(final_state),
-            _capi.ptr(self._ws), ws, _capi.stream_handle(q.device))
+            _capi.ptr(self._ws), ws, _capi.GDN_QK_L2NORM if qk_l2norm else 0,
+            _capi.stream_handle(q.device))
 
     def __call__(self) -> None:
         rc = self._fn(*self._args)
         if rc:
-            _capi.check(rc, "gdn_prefill_fwd")
+            _capi.check(rc, "gdn_prefill_ex_fwd")
