@@ -98,21 +98,6 @@ __device__ __forceinline__ float l2norm_factor_row16(const float (&x)[8]) {
   return l2norm_rsqrt(row16_sum(ss));
 }
 
-// Sum of squares of 8 packed bf16 values (two per dword), one v_dot2 each.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float sum_sq_bf16x8(uint4 w) {
-  float s = 0.f;
-  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x),
-                                      __builtin_bit_cast(bf16x2_t, w.x), s, false);
-  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y),
-                                      __builtin_bit_cast(bf16x2_t, w.y), s, false);
-  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z),
-                                      __builtin_bit_cast(bf16x2_t, w.z), s, false);
-  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w),
-                                      __builtin_bit_cast(bf16x2_t, w.w), s, false);
-  return s;
-}
-
 __device__ __forceinline__ void l2norm_row16(float (&x)[8]) {
   const float r = l2norm_factor_row16(x);
 #pragma unroll

@@ -5,7 +5,8 @@
 // :1570-1633, 1728-1759, 1762-1802) by one launch: a workgroup owns one
 // (sequence, v-head) chain and walks its 64-token chunks in order, gates
 // included.  The fp32 state S [V=128, K=128] never leaves registers between
-// chunks, and nothing but q/k/v/a/b is read and o / final state written.
+// chunks, and nothing but q/k/v/a/b is read and o / final state written (and,
+// in the kH instantiation, the state entering every chunk).
 //
 // Per chunk (C = 64 rows, gam = chunk-local cumsum of the log-decay,
 // S = state at chunk start), the same mathematics as the reference
@@ -24,8 +25,10 @@
 // only reaches the bf16 output, takes the raw bf16 Q rows and a bf16 copy of
 // S.  All products accumulate in fp32.
 //
-// Chain wave w (of 8) owns state rows v in [16w, 16w+16): every product that
-// touches S, X, Vn or O is split along v, so the waves never exchange state.
+// Chain wave w (of 4) owns state rows v in [32w, 32w+32), two 16-row column
+// tiles: every product that touches S, X, Vn or O is split along v, so the
+// chain waves never exchange state.  Four preparation waves build the next
+// chunk's A, Tm, P, gates and LDS copies alongside.
 // The state lives as S^T accumulator tiles of 16x16x32 MFMAs; because an MFMA
 // reduces over an arbitrary pairing of its k-slots, two stacked accumulator
 // tiles are used directly as the B operand of the next product (k-slot e of
@@ -267,6 +270,7 @@ using IC = std::integral_constant<int, N>;
 // phase at the end of the phase before whenever no wave overwrites them in
 // between, and its barriers leave those reads in flight.  Which wave computes
 // which tile is fixed at compile time, so tile offsets are immediates.
+//
 // kL2 (option GDN_QK_L2NORM): the q and k rows are used L2-normalised.  The
 // copying waves compute each row's factor (sum x^2 + 1e-6)^(-1/2) from the
 // rows they copied, right after their wait for them, and the factors scale
