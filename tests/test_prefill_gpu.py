@@ -150,3 +150,28 @@ def test_prefill_benchmark_workloads(device, name):
     torch.cuda.synchronize()
     x64 = dict(x, cu_seqlens=x["cu_seqlens"].long())
     _check(o, s, *_oracle(x64))
+
+
+def test_prefill_long_sequence_split_is_bit_exact(device):
+    """One 131 072-token sequence (2 048 chunks per chain): the run split at
+    a chunk boundary, the second half started from the first half's final
+    state, reproduces the single run bit for bit (same operations in the
+    same order; the fp32 state passes through memory unchanged)."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    T, H = 131072, 65536
+    print(f"prefill long sequence T={T}", flush=True)
+    x = inp.prefill_inputs([T], seed=4500, with_state=True)
+    g = _to(x, device)
+    o, s = _run(pre, g)
+    a = {k: (v[:H] if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == T else v) for k, v in g.items()}
+    b = {k: (v[H:] if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == T else v) for k, v in g.items()}
+    a["cu_seqlens"] = torch.tensor([0, H], dtype=torch.int64, device=device)
+    b["cu_seqlens"] = torch.tensor([0, T - H], dtype=torch.int64, device=device)
+    oa, sa = _run(pre, a)
+    b["state"] = sa
+    ob, sb = _run(pre, b)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([oa, ob]), o)
+    assert torch.equal(sb, s)
+    assert bool(torch.isfinite(s).all()) and float(s.abs().max()) < 1e3
