@@ -144,3 +144,35 @@ def test_decode_pool_matches_gather_step_scatter(device):
     pool_ref[idx] = s_ref
     _check(out[valid], pool_d, o_ref, pool_ref)
     assert torch.count_nonzero(out[3]) == 0
+
+
+def test_decode_pool_full_size_b1024_qk16_v32(device):
+    """Decode at batch 1024 against a [1024, 32, 128, 128] fp32 pool (2 GiB),
+    slots a random permutation: equal bit for bit to gather -> dense decode ->
+    scatter (same per-head arithmetic), and four sequences against the fp64
+    oracle on the operator bars."""
+    dec = pkg_module("decode")
+    inp = pkg_module("inputs")
+    B, HQ, HV = 1024, 16, 32
+    print(f"decode pool B={B} HQ={HQ} HV={HV}", flush=True)
+    x = inp.decode_inputs(B, HQ=HQ, HV=HV, seed=4600, with_state=False)
+    g = _to(x, device)
+    gen = torch.Generator(device=device).manual_seed(4601)
+    pool = torch.randn(B, HV, 128, 128, device=device, generator=gen) * 0.02
+    slots = torch.randperm(B, generator=torch.Generator().manual_seed(4602)).to(torch.int32)
+    dense = pool[slots.long().to(device)]
+    pool_run = pool.clone()
+    out = dec.decode_pool_(g["q"], g["k"], g["v"], pool_run, slots.to(device), g["A_log"], g["a"],
+                           g["dt_bias"], g["b"], g["scale"])
+    o_d, s_d = dec.gdn_decode(g["q"], g["k"], g["v"], dense, g["A_log"], g["a"], g["dt_bias"],
+                              g["b"], g["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, o_d)
+    assert torch.equal(pool_run[slots.long().to(device)], s_d)
+    del dense, pool_run
+    for n in (0, 1, 511, 1023):
+        sl = slice(n, n + 1)
+        o_ref, s_ref = O.decode_step(x["q"][sl], x["k"][sl], x["v"][sl],
+                                     pool[int(slots[n])][None].cpu(), x["A_log"], x["a"][sl],
+                                     x["dt_bias"], x["b"][sl], x["scale"])
+        _check(o_d[sl], s_d[sl], o_ref, s_ref)
