@@ -121,6 +121,24 @@ def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4, qk_l2norm=False)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=nbytes)
 
 
+def bench_decode_pool(dev, steps, warmup, B=1024, HQ=16, HV=32):
+    """One decode step of batch B against a [B, HV, 128, 128] pool (slot ids a
+    random permutation), updated in place."""
+    x = ginp.decode_inputs(B, HQ, HV, seed=1004, with_state=False)
+    g = _to(x, dev)
+    gen = torch.Generator(device=dev).manual_seed(1004)
+    pool = torch.randn(B, HV, D, D, device=dev, generator=gen) * 0.02
+    slots = torch.randperm(B, generator=torch.Generator().manual_seed(1004)).to(torch.int32).to(dev)
+    o = torch.empty(B, 1, HV, D, dtype=torch.bfloat16, device=dev)
+
+    def launch(i):
+        gdec.decode_pool_(g["q"], g["k"], g["v"], pool, slots, g["A_log"], g["a"], g["dt_bias"],
+                          g["b"], g["scale"], output=o)
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=decode_bytes(B, HQ, HV) + 4 * B)
+
+
 def decode_multi_bytes(B: int, T: int, HQ: int, HV: int) -> int:
     """State read + write once, per-token inputs and outputs T times."""
     return B * HV * 2 * D * D * 4 + T * B * (HV * (2 * D * 2 + 4) + HQ * 2 * D * 2)
@@ -285,6 +303,17 @@ def main():
         print(f"# decode multi B=256 T=4: kernel {kus:.2f} us ({mgbs:.0f} GB/s of algorithmic "
               f"bytes) vs 4 single steps {4 * line['roofline']['kernel_us']:.1f} us",
               file=sys.stderr, flush=True)
+        # slot-pool decode at batch 1024, qk16/v32 (a [1024, 32, 128, 128] pool, 2 GiB)
+        r = bench_decode_pool(dev, max(args.steps // 10, 5), args.warmup)
+        pgbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+        line["decode_pool"] = {
+            "workload": "decode_pool_b1024_qk16_v32", "batch": 1024, "pool": [1024, 32, 128, 128],
+            "kernel_us": round(r["kernel_ms"] * 1e3, 2),
+            "roofline": {"bound": "hbm", "achieved": round(pgbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(pgbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_launch": r["bytes"]}}
+        print(f"# decode pool B=1024 qk16/v32: {r['kernel_ms'] * 1e3:.1f} us, {pgbs:.0f} GB/s "
+              f"({pgbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)", file=sys.stderr, flush=True)
         # the in-kernel q/k L2-normalisation option on the same inputs
         r = bench_decode(dev, args.steps // 2, args.warmup, qk_l2norm=True)
         line["decode_qk_l2norm"] = {"workload": "decode_b256_qk4_v8",
