@@ -116,7 +116,9 @@ int gdn_decode_multi_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          int B, int T, int HQ, int HV, float scale, int flags, void* stream);
 
 /*
- * Workspace bytes gdn_prefill_fwd needs for this problem (may be 0).
+ * Workspace bytes gdn_prefill_fwd uses for this problem on the current
+ * device: the split path's workspace when it would run (few chains, see
+ * gdn_prefill_fwd), else 0.
  */
 size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV);
 
@@ -130,9 +132,16 @@ size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV);
  *   final_state : [N, HV, V, K] fp32 output.
  *   cu_seqlens  : device array, N+1 entries, cu_seqlens[0] == 0,
  *                 cu_seqlens[N] == T, non-decreasing (empty sequences allowed).
- *   scale       : the caller resolves None/0 to 1/sqrt(D) (kernel.py:1777-1778).
- *   workspace   : device buffer of at least gdn_prefill_workspace_bytes(...)
- *                 bytes (that is 0 in this implementation: NULL is accepted).
+ *   scale       : any float; the caller resolves None/0 to 1/sqrt(D)
+ *                 (kernel.py:1777-1778).  A negative scale negates the output.
+ *   workspace   : device buffer of gdn_prefill_workspace_bytes(...) bytes, or
+ *                 NULL.  With few (sequence, v-head) chains the split path
+ *                 runs when the workspace is given (gdn_prefill_split_fwd with
+ *                 the automatic slice count); without it, and with many
+ *                 chains, one fused workgroup per chain.
+ * Input range: the state path multiplies fp16 operands (k, the state, X and
+ * Vn); values must stay below 65504 in magnitude (normalised q / k, v and
+ * states of ordinary magnitude are far inside), else results overflow.
  * Sequences whose cu_seqlens ranges overlap or run backwards are read in
  * bounds, but their results are unspecified.
  */
@@ -155,6 +164,34 @@ int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                        int HQ, int HV, float scale,
                        uint16_t* out, float* final_state,
                        void* workspace, size_t workspace_bytes, int flags, void* stream);
+
+/*
+ * Workspace bytes of gdn_prefill_split_fwd: 14 080 bytes per (chunk, v-head)
+ * and 18 432 per (chunk, qk-head) for an upper bound of T / 64 + N chunks.
+ */
+size_t gdn_prefill_split_workspace_bytes(int N, int T, int HQ, int HV);
+
+/*
+ * gdn_prefill_ex_fwd on the split path, for batches with fewer chains than
+ * the GPU has CUs: a launch over all (chunk, v-head) pairs forms each
+ * chunk's state-independent operands (gates, the diagonal blocks of
+ * (I + A)^-1, -A_ba, P, fp16 K) in the workspace, then every chain runs as
+ * `slices` workgroups (4 or 8), each owning 128 / slices rows of the state.
+ * This is how the reference spreads its recurrence over the GPU: the
+ * per-chunk kernels over all chunks, the recurrence over V-slices
+ * (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:544, 1005, 1369).
+ * The final state equals gdn_prefill_ex_fwd's bit for bit without
+ * GDN_QK_L2NORM; outputs agree to within 1e-4.
+ *   workspace : at least gdn_prefill_split_workspace_bytes(...) bytes, else
+ *               GDN_ERR_WORKSPACE.  Other slice counts: GDN_ERR_SHAPE.
+ */
+int gdn_prefill_split_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                          const float* state, const float* A_log, const uint16_t* a,
+                          const float* dt_bias, const uint16_t* b,
+                          const void* cu_seqlens, int cu_is_int32, int N, int T,
+                          int HQ, int HV, float scale,
+                          uint16_t* out, float* final_state, int slices,
+                          void* workspace, size_t workspace_bytes, int flags, void* stream);
 
 /*
  * Number of 64-token chunks of a varlen batch, sum over n of

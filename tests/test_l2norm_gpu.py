@@ -136,7 +136,8 @@ def test_decode_multi_l2norm(device, B, T, HQ, HV):
 @pytest.mark.parametrize("lens,HQ,HV,with_state", [
     ([100, 37], 4, 8, True), ([1, 63, 64, 65, 129], 4, 8, True), ([0, 300], 4, 8, False),
     ([130, 70], 16, 32, True), ([1000, 777], 4, 8, True)])
-def test_prefill_l2norm_matches_oracle(device, lens, HQ, HV, with_state):
+@pytest.mark.parametrize("path", ["auto", "fused"])
+def test_prefill_l2norm_matches_oracle(device, lens, HQ, HV, with_state, path):
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
     print(f"prefill l2norm lens={lens} HQ={HQ} HV={HV}", flush=True)
@@ -145,7 +146,7 @@ def test_prefill_l2norm_matches_oracle(device, lens, HQ, HV, with_state):
     x["q"] = _raw_qk((T, HQ, 128), 3800 + T, zero_rows=[(T - 1, 0)])
     x["k"] = _raw_qk((T, HQ, 128), 3900 + T, zero_rows=[(T // 2, HQ - 1)])
     g = _to(x, device)
-    o, s = pre.gdn_prefill(*[g[n] for n in PRE_NAMES], g["scale"], qk_l2norm=True)
+    o, s = pre.gdn_prefill(*[g[n] for n in PRE_NAMES], g["scale"], qk_l2norm=True, path=path)
     torch.cuda.synchronize()
     xn = _normalised(x)
     o_ref, s_ref = O.prefill_chunked(*[xn[n] for n in PRE_NAMES], x["scale"])

@@ -1,4 +1,6 @@
-"""GPU parity of the fused HIP prefill kernel against the CPU oracle (fp64).
+"""GPU parity of the HIP prefill paths (the fused chain kernel, and the
+library's automatic choice, which is the split path for few chains) against
+the CPU oracle (fp64).
 
 Bar: output (bf16) within atol = rtol = 1e-2; final state relative error
 (Frobenius, per sequence and overall) <= 1e-3.
@@ -50,13 +52,19 @@ def _run(pre, g, **kw):
 @pytest.mark.parametrize("lens,with_state", [
     ([100, 37], True), ([64], False), ([1], True), ([0, 5], True), ([1, 63, 64, 65, 129], True),
     ([128, 0, 0, 300], False), ([200], True)])
-def test_prefill_small_matches_oracle(device, lens, with_state):
+@pytest.mark.parametrize("path", ["run", "fused"])
+def test_prefill_small_matches_oracle(device, lens, with_state, path):
+    """Through the reference-compatible ``run`` (the library's path choice:
+    the split path at these few chains) and through the fused chain kernel."""
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
-    print(f"prefill lens={lens} state={with_state}", flush=True)
+    print(f"prefill lens={lens} state={with_state} path={path}", flush=True)
     x = inp.prefill_inputs(lens, seed=sum(lens) + 7, with_state=with_state)
     g = _to(x, device)
-    o, s = pre.run(*[g[n] for n in NAMES], g["scale"])
+    if path == "run":
+        o, s = pre.run(*[g[n] for n in NAMES], g["scale"])
+    else:
+        o, s = _run(pre, g, path="fused")
     torch.cuda.synchronize()
     assert o.shape == (sum(lens), 8, 128) and o.dtype == torch.bfloat16
     assert s.shape == (len(lens), 8, 128, 128) and s.dtype == torch.float32
@@ -123,14 +131,15 @@ def test_prefill_single_token_equals_decode(device):
     assert float((s - sd).norm() / sd.norm()) <= STATE_REL_BAR
 
 
-def test_prefill_weak_decay_precision(device):
+@pytest.mark.parametrize("path", ["auto", "fused"])
+def test_prefill_weak_decay_precision(device, path):
     """Near-unit decay keeps long memory: the regime where bf16 intermediates fail the bar."""
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
     x = inp.prefill_inputs([700, 333], seed=27, with_state=True)
     x["A_log"] = torch.rand(8, generator=torch.Generator().manual_seed(3)) * 2.0 - 9.0
     g = _to(x, device)
-    o, s = _run(pre, g)
+    o, s = _run(pre, g, path=path)
     torch.cuda.synchronize()
     _check(o, s, *_oracle(x))
 
@@ -138,6 +147,8 @@ def test_prefill_weak_decay_precision(device):
 @pytest.mark.parametrize("name", ["prefill_t4096_n1_qk4_v8", "prefill_varlen16_qk4_v8",
                                   "prefill_varlen8_t32768_qk16_v32"])
 def test_prefill_benchmark_workloads(device, name):
+    """The library's path choice at each workload (split for the first two,
+    fused for the third) against the fp64 oracle."""
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
     w = inp.WORKLOADS[name]
@@ -152,7 +163,8 @@ def test_prefill_benchmark_workloads(device, name):
     _check(o, s, *_oracle(x64))
 
 
-def test_prefill_long_sequence_split_is_bit_exact(device):
+@pytest.mark.parametrize("path", ["auto", "fused"])
+def test_prefill_long_sequence_split_is_bit_exact(device, path):
     """One 131 072-token sequence (2 048 chunks per chain): the run split at
     a chunk boundary, the second half started from the first half's final
     state, reproduces the single run bit for bit (same operations in the
@@ -160,17 +172,17 @@ def test_prefill_long_sequence_split_is_bit_exact(device):
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
     T, H = 131072, 65536
-    print(f"prefill long sequence T={T}", flush=True)
+    print(f"prefill long sequence T={T} path={path}", flush=True)
     x = inp.prefill_inputs([T], seed=4500, with_state=True)
     g = _to(x, device)
-    o, s = _run(pre, g)
+    o, s = _run(pre, g, path=path)
     a = {k: (v[:H] if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == T else v) for k, v in g.items()}
     b = {k: (v[H:] if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == T else v) for k, v in g.items()}
     a["cu_seqlens"] = torch.tensor([0, H], dtype=torch.int64, device=device)
     b["cu_seqlens"] = torch.tensor([0, T - H], dtype=torch.int64, device=device)
-    oa, sa = _run(pre, a)
+    oa, sa = _run(pre, a, path=path)
     b["state"] = sa
-    ob, sb = _run(pre, b)
+    ob, sb = _run(pre, b, path=path)
     torch.cuda.synchronize()
     assert torch.equal(torch.cat([oa, ob]), o)
     assert torch.equal(sb, s)

@@ -47,7 +47,7 @@ def test_prefill_h_matches_oracle(device, lens, HQ, HV, with_state, l2):
     x = inp.prefill_inputs(lens, HQ=HQ, HV=HV, seed=4100 + sum(lens), with_state=with_state)
     g = _to(x, device)
     o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2)
-    o0, s0 = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2)
+    o0, s0 = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2, path="fused")
     torch.cuda.synchronize()
     assert torch.equal(o, o0) and torch.equal(s, s0)
     offs = O.chunk_offsets(x["cu_seqlens"], 64)

@@ -1,0 +1,175 @@
+"""GPU parity of the split prefill path (parallel chunk preparation + state
+slices) against the CPU oracle (fp64) and against the fused chain kernel.
+
+Bars: output (bf16) within atol = rtol = 1e-2; final state relative error
+(Frobenius, per sequence and overall) <= 1e-3.  Without the L2-norm option
+the split path performs the state-path operations of the fused kernel in the
+same order: the final states must be equal bit for bit.  The outputs agree
+to within 1e-4 (in a few elements per million a P entry rounds to the other
+neighbouring fp16 value; both paths are equally close to the oracle there).
+"""
+
+import pytest
+import torch
+
+from conftest import pkg_module
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+STATE_REL_BAR = 1e-3
+NAMES = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+
+
+def _to(x, dev):
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in x.items()}
+
+
+def _check(o, s, o_ref, s_ref):
+    torch.testing.assert_close(o.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    s = s.cpu().double()
+    rel = float((s - s_ref).norm() / s_ref.norm().clamp_min(1e-300))
+    assert rel <= STATE_REL_BAR, rel
+    for n in range(s.shape[0]):
+        nr = float(s_ref[n].norm())
+        if nr > 0:
+            assert float((s[n] - s_ref[n]).norm()) / nr <= STATE_REL_BAR, n
+        else:
+            assert float(s[n].abs().max()) == 0.0
+    return rel
+
+
+def _same(o, s, of, sf):
+    """States equal bit for bit; outputs equal but for rare last-place roundings."""
+    assert torch.equal(s, sf)
+    d = (o.float() - of.float()).abs()
+    assert float(d.max()) <= 1e-4, float(d.max())
+    assert int((d > 0).sum()) <= max(1, o.numel() // 100000)
+
+
+def _run(g, **kw):
+    pre = pkg_module("prefill")
+    return pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], **kw)
+
+
+def _oracle(x):
+    x64 = dict(x, cu_seqlens=x["cu_seqlens"].long())
+    return O.prefill_recurrent(*[x64[n] for n in NAMES], x["scale"])
+
+
+@pytest.mark.parametrize("slices", [4, 8])
+@pytest.mark.parametrize("lens,with_state,cu32", [
+    ([100, 37], True, False), ([64], False, True), ([1], True, False), ([0, 5], True, True),
+    ([1, 63, 64, 65, 129], True, False), ([128, 0, 0, 300], False, False), ([200], True, True)])
+def test_split_small_matches_oracle_and_fused(device, slices, lens, with_state, cu32):
+    inp = pkg_module("inputs")
+    print(f"split slices={slices} lens={lens} state={with_state} int32={cu32}", flush=True)
+    x = inp.prefill_inputs(lens, seed=sum(lens) + 11, with_state=with_state,
+                           cu_dtype=torch.int32 if cu32 else torch.int64)
+    g = _to(x, device)
+    o, s = _run(g, path="split", slices=slices)
+    of, sf = _run(g, path="fused")
+    torch.cuda.synchronize()
+    _check(o, s, *_oracle(x))
+    _same(o, s, of, sf)
+
+
+@pytest.mark.parametrize("HQ,HV", [(16, 32), (4, 4), (1, 4), (2, 8)])
+def test_split_head_layouts(device, HQ, HV):
+    inp = pkg_module("inputs")
+    print(f"split heads HQ={HQ} HV={HV}", flush=True)
+    x = inp.prefill_inputs([90, 170, 3], HQ=HQ, HV=HV, seed=HQ * 7 + HV, with_state=True)
+    g = _to(x, device)
+    o, s = _run(g, path="split", slices=4)
+    of, sf = _run(g, path="fused")
+    torch.cuda.synchronize()
+    _check(o, s, *_oracle(x))
+    _same(o, s, of, sf)
+
+
+@pytest.mark.parametrize("slices", [4, 8])
+def test_split_qk_l2norm(device, slices):
+    """Raw (unnormalised) q / k rows, normalised inside the kernels."""
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs([150, 64, 7], seed=77, with_state=True)
+    gen = torch.Generator().manual_seed(78)
+    x["q"] = (torch.randn(x["q"].shape, generator=gen) * 3.0).to(torch.bfloat16)
+    x["k"] = (torch.randn(x["k"].shape, generator=gen) * 0.5).to(torch.bfloat16)
+    x["k"][5] = 0
+    g = _to(x, device)
+    o, s = _run(g, path="split", slices=slices, qk_l2norm=True)
+    torch.cuda.synchronize()
+    xn = dict(x, q=O.qk_l2norm(x["q"]), k=O.qk_l2norm(x["k"]))
+    x64 = dict(xn, cu_seqlens=x["cu_seqlens"].long())
+    o_ref, s_ref = O.prefill_recurrent(*[x64[n] for n in NAMES], x["scale"])
+    _check(o, s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("path", ["split", "fused"])
+def test_negative_scale(device, path):
+    """A negative scale flips the sign of the output and leaves the state alone."""
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs([130, 20], seed=91, with_state=True)
+    x["scale"] = -0.3
+    g = _to(x, device)
+    o, s = _run(g, path=path)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o.float()).all())
+    _check(o, s, *_oracle(x))
+
+
+def test_auto_path_uses_split_for_few_chains(device):
+    """With few chains the library's own choice is the split path (it asks
+    for a workspace), and its results equal the fused kernel's."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs([4096], seed=1002)
+    assert pre.workspace_bytes(1, 4096, 4, 8) == pre.split_workspace_bytes(1, 4096, 4, 8) > 0
+    g = _to(x, device)
+    o, s = _run(g)
+    of, sf = _run(g, path="fused")
+    torch.cuda.synchronize()
+    _same(o, s, of, sf)
+
+
+@pytest.mark.parametrize("name,slices", [("prefill_t4096_n1_qk4_v8", 8),
+                                         ("prefill_varlen16_qk4_v8", 4)])
+def test_split_benchmark_workloads(device, name, slices):
+    inp = pkg_module("inputs")
+    w = inp.WORKLOADS[name]
+    lens = inp.workload_lengths(name)
+    print(f"split workload {name} T={sum(lens)} slices={slices}", flush=True)
+    x = inp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"],
+                           cu_dtype=torch.int32)
+    g = _to(x, device)
+    o, s = _run(g, path="split", slices=slices)
+    of, sf = _run(g, path="fused")
+    torch.cuda.synchronize()
+    _same(o, s, of, sf)
+    x64 = dict(x, cu_seqlens=x["cu_seqlens"].long())
+    _check(o, s, *O.prefill_chunked(*[x64[n] for n in NAMES], x["scale"]))
+
+
+def test_split_workspace_errors(device):
+    """The split entry point refuses a missing or short workspace and a bad slice count."""
+    capi = pkg_module("_capi")
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs([100], seed=5)
+    g = _to(x, device)
+    out = torch.empty(100, 8, 128, dtype=torch.bfloat16, device=device)
+    fs = torch.empty(1, 8, 128, 128, dtype=torch.float32, device=device)
+    need = pre.split_workspace_bytes(1, 100, 4, 8)
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    p = capi.ptr
+    args = [p(g["q"]), p(g["k"]), p(g["v"]), 0, p(g["A_log"]), p(g["a"]), p(g["dt_bias"]),
+            p(g["b"]), p(g["cu_seqlens"]), 0, 1, 100, 4, 8, float(x["scale"]), p(out), p(fs)]
+    lib = capi.lib()
+    st = capi.stream_handle(device)
+    assert lib.gdn_prefill_split_fwd(*args, 8, None, 0, 0, st) == capi.GDN_ERR_WORKSPACE
+    assert lib.gdn_prefill_split_fwd(*args, 8, p(ws), need - 1, 0, st) == capi.GDN_ERR_WORKSPACE
+    assert lib.gdn_prefill_split_fwd(*args, 3, p(ws), need, 0, st) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_split_fwd(*args, 2, p(ws), need, 0, st) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_split_fwd(*args, 8, p(ws), need, 0, st) == capi.GDN_OK
+    torch.cuda.synchronize()
+    _check(out, fs, *_oracle(x))

@@ -18,10 +18,14 @@ INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libgdn_hip.so"
 ARCH = "gfx950"
 
-# Packed fp32 VALU ops are disabled for every HIP translation unit.
+# Packed fp32 VALU ops are disabled for every HIP translation unit.  MFMA
+# accumulators stay in VGPRs (amdgpu-mfma-vgpr-form): kernels that run one
+# wave per SIMD would otherwise get AGPR accumulators and a copy to VGPRs for
+# every VALU touch of them.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
 ]
 

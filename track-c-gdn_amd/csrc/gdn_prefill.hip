@@ -36,28 +36,14 @@
 // the matching order (the p32 column order below): no cross-lane shuffles,
 // only fp32->fp16 packs.
 
-#include <type_traits>
-
-#include "gdn_common.h"
+#include "gdn_prefill_common.h"
+#include "gdn_prefill_split.h"
 #include "../../include/gdn_hip.h"
 
 namespace {
 
 using namespace gdn;
 
-constexpr int D = kHeadDim;   // 128
-constexpr int C = 64;         // chunk
-// Row strides, chosen so that the MFMA operand reads (16-byte reads down 16
-// rows, and the transposing 8-byte reads down 4 rows x 4 quads) are free of
-// LDS bank conflicts: rows of 288 B (Kc, A) and 160 B (Tm / P).
-constexpr int KCLD = D + 16;  // Kc row stride (halves): 288 B rows
-constexpr int TLD = C + 16;   // Tm / P row stride (halves): 160 B rows
-constexpr int ALD = C + 8;    // A row stride (floats): 288 B rows
-constexpr int BLD = C / 2 + 8;  // Aba row stride (halves): 80 B rows
-// Gate data per chunk, GSZ floats: gam log2(e) | beta | e^gam | scale e^gam | e^(gam_L - gam)
-// (gam = chunk-local cumsum of the log-decay, gam_L its value at the chunk's last token).
-constexpr int G_L2 = 0, G_BETA = C, G_EG = 2 * C, G_EGS = 3 * C, G_ED = 4 * C;
-constexpr int GSZ = 5 * C;
 constexpr int kChainWaves = 4;              // state-chain waves, one per SIMD, 32 state rows each
 constexpr int kPrepWaves = 4;               // preparation / copy waves, one per SIMD
 constexpr int kWaves = kChainWaves + kPrepWaves;
@@ -65,182 +51,6 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kPrepThreads = kPrepWaves * 64;
 constexpr int kRowsPerWave = D / kChainWaves;   // state rows (v) per chain wave
 constexpr int kTiles = kRowsPerWave / 16;        // 16-row column tiles per chain wave
-
-typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-
-// Column order inside every 32-column group of the fp16 operand tiles: column
-// 16 a + 4 q + r is stored at position 8 q + 4 a + r.  The 8 k-slots that
-// lane group q feeds a 16x16x32 MFMA from two stacked 16x16 accumulator tiles
-// -- rows 4q..4q+3 of each -- are then 16 contiguous bytes, and every quad
-// of 4 consecutive columns stays contiguous.
-__device__ __forceinline__ int p32(int c) {
-  return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
-}
-
-// Raw bf16 rows as copied from HBM: 16-byte chunk c of row t sits in slot
-// c ^ (t & 15) of that row (the copy picks which global chunk each lane
-// fetches), so column reads down 16 consecutive rows hit 16 distinct banks.
-__device__ __forceinline__ int raw_off(int t, int col) { return t * D + 8 * ((col >> 3) ^ (t & 15)) + (col & 7); }
-
-struct __align__(16) SmemRaw {
-  uint16_t k[2][C * D];        // K rows of the chunks of parity 0 / 1 (bf16, swizzled), DMA target
-  uint16_t q[2][C * D];        // Q rows of the chunks of parity 0 / 1 (bf16, swizzled), DMA target
-};
-
-struct __align__(16) Smem {
-  _Float16 Kc[2][C * KCLD];    // K chunk in fp16 [t][p32(k)], double-buffered
-  _Float16 Tm[C * TLD];        // diagonal 32-row blocks of (I + A)^-1 [t][p32(t')]
-  _Float16 P[C * TLD];         // decayed causal Q K^T [t][p32(t')]
-  float A[C * ALD];            // beta-scaled decayed strict K K^T [t][t'] (fp32), diagonal 32-row blocks
-  _Float16 Aba[(C / 2) * BLD]; // its lower-left 32x32 block, negated, in fp16 [t - 32][p32(t')]
-};
-
-// Workgroup barrier for LDS traffic only: waits for this wave's LDS
-// operations, not for outstanding global stores or HBM->LDS copies.  The asm
-// statement is a compiler memory barrier as well.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Workgroup barrier that leaves up to N of this wave's most recent LDS reads
-// in flight.  For a wave that reads LDS and never writes it: every read whose
-// value it has used before the barrier has completed, and what may still be
-// outstanding are reads whose values are used after it -- reads of data that
-// no wave overwrites in the next phase.
-template <int N>
-__device__ __forceinline__ void lds_barrier_keep() {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" :: "n"(N) : "memory");
-}
-
-// Waits until at most N vector-memory operations of this wave are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
-}
-
-__device__ __forceinline__ f16x8 ld16(const _Float16* p) { return *reinterpret_cast<const f16x8*>(p); }
-
-__device__ __forceinline__ bf16x8_t ld16_bf(const uint16_t* p) {
-  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
-}
-
-// Transposing LDS read (ds_read_b64_tr_b16): inside each 16-lane group, lane i
-// receives element i % 4 of the 8-byte reads issued by lanes 4 m + i / 4,
-// m = 0..3, of the same group.
-__device__ __forceinline__ f16x4_t ld_tr16(const _Float16* p) {
-  return __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                         (__attribute__((address_space(3))) i16x4_t*)p));
-}
-
-__device__ __forceinline__ f16x8 ld_f32x8_as_f16(const float* p) {
-  const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
-  return f16x8{(_Float16)lo[0], (_Float16)lo[1], (_Float16)lo[2], (_Float16)lo[3],
-               (_Float16)hi[0], (_Float16)hi[1], (_Float16)hi[2], (_Float16)hi[3]};
-}
-
-// Two stacked 16x16 accumulator tiles -> one 8-slot fp16 operand.
-__device__ __forceinline__ f16x8 pack2(const f32x4& a, const f32x4& b) {
-  return f16x8{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
-               (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
-}
-
-// Two stacked 16x16 accumulator tiles -> one 8-slot bf16 operand.
-__device__ __forceinline__ bf16x8_t pack2_bf(const f32x4& a, const f32x4& b) {
-  return bf16x8_t{(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
-                  (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
-}
-
-__device__ __forceinline__ f16x8 pack8(const f32x16& x, int s) {
-  f16x8 r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (_Float16)x[8 * s + e];
-  return r;
-}
-
-__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x4 mfma16_bf(bf16x8_t a, bf16x8_t b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x4 mfma16k16(f16x4_t a, f16x4_t b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
-
-// Row of accumulator element i for lane half h (32x32 layout).
-__device__ __forceinline__ int acc_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
-
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
-
-// HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l's
-// bytes land at lds_dst + 16 l; lds_dst must be uniform across the wave.
-// Issued from asm so that the compiler does not wait for it at LDS accesses
-// it cannot tell apart from the destination; every consumer of the copied
-// data waits for it explicitly (wait_vm) and then crosses a barrier.
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
-  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(lds_addr), "v"(src) : "memory");
-}
-
-// The same copy from base + off: base uniform (an SGPR pair), off a 32-bit
-// lane offset (no 64-bit address arithmetic per copy).
-__device__ __forceinline__ void lds_dma16_saddr(const void* base, uint32_t off, void* lds_dst) {
-  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(off), "s"(base) : "memory");
-}
-
-// Round-to-nearest-even fp32 pair -> packed bf16 pair (one v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
-}
-
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-// 16 bytes to base + off: base uniform (an SGPR pair), off a 32-bit lane offset.
-// Nothing in the kernel reads what these stores write.
-// A store of more than 8 bytes keeps reading its data VGPRs after issue: a
-// VALU write to them needs 2 wait states first (the compiler counts them for
-// its own stores, not for this asm), hence the s_nop.
-__device__ __forceinline__ void store_b128_saddr(char* base, uint32_t off, u32x4_t data) {
-  asm volatile("global_store_dwordx4 %0, %1, %2\n\ts_nop 1" :: "v"(off), "v"(data), "s"(base)
-               : "memory");
-}
-
-// Tokens [bos, bos + len) of sequence n, clamped into [0, T].
-template <typename CuT>
-__host__ __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {
-  long long b0 = (long long)cu[n], e0 = (long long)cu[n + 1];
-  b0 = b0 < 0 ? 0 : (b0 > T ? T : b0);
-  e0 = e0 < b0 ? b0 : (e0 > T ? T : e0);
-  bos = int(b0);
-  len = int(e0 - b0);
-}
-
-// Lower 16x16 tiles of a 64x64 chunk matrix, row-major: tile -> (ti, tj).
-template <int TILE>
-struct Tile16 {
-  static constexpr int ti = TILE < 1 ? 0 : TILE < 3 ? 1 : TILE < 6 ? 2 : 3;
-  static constexpr int tj = TILE - (ti * (ti + 1)) / 2;
-};
-template <int N>
-using IC = std::integral_constant<int, N>;
 
 // The state chain.  One workgroup of 8 waves per (sequence, v-head), two on
 // each SIMD: waves 0-3 run the chain (wave w owns state rows v in
@@ -322,7 +132,9 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   int ptid = tid - kChainWaves * 64;          // preparation thread index
   const int v0 = kRowsPerWave * (wave & (kChainWaves - 1));
   const int vrow = v0 + c;        // state row v owned by this lane (chain waves)
-  const float scale_l2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__log2f(scale))));
+  // |scale| enters the P exponent and its sign the P product (scale < 0 is allowed)
+  const float scale_l2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__log2f(fabsf(scale)))));
+  const bool neg_scale = scale < 0.f;
 
   int bos, len;
   seq_bounds(cu_seqlens, n, T, bos, len);
@@ -558,6 +370,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
+    if (neg_scale) acc = -acc;
     const float gr = gd[G_L2 + 16 * ti + c] + scale_l2;
     const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
     if constexpr (kL2) acc *= nq(pb)[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk(pb)[16 * tj + 4 * g]);
@@ -1196,11 +1009,13 @@ int prefill_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
 }  // namespace
 
 extern "C" size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV) {
-  (void)N;
-  (void)T;
-  (void)HQ;
-  (void)HV;
-  return 0;
+  if (N <= 0 || T <= 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return 0;
+  return gdn::prefill_split_auto_slices(N, HV) > 0 ? gdn::prefill_split_workspace_bytes(N, T, HQ, HV) : 0;
+}
+
+extern "C" size_t gdn_prefill_split_workspace_bytes(int N, int T, int HQ, int HV) {
+  if (N <= 0 || T < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return 0;
+  return gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
 }
 
 extern "C" int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -1209,16 +1024,40 @@ extern "C" int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const ui
                                   int cu_is_int32, int N, int T, int HQ, int HV, float scale,
                                   uint16_t* out, float* final_state, void* workspace,
                                   size_t workspace_bytes, int flags, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
                                     N, T, HQ, HV);
   if (rc != GDN_OK) return rc;
   if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
   if (N == 0) return GDN_OK;
+  // Few chains: split each over workgroups when the caller supplied the workspace for it.
+  const int slices = T > 0 ? gdn::prefill_split_auto_slices(N, HV) : 0;
+  if (slices > 0 && workspace != nullptr &&
+      workspace_bytes >= gdn::prefill_split_workspace_bytes(N, T, HQ, HV)) {
+    return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32,
+                                     N, T, HQ, HV, scale, out, final_state, slices, workspace, flags,
+                                     static_cast<hipStream_t>(stream));
+  }
   return prefill_dispatch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ,
                           HV, scale, out, final_state, nullptr, 0, flags,
                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gdn_prefill_split_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                     const float* state, const float* A_log, const uint16_t* a,
+                                     const float* dt_bias, const uint16_t* b, const void* cu_seqlens,
+                                     int cu_is_int32, int N, int T, int HQ, int HV, float scale,
+                                     uint16_t* out, float* final_state, int slices, void* workspace,
+                                     size_t workspace_bytes, int flags, void* stream) {
+  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
+                                    N, T, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if ((flags & ~GDN_FLAGS_ALL) || !gdn::prefill_split_slices_valid(slices)) return GDN_ERR_SHAPE;
+  if (N == 0) return GDN_OK;
+  const size_t need = gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return GDN_ERR_WORKSPACE;
+  return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
+                                   T, HQ, HV, scale, out, final_state, slices, workspace, flags,
+                                   static_cast<hipStream_t>(stream));
 }
 
 extern "C" long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, int N,

@@ -1,0 +1,31 @@
+// Host-side interface of the split prefill path (gdn_prefill_split.hip): a
+// parallel chunk-preparation launch followed by a launch of state slices,
+// for batches with fewer (sequence, v-head) chains than the GPU has CUs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn {
+
+// Workspace bytes of the split path for an upper bound of T / 64 + N chunks:
+// one 14 080-byte record per (chunk, v-head) and one 18 432-byte fp16 K image
+// per (chunk, qk-head).
+size_t prefill_split_workspace_bytes(int N, int T, int HQ, int HV);
+
+// Slices per chain the split path uses on the current device for N * HV
+// chains: 8 when chains * 8 fit the CUs, 4 when chains * 4 fit twice the
+// CUs, else 0 (the fused chain kernel runs).
+int prefill_split_auto_slices(int N, int HV);
+
+bool prefill_split_slices_valid(int slices);
+
+// Enqueues both launches on st; workspace holds prefill_split_workspace_bytes.
+int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
+                         const float* A_log, const uint16_t* a, const float* dt_bias,
+                         const uint16_t* b, const void* cu_seqlens, int cu_is_int32, int N, int T,
+                         int HQ, int HV, float scale, uint16_t* out, float* final_state,
+                         int slices, void* workspace, int flags, hipStream_t st);
+
+}  // namespace gdn

@@ -1,0 +1,861 @@
+// GDN chunked varlen prefill for batches with fewer (sequence, v-head) chains
+// than the GPU has CUs (gfx950 / CDNA4, wave64, MFMA).  Two launches:
+//
+//  1. gdn_prefill_prep_kernel: one workgroup per (chunk, v-head), every chunk
+//     of every sequence at once.  It forms what of a chunk does not depend on
+//     the state -- the gates, A = tril_strict(beta_i e^{gam_i-gam_j} K K^T),
+//     the diagonal 32-row blocks of Tm = (I + A)^-1, -A_ba (the lower-left
+//     32x32 block of A) and P = scale tril_incl(e^{gam_i-gam_j} Q K^T) -- and
+//     writes it to the workspace as ready MFMA operand fragments.  This is
+//     the work of the reference's chunk_scaled_dot_kkt_fwd and
+//     recompute_w_u_fwd (gdn_prefill_qk4_v8_d128_k_last/solution/triton/
+//     kernel.py:473-559, 617-796, gating :1706-1722) run over all chunks in
+//     parallel, as the reference launches them (grids over chunks, :544,
+//     :1005), but stopping before W and U.
+//  2. gdn_prefill_slice_kernel: one workgroup per (sequence, v-head, slice of
+//     R state rows).  The rows of the state evolve independently -- with
+//     X = beta (V - e^gam K S^T) and Vn = Tm X every product that touches S,
+//     X, Vn or O is row-separable in v -- so a chain splits over 128 / R
+//     workgroups that never exchange data (the reference splits its
+//     recurrence the same way, grid (V / BV, N H), kernel.py:1369).  Each
+//     workgroup walks the chunks of its sequence in order with its rows of
+//     S in MFMA accumulators: K S^T, X, Vn = Tm X (two-level, as in the
+//     fused kernel), O = scale e^gam Q S^T + P Vn, S <- e^{gam_L} S + K^T Vd.
+//
+// Arithmetic and operand precisions are those of the fused chain kernel
+// (gdn_prefill.hip): bf16 MFMA for A and P from the exact bf16 rows, fp16
+// operands on the state path, bf16 S for Q S^T, fp32 accumulation.
+
+#include "gdn_prefill_common.h"
+#include "gdn_prefill_split.h"
+#include "../../include/gdn_hip.h"
+
+namespace {
+
+using namespace gdn;
+
+// ---------------------------------------------------------------------------
+// Workspace record of one (chunk, v-head), 14 080 bytes.  An operand
+// fragment is 1 KB: lane l's 16 bytes at 16 l, exactly the register image a
+// 16x16x32 MFMA operand read gives lane l, so readers copy it whole and read
+// it back with one conflict-free 16-byte LDS read per lane.
+constexpr int kFrag = 1024;
+constexpr int BL_TM = 0;               // 4 fragments: T_a rows 0-15, 16-31; T_b rows 32-47, 48-63
+constexpr int BL_AB = 4 * kFrag;       // 2 fragments: -A_ba rows 32-47, 48-63
+constexpr int BL_P = 6 * kFrag;        // 6 fragments: P (token block, column block) 00 10 20 21 30 31
+constexpr int BL_G = 12 * kFrag;       // gate data, GSZ floats (layout of the G_* offsets)
+constexpr int BL_N = BL_G + 4 * GSZ;   // GDN_QK_L2NORM: row factors of K (64 floats), then of Q
+constexpr int kBlob = BL_N + 4 * 2 * C;
+static_assert(kBlob % 256 == 0, "records stay 256-byte aligned");
+constexpr int kBlobCopies = (kBlob + kFrag - 1) / kFrag;   // 1 KB copy instructions per record
+// fp16 K rows of one (chunk, qk-head) as the chain reads them in LDS: [t][p32(k)]
+// with KCLD-element rows (the padding is never read), rows past the chunk end 0.
+constexpr int kKcBytes = C * KCLD * 2;
+static_assert(kKcBytes % kFrag == 0, "whole 1 KB copies");
+constexpr int kKcCopies = kKcBytes / kFrag;
+// gate data and L2-norm factors of a record, staged in LDS by the state slices
+constexpr int kGateBytes = kBlob - BL_G;
+constexpr int kGateCopies = (kGateBytes + kFrag - 1) / kFrag;
+
+constexpr int kPrepThreads = 256;
+
+// HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): from
+// base + off (base uniform, off a 32-bit lane offset) to LDS byte address
+// lds + 16 l for lane l (lds uniform).  Issued from asm so that the compiler
+// places no waits for it; consumers wait with explicit vmcnt counts and a
+// barrier.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds), "v"(off), "s"(base) : "memory", "m0");
+}
+
+// Inclusive prefix sum of an int over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_scan_incl(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Sequence n and chunk i of chunk slot `slot` = chunk_offset(n) + i, where
+// chunk_offset(n) counts the 64-token chunks of sequences 0 .. n-1 (lengths
+// clamped as seq_bounds clamps them).  n = -1 past the last chunk.
+// Wave-uniform result.  The reference builds the same (sequence, chunk)
+// table on the host (prepare_chunk_indices, kernel.py:175-202).
+template <typename CuT>
+__device__ void locate_chunk(const CuT* cu, int N, int T, int slot, int lane, int& n, int& ci) {
+  int base = 0;
+  n = -1;
+  ci = 0;
+  for (int m0 = 0; m0 < N; m0 += 64) {
+    const int m = m0 + lane;
+    int cnt = 0;
+    if (m < N) {
+      int bm, lm;
+      seq_bounds(cu, m, T, bm, lm);
+      cnt = (lm + C - 1) / C;
+    }
+    const int incl = wave_scan_incl(cnt, lane);
+    const unsigned long long hit = __ballot(base + incl > slot);
+    if (hit) {
+      const int first = __ffsll((long long)hit) - 1;
+      n = m0 + first;
+      ci = slot - base - __shfl(incl - cnt, first);
+      return;
+    }
+    base += __shfl(incl, 63);
+  }
+}
+
+// chunk_offset(n) (wave-uniform): lanes take every 64th sequence, then a wave sum.
+template <typename CuT>
+__device__ int chunk_offset(const CuT* cu, int n, int T, int lane) {
+  int part = 0;
+  for (int m = lane; m < n; m += 64) {
+    int bm, lm;
+    seq_bounds(cu, m, T, bm, lm);
+    part += (lm + C - 1) / C;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+  return __builtin_amdgcn_readfirstlane(part);
+}
+
+// ---------------------------------------------------------------------------
+// Preparation of one chunk of one v-head.  Four waves:
+//   copies   raw K and Q rows (bf16) of the chunk into LDS, swizzled;
+//   wave 0   gates (softplus, sigmoid, chunk-local cumsum by a DPP scan);
+//   all      (option) L2-norm factors of the 128 rows; 20 A / P tiles;
+//   wave 0   the four diagonal 16x16 blocks of Tm by forward substitution;
+//   waves 2-3  the two 16-row merges inside the diagonal 32-row blocks;
+//   all      the operand fragments to the workspace, and (first v-head of
+//            each qk-head) the fp16 K rows in the chain's LDS layout.
+// Rows past the chunk end are copies of its last row with beta = 0 and a
+// zero log-decay, so their A rows vanish and their Tm rows are unit rows.
+template <typename CuT, bool kL2>
+__global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
+    const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV, float scale,
+    char* __restrict__ blob, int n_slots) {
+  __shared__ __align__(16) uint16_t rk[C * D];
+  __shared__ __align__(16) uint16_t rq[C * D];
+  __shared__ __align__(16) float sA[C * ALD];
+  __shared__ __align__(16) _Float16 sTm[C * TLD];
+  __shared__ __align__(16) _Float16 sP[C * TLD];
+  __shared__ __align__(16) _Float16 sAba[(C / 2) * BLD];
+  __shared__ __align__(16) float gd[GSZ];
+  __shared__ __align__(16) float nrm[2 * C];
+
+  const int slot = blockIdx.x, hv = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  int n, ci;
+  locate_chunk(cu_seqlens, N, T, slot, lane, n, ci);
+  if (n < 0) return;
+  int bos, len;
+  seq_bounds(cu_seqlens, n, T, bos, len);
+  const int t0 = bos + ci * C;
+  const int L = min(C, len - ci * C);
+  const int hq = hv / (HV / HQ);
+  const size_t qk_stride = size_t(HQ) * D;
+  char* rec = blob + (size_t(slot) * HV + hv) * kBlob;
+
+  // The upper 16x16 tiles inside the diagonal 32x32 blocks of Tm and P are
+  // part of the fragments and must be zero.
+  for (int e = tid; e < 2 * 16 * 16; e += kPrepThreads) {
+    const int blk = e >> 8, r = (e >> 4) & 15, cc = e & 15;
+    const int R0 = 32 * blk + r, pc = p32(32 * blk + 16 + cc);
+    sTm[R0 * TLD + pc] = (_Float16)0.f;
+    sP[R0 * TLD + pc] = (_Float16)0.f;
+  }
+  // Raw rows: 16 threads per row, one 16-byte piece each, into swizzled slots.
+#pragma unroll
+  for (int j = 0; j < (C * D / 8) / kPrepThreads; ++j) {
+    const int item = tid + kPrepThreads * j;
+    const int row = item >> 4, pc = item & 15;
+    const size_t src = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * pc;
+    const uint4 kv = *reinterpret_cast<const uint4*>(k + src);
+    const uint4 qv = *reinterpret_cast<const uint4*>(q + src);
+    *reinterpret_cast<uint4*>(&rk[raw_off(row, 8 * pc)]) = kv;
+    *reinterpret_cast<uint4*>(&rq[raw_off(row, 8 * pc)]) = qv;
+  }
+  // Gates of the chunk's tokens (reference PRE:1706-1722 and the chunk-local
+  // cumsum of PRE:1721): lane = token.
+  if (wave == 0) {
+    constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
+    const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
+    const float xa = bf16_bits_to_f32(a[gi]) + dt_bias[hv];
+    const float xb = bf16_bits_to_f32(b[gi]);
+    const float a_log_exp = expf(A_log[hv]);
+    float ld = 0.f, bt = 0.f;
+    if (lane < L) {
+      // softplus(x) = max(x, 0) + ln(1 + e^-|x|); sigmoid(y) = 1 / (1 + e^-y)
+      const float sp = fmaxf(xa, 0.f) + kLn2 * __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(xa) * kLog2e));
+      ld = -a_log_exp * sp;
+      bt = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-xb * kLog2e));
+    }
+    ld = wave_inclusive_scan(ld);
+    const float l2 = ld * kLog2e;
+    const float gl2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), L - 1));
+    const float eg = __builtin_amdgcn_exp2f(l2);
+    const float vals[5] = {l2, bt, eg, scale * eg, __builtin_amdgcn_exp2f(gl2 - l2)};
+#pragma unroll
+    for (int f = 0; f < 5; ++f) {
+      gd[f * C + lane] = vals[f];
+      reinterpret_cast<float*>(rec + BL_G)[f * C + lane] = vals[f];
+    }
+  }
+  __syncthreads();
+  if constexpr (kL2) {
+    // Row factors (sum x^2 + 1e-6)^(-1/2): two threads per row of K, then Q.
+    const int r = tid >> 1, hf = tid & 1;
+    const uint16_t* src = r < C ? rk : rq;
+    const int row = r & (C - 1);
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const uint4 w = *reinterpret_cast<const uint4*>(&src[raw_off(row, 64 * hf + 8 * p)]);
+      float f[8];
+      unpack_bf16x2(w.x, f[0], f[1]); unpack_bf16x2(w.y, f[2], f[3]);
+      unpack_bf16x2(w.z, f[4], f[5]); unpack_bf16x2(w.w, f[6], f[7]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    }
+    ss += __shfl_xor(ss, 1);
+    if (hf == 0) {
+      const float fac = l2norm_rsqrt(ss);
+      nrm[r] = fac;
+      reinterpret_cast<float*>(rec + BL_N)[r] = fac;
+    }
+    __syncthreads();
+  }
+  const float* nk = nrm;
+  const float* nq = nrm + C;
+  const bool neg_scale = scale < 0.f;
+  // The fp16 K rows of the chunk, once per qk-head (by its first v-head), in
+  // the chain's LDS layout: [t][p32(k)], rows past the chunk end 0, scaled by
+  // the row factor with the L2-norm option.
+  if (hv % (HV / HQ) == 0) {
+    char* kimg = blob + size_t(n_slots) * HV * kBlob + (size_t(slot) * HQ + hq) * kKcBytes;
+#pragma unroll
+    for (int j = 0; j < (C * D / 8) / kPrepThreads; ++j) {
+      const int item = tid + kPrepThreads * j;
+      const int row = item >> 4, cc = (item & 15) * 8;
+      uint4 w = *reinterpret_cast<const uint4*>(&rk[raw_off(row, cc)]);
+      if (row >= L) w = uint4{0u, 0u, 0u, 0u};
+      float f[8];
+      unpack_bf16x2(w.x, f[0], f[1]); unpack_bf16x2(w.y, f[2], f[3]);
+      unpack_bf16x2(w.z, f[4], f[5]); unpack_bf16x2(w.w, f[6], f[7]);
+      if constexpr (kL2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] *= nk[row];
+      }
+      _Float16* d = reinterpret_cast<_Float16*>(kimg) + row * KCLD + p32(cc);
+      *reinterpret_cast<f16x4_t*>(d) = f16x4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+      *reinterpret_cast<f16x4_t*>(d + 8) = f16x4_t{(_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
+    }
+  }
+  const float scale_l2 = __log2f(fabsf(scale));
+
+  // Per-lane swizzled offsets of the 8-column pieces read from a raw row r
+  // with r % 16 == c: piece 4 ks + g sits in slot (4 ks + g) ^ c.
+  int raw_lane[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) raw_lane[ks] = c * D + 8 * ((4 * ks + g) ^ c);
+
+  // A tile = tril_strict(beta_i e^{gam_i - gam_j} K K^T), formed transposed
+  // (K_j K_i^T) so that lane (g, c) holds row 16 ti + c, columns 16 tj + 4 g
+  // .. +3.  Tiles of the diagonal 32-row blocks stay fp32 (the inverse's
+  // input); the lower-left block is stored negated in fp16 (a chain operand).
+  auto tile_A = [&](auto tile_c) {
+    constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
+    constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
+    bf16x8_t fa[4], fb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = ld16_bf(&rk[raw_lane[ks] + 16 * ti * D]);
+      fb[ks] = ld16_bf(&rk[raw_lane[ks] + 16 * tj * D]);
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
+    const float gr = gd[G_L2 + 16 * ti + c];
+    float br = gd[G_BETA + 16 * ti + c];
+    const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
+    if constexpr (kL2) {
+      br *= nk[16 * ti + c];
+      acc *= *reinterpret_cast<const f32x4*>(&nk[16 * tj + 4 * g]);
+    }
+    f32x4 val;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      val[i] = br * __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
+      if (ti == tj) val[i] = (c > 4 * g + i) ? val[i] : 0.f;
+    }
+    if (ti >= 2 && tj <= 1) {
+      *reinterpret_cast<f16x4_t*>(&sAba[(16 * (ti - 2) + c) * BLD + 8 * g + 4 * tj]) =
+          f16x4_t{(_Float16)-val[0], (_Float16)-val[1], (_Float16)-val[2], (_Float16)-val[3]};
+    } else {
+      *reinterpret_cast<f32x4*>(&sA[(16 * ti + c) * ALD + 16 * tj + 4 * g]) = val;
+    }
+  };
+  // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T), formed transposed like
+  // the A tiles; |scale| enters the exponent, its sign the product.
+  auto tile_P = [&](auto tile_c) {
+    constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
+    constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
+    bf16x8_t fa[4], fb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = ld16_bf(&rq[raw_lane[ks] + 16 * ti * D]);
+      fb[ks] = ld16_bf(&rk[raw_lane[ks] + 16 * tj * D]);
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
+    if (neg_scale) acc = -acc;
+    const float gr = gd[G_L2 + 16 * ti + c] + scale_l2;
+    const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
+    if constexpr (kL2) acc *= nq[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk[16 * tj + 4 * g]);
+    f16x4_t val;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
+      if (ti == tj) x = (c >= 4 * g + i) ? x : 0.f;
+      val[i] = (_Float16)x;
+    }
+    *reinterpret_cast<f16x4_t*>(&sP[(16 * ti + c) * TLD + 32 * (tj >> 1) + 8 * g + 4 * (tj & 1)]) = val;
+  };
+  switch (wave) {
+    case 0: tile_A(IC<0>{}); tile_A(IC<4>{}); tile_A(IC<8>{}); tile_P(IC<0>{}); tile_P(IC<4>{}); break;
+    case 1: tile_A(IC<1>{}); tile_A(IC<5>{}); tile_A(IC<9>{}); tile_P(IC<1>{}); tile_P(IC<5>{}); break;
+    case 2: tile_A(IC<2>{}); tile_A(IC<6>{}); tile_P(IC<2>{}); tile_P(IC<6>{}); tile_P(IC<8>{}); break;
+    default: tile_A(IC<3>{}); tile_A(IC<7>{}); tile_P(IC<3>{}); tile_P(IC<7>{}); tile_P(IC<9>{}); break;
+  }
+  __syncthreads();
+
+  auto put_frag = [&](int off, f16x8 x) {
+    *reinterpret_cast<f16x8*>(rec + off + 16 * lane) = x;
+  };
+  if (wave == 0) {
+    // Rows of the diagonal 16x16 blocks of Tm: lane group g inverts block g
+    // by forward substitution in fp32 (lane = column), Tm[i] = e_i - sum_{j<i}
+    // A[i][j] Tm[j] (the reference's diagonal-block solve, PRE:661-699).
+    const float* Ab = &sA[(16 * g) * ALD + 16 * g];
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s0 = (i == c) ? 1.f : 0.f, s1 = 0.f;   // two partial sums halve the dependent chain
+#pragma unroll
+      for (int j4 = 0; j4 < i; j4 += 4) {
+        const f32x4 arow = *reinterpret_cast<const f32x4*>(&Ab[i * ALD + j4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (j4 + e < i) {
+            if ((j4 >> 2) & 1) s1 = fmaf(-arow[e], x[j4 + e], s1);
+            else s0 = fmaf(-arow[e], x[j4 + e], s0);
+          }
+        }
+      }
+      x[i] = s0 + s1;
+    }
+    const int pc = p32(16 * g + c);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sTm[(16 * g + i) * TLD + pc] = (_Float16)x[i];
+  } else {
+    // P and -A_ba fragments, as the chain reads them: lane (g, c) gets row
+    // 16 tb + c, p32 positions 32 p + 8 g .. + 7.
+    constexpr int kPt[6] = {0, 1, 2, 2, 3, 3}, kPp[6] = {0, 0, 0, 1, 0, 1};
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      if (f % 3 != wave - 1) continue;
+      if (f < 6) put_frag(BL_P + f * kFrag, ld16(&sP[(16 * kPt[f] + c) * TLD + 8 * g + 32 * kPp[f]]));
+      else put_frag(BL_AB + (f - 6) * kFrag, ld16(&sAba[(16 * (f - 6) + c) * BLD + 8 * g]));
+    }
+  }
+  __syncthreads();
+  if (wave >= 2) {
+    // 16-row merge inside the 32-row block at a0: T_{a0+16.., a0..} = -T_22 A_21 T_11.
+    const int a0 = 32 * (wave - 2);
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sA[(a0 + 16 + c) * ALD + a0 + 4 * g]);
+    const f16x4_t fa = {(_Float16)a4[0], (_Float16)a4[1], (_Float16)a4[2], (_Float16)a4[3]};
+    f16x4_t fb;
+    const int pcb = p32(a0 + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) fb[e] = sTm[(a0 + 4 * g + e) * TLD + pcb];
+    const f32x4 y = mfma16k16(fa, fb, f32x4{0.f, 0.f, 0.f, 0.f});
+    const f16x4_t ft = *reinterpret_cast<const f16x4_t*>(&sTm[(a0 + 16 + c) * TLD + p32(a0 + 16 + 4 * g)]);
+    const f16x4_t fy = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+    const f32x4 t21 = mfma16k16(ft, fy, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sTm[(a0 + 16 + 4 * g + i) * TLD + pcb] = (_Float16)(-t21[i]);
+  }
+  __syncthreads();
+  // Tm fragments: T_a rows 0-15 / 16-31 (p32 group 0), T_b rows 32-47 / 48-63 (group 1).
+  {
+    const int j = wave;
+    const int off = j < 2 ? (16 * j + c) * TLD + 8 * g : (16 * j + c) * TLD + 32 + 8 * g;
+    put_frag(BL_TM + j * kFrag, ld16(&sTm[off]));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// State slice of one chain: R = 16 NRG state rows per workgroup.  Each group
+// of 16 rows is carried by two waves that both hold those rows of S:
+//   state wave  : KS = K S^T;  X = beta (V - e^gam KS);  Vn_top = T_a X_top,
+//                 Vn_bot = T_b (X_bot - A_ba Vn_top);  Vd = e^{gam_L - gam} Vn
+//                 -> Vn and Vd to LDS
+//   output wave : O^T = scale e^gam S Q^T, then (Vn from LDS) + Vn^T P^T,
+//                 stored as bf16 rows
+//   both        : S <- e^{gam_L} S + K^T Vd (the same operations in the same
+//                 order, so the two copies of S stay equal bit for bit)
+// and one copy wave stages, by HBM -> LDS copies issued two chunks ahead into
+// three buffers each, the raw Q rows, the slice's V columns, the chunk's fp16
+// K image and its gate data.  The Tm, A_ba and P fragments of the chunk's
+// workspace record go straight into the registers of the waves that use
+// them, also two chunks ahead.  Two LDS barriers per chunk: after Vn is in
+// LDS, and at the end of the chunk.  State waves 0 .. NRG-1 and output waves
+// NRG .. 2 NRG - 1 land on different SIMDs pairwise.
+template <int NRG>
+struct SliceCfg {
+  static constexpr int R = 16 * NRG;            // state rows per workgroup
+  static constexpr int kThreads = 64 * (2 * NRG + 1);
+  static constexpr int VS = R / 8;              // 16-byte slots per V row
+  static constexpr int VRows = 1024 / (2 * R);  // V rows per 1 KB copy instruction
+  static constexpr int kCopies = 16 + VS + kKcCopies + kGateCopies;   // copy instructions per chunk
+  // LDS buffer sets (copies are issued kNB - 1 chunks ahead)
+  static constexpr int kNB = NRG == 1 ? 4 : 3;
+  // chunks ahead that the record fragments are loaded (24 VGPRs a chunk)
+  static constexpr int kAhead = kNB - 1;
+};
+
+template <typename CuT, bool kL2, int NRG>
+__global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ v, const float* __restrict__ h0,
+    const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV,
+    uint16_t* __restrict__ out, float* __restrict__ ht, const char* __restrict__ ws, int nt_bound) {
+  using Cfg = SliceCfg<NRG>;
+  constexpr int R = Cfg::R;
+  constexpr int VS = Cfg::VS;
+  constexpr int S = D / R;                      // slices per chain
+  constexpr int NB = Cfg::kNB;
+  __shared__ __align__(16) _Float16 Kc[NB][C * KCLD];
+  __shared__ __align__(16) uint16_t rq[NB][C * D];
+  __shared__ __align__(16) uint16_t rv[NB][C * R];
+  __shared__ __align__(16) char gt[NB][kGateBytes];
+  __shared__ __align__(16) f16x8 xch[NRG][4][64];   // Vn (2 fragments) and Vd (2) per row group
+
+  // Workgroup -> (unit = (sequence, qk-head), member m, slice s).  The G * S
+  // workgroups of one unit read the same K, Q and (per member) records; they
+  // get ids 8 apart, which puts them on one XCD (ids go round-robin over the
+  // 8 XCDs), so only the first read of each line goes to HBM.
+  const int G = HV / HQ;
+  const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
+  const int unit = 8 * (id_row / (G * S)) + xcd;
+  if (unit >= N * HQ) return;
+  const int within = id_row - (id_row / (G * S)) * (G * S);
+  const int m = within / S, s = within - m * S;
+  const int n = unit / HQ;
+  const int hq = unit - n * HQ;
+  const int hv = hq * G + m;
+  const int vb = R * s;                         // first state row of the slice
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4, c = lane & 15;
+  int bos, len;
+  seq_bounds(cu_seqlens, n, T, bos, len);
+  const int n_chunks = (len + C - 1) / C;
+  const size_t qk_stride = size_t(HQ) * D;
+  const size_t v_stride = size_t(HV) * D;
+  auto chunk_len = [&](int ch) { return min(C, len - ch * C); };
+  const int coff = chunk_offset(cu_seqlens, n, T, lane);
+  // workspace record of chunk ch of this chain
+  auto record = [&](int ch) { return ws + (size_t(coff + ch) * HV + hv) * kBlob; };
+
+  if (wave < 2 * NRG) {
+    // ======================= state / output waves
+    const bool out_role = wave >= NRG;
+    const int r = out_role ? wave - NRG : wave;     // row group
+    const int v0 = vb + 16 * r;                 // rows v0 + c
+    const int vl = 16 * r;                      // the same, relative to the slice
+    // Sacc[kb][i] = S[v0 + c][16 kb + 4 g + i]: the S^T accumulator tiles.
+    f32x4 Sacc[8];
+    const float* h0row = h0 == nullptr ? nullptr
+                                       : h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+      Sacc[kb] = h0row ? *reinterpret_cast<const f32x4*>(h0row + 16 * kb + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    // Fragments of the chunk's record this wave multiplies with (state: T_a,
+    // T_b, -A_ba; output: P), loaded kAhead chunks ahead.
+    constexpr int kAhead = Cfg::kAhead;
+    const int frag_base = out_role ? BL_P : BL_TM;
+    f16x8 fr[NB][6];
+    auto load_frags = [&](int ch, f16x8 (&dst)[6]) {
+      const char* rec = record(ch) + frag_base + 16 * lane;
+#pragma unroll
+      for (int f = 0; f < 6; ++f) dst[f] = *reinterpret_cast<const f16x8*>(rec + f * kFrag);
+    };
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a)
+      if (a < n_chunks) load_frags(a, fr[a]);
+    // Per-lane element offsets of the two 4-column pieces of a Q fragment
+    // (raw row 16 tb + c, columns 32 p + 4 g .. and 32 p + 16 + 4 g ..).
+    const int sw = (g >> 1) ^ c;
+    const int q_lane = c * D + 4 * (g & 1);
+
+    // State update with the chunk's K^T fragments (transposing reads, a
+    // k-block ahead) and Vd (both waves of a row group, identical operations).
+    auto update = [&](const _Float16* kc, float egL, const f16x8 (&vd)[2]) {
+      auto load_kt = [&](int kb, f16x8 (&dst)[2]) {
+        const int kq = p32(16 * kb + 4 * (c & 3));
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int tr0 = 32 * p + 4 * g + (c >> 2);
+          const f16x4_t lo = ld_tr16(&kc[tr0 * KCLD + kq]);
+          const f16x4_t hi = ld_tr16(&kc[(tr0 + 16) * KCLD + kq]);
+          dst[p] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      };
+      f16x8 fa[2][2];
+      load_kt(0, fa[0]);
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        if (kb + 1 < 8) load_kt(kb + 1, fa[(kb + 1) & 1]);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) asm volatile("" : "+v"(fa[kb & 1][p]));
+        Sacc[kb] *= egL;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) Sacc[kb] = mfma16(fa[kb & 1][p], vd[p], Sacc[kb]);
+      }
+    };
+
+    // One chunk; b3c (0, 1, 2) is the buffer set as a compile-time constant,
+    // so every LDS address is a loop-invariant lane offset plus an immediate.
+    auto chunk = [&](auto b3c, int ch) {
+      constexpr int b3 = decltype(b3c)::value;
+      const int L = chunk_len(ch);
+      const float* gd = reinterpret_cast<const float*>(gt[b3]);
+      const _Float16* kc = Kc[b3];
+      const float egL = gd[G_EG + L - 1];
+      if (ch + kAhead < n_chunks) load_frags(ch + kAhead, fr[(b3 + kAhead) % NB]);
+      if (!out_role) {
+        // ---- K S^T (the state before this chunk), K fragments a column block ahead
+        f32x4 KS[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f16x8 kf[2][4];                         // K rows 16 tb + c, p32 positions 32 p + 8 g ..
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) kf[0][tb] = ld16(&kc[(16 * tb + c) * KCLD + 8 * g]);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          if (p + 1 < 4) {
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) kf[(p + 1) & 1][tb] = ld16(&kc[(16 * tb + c) * KCLD + 32 * (p + 1) + 8 * g]);
+          }
+          const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            asm volatile("" : "+v"(kf[p & 1][tb]));
+            KS[tb] = mfma16(kf[p & 1][tb], sb, KS[tb]);
+          }
+        }
+        // ---- X = beta (V - e^gam K S^T).  V[16 tb + 4 g + i][v0 + c] by one
+        //      transposing read per tb: lane 4 mm + j reads columns vl + 4 j
+        //      .. +3 of row 16 tb + 4 g + mm.
+        {
+          const int mm = c >> 2, j = c & 3;
+          const int col = vl + 4 * j;
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const int t = 16 * tb + 4 * g + mm;
+            const i16x4_t vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4_t*)&rv[b3][t * R + 8 * ((col >> 3) ^ (t & (VS - 1))) + (col & 7)]);
+            const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + 16 * tb + 4 * g]);
+            const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * tb + 4 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              KS[tb][i] = bt[i] * (bf16_bits_to_f32(uint16_t(vv[i])) - eg[i] * KS[tb][i]);
+          }
+        }
+        // ---- Vn = Tm X in 32-row blocks: Vn_top = T_a X_top, Vn_bot = T_b (X_bot - A_ba Vn_top)
+        f16x8 vd[2];
+        {
+          const f16x8* tf = fr[b3];             // T_a rows 0-15, 16-31; T_b rows 32-47, 48-63; -A_ba
+          f32x4 ed[4];
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) ed[tb] = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb + 4 * g]);
+          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          f32x4 Vn[4];
+          f16x8 xb = pack2(KS[0], KS[1]);
+          Vn[0] = mfma16(tf[0], xb, z);
+          Vn[1] = mfma16(tf[1], xb, z);
+          const f16x8 vn0 = pack2(Vn[0], Vn[1]);
+          KS[2] = mfma16(tf[4], vn0, KS[2]);
+          KS[3] = mfma16(tf[5], vn0, KS[3]);
+          vd[0] = pack2(Vn[0] * ed[0], Vn[1] * ed[1]);
+          xb = pack2(KS[2], KS[3]);
+          Vn[2] = mfma16(tf[2], xb, z);
+          Vn[3] = mfma16(tf[3], xb, z);
+          const f16x8 vn1 = pack2(Vn[2], Vn[3]);
+          vd[1] = pack2(Vn[2] * ed[2], Vn[3] * ed[3]);
+          xch[r][0][lane] = vn0;
+          xch[r][1][lane] = vn1;
+          xch[r][2][lane] = vd[0];
+          xch[r][3][lane] = vd[1];
+        }
+        lds_barrier();                          // Vn, Vd of every row group in LDS
+        update(kc, egL, vd);
+      } else {
+        // ---- O^T = S Q^T (transposed output tile: lane (g, c) of OT[tb] holds
+        //      token 16 tb + c, state rows v0 + 4 g .. +3)
+        f32x4 OT[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) OT[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto load_q = [&](int p, bf16x8_t (&dst)[4]) {
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const uint16_t* qr = &rq[b3][q_lane + 16 * tb * D];
+            const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&qr[8 * ((4 * p) ^ sw)]);
+            const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&qr[8 * ((4 * p + 2) ^ sw)]);
+            dst[tb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          }
+        };
+        bf16x8_t qf[2][4];
+        load_q(0, qf[0]);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          if (p + 1 < 4) load_q(p + 1, qf[(p + 1) & 1]);
+          const bf16x8_t sbf = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            asm volatile("" : "+v"(qf[p & 1][tb]));
+            OT[tb] = mfma16_bf(sbf, qf[p & 1][tb], OT[tb]);
+          }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          float egs = gd[G_EGS + 16 * tb + c];
+          if constexpr (kL2) egs *= gd[(BL_N - BL_G) / 4 + C + 16 * tb + c];
+          OT[tb] *= egs;
+        }
+        lds_barrier();                          // Vn, Vd of every row group in LDS
+        f16x8 vn[2], vd[2];
+        vn[0] = xch[r][0][lane];
+        vn[1] = xch[r][1][lane];
+        vd[0] = xch[r][2][lane];
+        vd[1] = xch[r][3][lane];
+        // ---- + Vn^T P^T, then the rows to HBM
+        {
+          const f16x8* pf = fr[b3];             // P (token block, column block) 00 10 20 21 30 31
+          constexpr int kPt[6] = {0, 1, 2, 2, 3, 3}, kPp[6] = {0, 0, 0, 1, 0, 1};
+#pragma unroll
+          for (int f = 0; f < 6; ++f) OT[kPt[f]] = mfma16(vn[kPp[f]], pf[f], OT[kPt[f]]);
+          uint16_t* obase = out + size_t(bos + ch * C) * v_stride + size_t(hv) * D + v0 + 4 * g;
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const int t = 16 * tb + c;
+            if (t < L)
+              *reinterpret_cast<uint2*>(obase + size_t(t) * v_stride) =
+                  uint2{cvt_pk_bf16(OT[tb][0], OT[tb][1]), cvt_pk_bf16(OT[tb][2], OT[tb][3])};
+          }
+        }
+        update(kc, egL, vd);
+      }
+      lds_barrier();                            // chunk ch+1 staged; buffers of ch free
+    };
+    if (n_chunks > 0) lds_barrier();            // chunk 0 staged
+    for (int ch = 0; ch < n_chunks; ch += NB) {
+      chunk(IC<0>{}, ch);
+      if (ch + 1 < n_chunks) chunk(IC<1>{}, ch + 1);
+      if (ch + 2 < n_chunks) chunk(IC<2>{}, ch + 2);
+      if (NB > 3 && ch + 3 < n_chunks) chunk(IC<(NB > 3 ? 3 : 0)>{}, ch + 3);
+    }
+    if (!out_role) {
+      float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
+    }
+  } else {
+    // ======================= copy wave
+    // Per-lane byte offsets from a full chunk's first row: raw Q rows (4 rows
+    // per instruction, lane l -> row 4 j + l / 16, slot l % 16 holding piece
+    // (l % 16) ^ row) and V columns (lane l -> row VRows j + l / VS, slot
+    // l % VS holding piece (l % VS) ^ (row % VS)).
+    uint32_t q_off[16], v_off[VS];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = 4 * j + (lane >> 4);
+      q_off[j] = uint32_t(row) * uint32_t(qk_stride * 2) + uint32_t((lane & 15) ^ (row & 15)) * 16u;
+    }
+#pragma unroll
+    for (int j = 0; j < VS; ++j) {
+      const int row = Cfg::VRows * j + lane / VS;
+      v_off[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane % VS) ^ (row & (VS - 1))) * 16u;
+    }
+    const char* kc0 = ws + size_t(nt_bound) * HV * kBlob + (size_t(coff) * HQ + hq) * kKcBytes;
+    const uint32_t lane16 = 16u * uint32_t(lane);
+    // LDS byte address of a buffer, as a wave-uniform scalar.
+    auto lds_u32 = [](const void* p) {
+      return __builtin_amdgcn_readfirstlane(
+          (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+    };
+    auto issue_copies = [&](int ch) {
+      const int t0 = bos + ch * C, L = chunk_len(ch);
+      const int b3 = ch % NB;
+      const uint32_t lq = lds_u32(rq[b3]), lv = lds_u32(rv[b3]);
+      if (L == C) {
+        const char* qb = reinterpret_cast<const char*>(q + size_t(t0) * qk_stride + size_t(hq) * D);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dma16(qb, q_off[j], lq + uint32_t(kFrag * j));
+        const char* vbp = reinterpret_cast<const char*>(v + size_t(t0) * v_stride + size_t(hv) * D + vb);
+#pragma unroll
+        for (int j = 0; j < VS; ++j) dma16(vbp, v_off[j], lv + uint32_t(kFrag * j));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int row = 4 * j + (lane >> 4);
+          const int src_piece = (lane & 15) ^ (row & 15);
+          lds_dma16(q + size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_piece,
+                    &rq[b3][4 * j * D]);
+        }
+#pragma unroll
+        for (int j = 0; j < VS; ++j) {
+          const int row = Cfg::VRows * j + lane / VS;
+          const int src_piece = (lane % VS) ^ (row & (VS - 1));
+          lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + vb + 8 * src_piece,
+                    &rv[b3][Cfg::VRows * j * R]);
+        }
+      }
+      const char* kcs = kc0 + size_t(ch) * HQ * kKcBytes;
+      const uint32_t lk = lds_u32(Kc[b3]);
+#pragma unroll
+      for (int j = 0; j < kKcCopies; ++j) dma16(kcs + kFrag * j, lane16, lk + uint32_t(kFrag * j));
+      const char* gsrc = record(ch) + BL_G;
+      const uint32_t lg = lds_u32(gt[b3]);
+#pragma unroll
+      for (int j = 0; j < kGateCopies; ++j)
+        if (j < kGateCopies - 1 || kFrag * j + 16 * lane < kGateBytes)
+          dma16(gsrc + kFrag * j, lane16, lg + uint32_t(kFrag * j));
+    };
+    // copies(ch) land before the barrier that ends chunk ch - 1: at most
+    // (NB - 2) later chunks' copies are still in flight then.
+    constexpr int kWait1 = Cfg::kCopies < 63 ? Cfg::kCopies : 63;
+    constexpr int kWait2 = 2 * Cfg::kCopies < 63 ? 2 * Cfg::kCopies : 63;
+    auto wait_ahead = [&](int later) {          // wait until `later` chunks' copies remain
+      if (later >= 2 && NB > 3) wait_vm<kWait2>();
+      else if (later >= 1) wait_vm<kWait1>();
+      else wait_vm<0>();
+    };
+    if (n_chunks > 0) {
+#pragma unroll
+      for (int a = 0; a < NB - 1; ++a)
+        if (a < n_chunks) issue_copies(a);
+      wait_ahead(min(n_chunks, NB - 1) - 1);    // copies(0) landed
+      lds_barrier();
+    }
+    for (int ch = 0; ch < n_chunks; ++ch) {
+      // the chain reads chunk ch; copies(ch+1 .. ch+NB-2) are in flight,
+      // copies(ch+NB-1) go into the buffers chunk ch-1 used
+      if (ch + NB - 1 < n_chunks) issue_copies(ch + NB - 1);
+      lds_barrier();                            // Vn exchange of chunk ch
+      wait_ahead(min(n_chunks - 1, ch + NB - 1) - (ch + 1));   // copies(ch+1) landed
+      lds_barrier();
+    }
+  }
+}
+
+template <typename CuT, bool kL2>
+int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
+                   const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                   const CuT* cu, int N, int T, int HQ, int HV, float scale, uint16_t* out,
+                   float* final_state, int slices, char* ws, hipStream_t st) {
+  const int nt_bound = T / C + N;
+  if (nt_bound > 0) {
+    hipLaunchKernelGGL((gdn_prefill_prep_kernel<CuT, kL2>), dim3(nt_bound, HV), dim3(kPrepThreads), 0,
+                       st, q, k, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale, ws, nt_bound);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return -int(e);
+  }
+  const unsigned units = unsigned(N) * unsigned(HQ);
+  const unsigned G = unsigned(HV / HQ);
+  const dim3 grid{8u * G * unsigned(slices) * ((units + 7u) / 8u), 1u, 1u};
+  switch (slices) {
+    case 8:
+      hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, 1>), grid, dim3(SliceCfg<1>::kThreads), 0,
+                         st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, 2>), grid, dim3(SliceCfg<2>::kThreads), 0,
+                         st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound);
+      break;
+    default:
+      return GDN_ERR_SHAPE;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GDN_OK : -int(e);
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
+}  // namespace
+
+namespace gdn {
+
+size_t prefill_split_workspace_bytes(int N, int T, int HQ, int HV) {
+  if (N <= 0 || T < 0 || HQ <= 0 || HV <= 0) return 0;
+  return size_t(T / C + N) * (size_t(HV) * size_t(kBlob) + size_t(HQ) * size_t(kKcBytes));
+}
+
+int prefill_split_auto_slices(int N, int HV) {
+  const long long chains = (long long)N * HV;
+  const int cus = device_cu_count();
+  if (chains <= 0 || cus <= 0) return 0;
+  // 8 slices while they fit the CUs at once; 4 slices for up to two
+  // workgroups per CU (measured faster than one fused workgroup per chain at
+  // 128 chains on 256 CUs); past that the fused kernel.
+  if (chains * 8 <= cus) return 8;
+  if (chains * 4 <= 2LL * cus) return 4;
+  return 0;
+}
+
+bool prefill_split_slices_valid(int slices) { return slices == 4 || slices == 8; }
+
+int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
+                         const float* A_log, const uint16_t* a, const float* dt_bias,
+                         const uint16_t* b, const void* cu_seqlens, int cu_is_int32, int N, int T,
+                         int HQ, int HV, float scale, uint16_t* out, float* final_state,
+                         int slices, void* workspace, int flags, hipStream_t st) {
+  char* ws = static_cast<char*>(workspace);
+  const bool l2 = (flags & GDN_QK_L2NORM) != 0;
+  if (cu_is_int32) {
+    const int32_t* cu = static_cast<const int32_t*>(cu_seqlens);
+    return l2 ? launch_split_t<int32_t, true>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
+                                              out, final_state, slices, ws, st)
+              : launch_split_t<int32_t, false>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
+                                               out, final_state, slices, ws, st);
+  }
+  const int64_t* cu = static_cast<const int64_t*>(cu_seqlens);
+  return l2 ? launch_split_t<int64_t, true>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
+                                            out, final_state, slices, ws, st)
+            : launch_split_t<int64_t, false>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
+                                             out, final_state, slices, ws, st);
+}
+
+}  // namespace gdn

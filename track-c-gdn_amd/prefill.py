@@ -78,7 +78,14 @@ def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
 
 
 def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
+    """Workspace the automatic path selection uses for this problem on the
+    current device (0 when the fused chain kernel runs)."""
     return int(_capi.lib().gdn_prefill_workspace_bytes(N, T, HQ, HV))
+
+
+def split_workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
+    """Workspace of the split path (chunk preparation + state slices)."""
+    return int(_capi.lib().gdn_prefill_split_workspace_bytes(N, T, HQ, HV))
 
 
 def num_chunks(cu_seqlens: torch.Tensor, T: int) -> int:
@@ -96,7 +103,7 @@ def num_chunks(cu_seqlens: torch.Tensor, T: int) -> int:
 @torch.no_grad()
 def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
                 output=None, final_state=None, workspace=None, validate: bool = True,
-                qk_l2norm: bool = False, h=None):
+                qk_l2norm: bool = False, h=None, path: str = "auto", slices: int = 8):
     """Chunked GDN prefill over packed varlen sequences, any ``HV % HQ == 0``.
 
     ``q, k [T, HQ, 128]``, ``v [T, HV, 128]``, ``a, b [T, HV]`` bf16;
@@ -109,6 +116,13 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     normalised inputs).  ``h``, a ``[NT, HV, 128, 128]`` bf16 buffer
     (``NT = num_chunks(cu_seqlens, T)``), also receives the state entering
     every chunk; the output and final state are the same bit for bit.
+
+    ``path`` selects the kernels: ``"auto"`` (the library's choice: the split
+    path -- a parallel chunk-preparation launch and ``HV * N * slices`` state
+    slices -- when the chains alone leave CUs idle, else the fused chain
+    kernel), ``"fused"`` (one workgroup per chain) or ``"split"`` with
+    ``slices`` in (2, 4, 8) state slices per chain.  Results of the two paths
+    are the same bit for bit without ``qk_l2norm``.
     """
     T, nq, d = q.shape
     nv = v.shape[1]
@@ -132,11 +146,28 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     assert output.shape == (T, nv, HEAD_SIZE)
     assert final_state.dtype == torch.float32 and final_state.is_contiguous()
     assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
-    ws_need = workspace_bytes(N, T, nq, nv)
+    assert path in ("auto", "fused", "split"), path
+    if path == "split":
+        assert h is None, "the per-chunk states are written by the fused kernel only"
+        ws_need = split_workspace_bytes(N, T, nq, nv)
+    elif path == "auto" and h is None:
+        ws_need = workspace_bytes(N, T, nq, nv)
+    else:
+        ws_need = 0
+        workspace = None
     if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
         workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     flags = _capi.GDN_QK_L2NORM if qk_l2norm else 0
+    if path == "split":
+        rc = _capi.lib().gdn_prefill_split_fwd(
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
+            _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
+            1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
+            _capi.ptr(output), _capi.ptr(final_state), int(slices), _capi.ptr(workspace),
+            ws_bytes, flags, _capi.stream_handle(q.device))
+        _capi.check(rc, "gdn_prefill_split_fwd")
+        return output, final_state
     if h is not None:
         assert h.dtype == torch.bfloat16 and h.is_contiguous() and h.device == q.device
         assert h.dim() == 4 and h.shape[1:] == (nv, HEAD_SIZE, HEAD_SIZE)
