@@ -93,3 +93,41 @@ def test_decode_multi_none_state_inplace(device):
     _, s_ref2 = _oracle_steps(x2)
     rel = float((st.cpu().double() - s_ref2).norm() / s_ref2.norm())
     assert rel <= 1e-3, rel
+
+
+@pytest.mark.parametrize("T,l2", [(17, False), (17, True), (40, False), (40, True)])
+def test_decode_multi_past_one_staging_block(device, T, l2):
+    """T beyond the 16 tokens the kernel stages in LDS at a time: the second
+    and third blocks reuse the staging buffers after a barrier and read tokens
+    t0 + t.  Checked against the oracle stepped per token and, bit for bit,
+    against T successive single-step launches (with and without q/k L2-norm)."""
+    dec = pkg_module("decode")
+    inp = pkg_module("inputs")
+    B = 5
+    print(f"decode multi long T={T} l2={l2}", flush=True)
+    x = inp.decode_multi_inputs(B, T, HQ=4, HV=8, seed=2300 + T)
+    if l2:
+        gen = torch.Generator().manual_seed(2400 + T)
+        x["q"] = (torch.randn(x["q"].shape, generator=gen) * 2.0).to(torch.bfloat16)
+        x["k"] = (torch.randn(x["k"].shape, generator=gen) * 0.7).to(torch.bfloat16)
+    g = _to(x, device)
+    o_m, s_m = dec.gdn_decode_multi(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
+                                    g["dt_bias"], g["b"], g["scale"], qk_l2norm=l2)
+    st = g["state"].clone()
+    outs = []
+    for t in range(T):
+        sl = slice(t, t + 1)
+        o, st = dec.gdn_decode(g["q"][:, sl], g["k"][:, sl], g["v"][:, sl], st, g["A_log"],
+                               g["a"][:, sl], g["dt_bias"], g["b"][:, sl], g["scale"],
+                               qk_l2norm=l2)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(o_m, torch.cat(outs, dim=1))
+    assert torch.equal(s_m, st)
+    xr = dict(x)
+    if l2:
+        xr["q"], xr["k"] = O.qk_l2norm(x["q"]), O.qk_l2norm(x["k"])
+    o_ref, s_ref = _oracle_steps(xr)
+    torch.testing.assert_close(o_m.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    rel = float((s_m.cpu().double() - s_ref).norm() / s_ref.norm())
+    assert rel <= 1e-3, rel

@@ -109,14 +109,22 @@ def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
 def run(q, k, v, state, A_log, a, dt_bias, b, scale):
     """Reference-compatible decode entry (DEC:100-146), qk4 / v8 / d128.
 
-    Returns ``(output [B, 1, 8, 128] bf16, new_state [B, 8, 128, 128] fp32)``;
-    the input state is not modified.
+    Returns ``(output [B, 1, 8, 128], new_state [B, 8, 128, 128] fp32)``;
+    the input state is not modified.  As at DEC:122 the output has q's dtype.
+    The reference kernel loads q, k, v, a and b of any float dtype; here
+    fp16 / fp32 inputs are rounded to bf16 (the operator definition's dtype)
+    before the kernel reads them.
     """
     assert q.shape[1:] == (1, HQ, D)    # DEC:117-120
     assert k.shape[1:] == (1, HQ, D)
     assert v.shape[1:] == (1, HV, D)
     assert q.shape[0] == v.shape[0]
-    return gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale)
+    out_dtype = q.dtype
+    assert out_dtype.is_floating_point
+    q, k, v, a, b = (t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+                     for t in (q, k, v, a, b))
+    o, s = gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale)
+    return (o if out_dtype == torch.bfloat16 else o.to(out_dtype)), s
 
 
 @torch.no_grad()

@@ -121,13 +121,28 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     path -- a parallel chunk-preparation launch and ``HV * N * slices`` state
     slices -- when the chains alone leave CUs idle, else the fused chain
     kernel), ``"fused"`` (one workgroup per chain) or ``"split"`` with
-    ``slices`` in (2, 4, 8) state slices per chain.  Results of the two paths
-    are the same bit for bit without ``qk_l2norm``.
+    ``slices`` in (4, 8) state slices per chain.  Without ``qk_l2norm`` the
+    two paths give the same final state bit for bit.
+
+    Input range: the state path multiplies fp16 operands, so k, v, the state
+    and the intermediate X and Vn must stay below 65504 in magnitude (far
+    above normalised q / k and states of ordinary size; the reference's bf16
+    intermediates reach 3e38).
     """
+    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, q.shape[1], v.shape[1],
+                    check_total=validate)
+    return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
+                   final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h,
+                   path=path, slices=slices)
+
+
+def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, output=None,
+            final_state=None, workspace=None, qk_l2norm: bool = False, h=None,
+            path: str = "auto", slices: int = 8):
+    """Allocation, layout and the C call behind :func:`gdn_prefill` (inputs
+    already validated)."""
     T, nq, d = q.shape
     nv = v.shape[1]
-    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv,
-                    check_total=validate)
     assert nv % nq == 0
     scale = _resolve_scale(scale)
     N = cu_seqlens.numel() - 1
@@ -213,17 +228,20 @@ def gdn_prefill_h(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, 
 
 @torch.no_grad()
 def run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale):
-    """Reference-compatible prefill entry (PRE:1762-1802), qk4 / v8 / d128."""
-    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, check_total=False)
-    return gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale)
+    """Reference-compatible prefill entry (PRE:1762-1802), qk4 / v8 / d128.
+
+    Validates once, as PRE:1635-1667 does (one host read of
+    ``cu_seqlens[-1]``), then launches."""
+    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
+    return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale)
 
 
 @torch.no_grad()
 def run_dps(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, final_state):
     """Destination-passing prefill: writes ``output`` / ``final_state``, returns None."""
-    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, check_total=False)
-    gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
-                final_state=final_state)
+    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
+    _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
+            final_state=final_state)
 
 
 class PreparedPrefill:
