@@ -182,7 +182,8 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk
     total_ms, kern_ms = timed_launches(launch, steps, warmup)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, T=T, N=N, lens=lens, HQ=w["HQ"],
                 HV=w["HV"], flops=prefill_flops(T, w["HV"]),
-                flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True))
+                flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True),
+                path=gpre.auto_path(N, w["HV"]))
 
 
 def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
@@ -206,6 +207,83 @@ def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     return dict(total_ms=total_ms, kernel_ms=kern_ms, chunks=NT, h_bytes=h.numel() * 2)
 
 
+def bench_run_latency(dev, kernel_us, reps=50):
+    """End-to-end latency of the reference-compatible ``run`` entry points
+    (validation, allocation of the outputs and workspace, the ctypes call,
+    the kernel) with a synchronisation after every call: the median over
+    ``reps`` calls, beside the kernel time alone."""
+    res = {}
+
+    def median_call_us(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append((time.perf_counter() - t0) * 1e6)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    for name, B in (("decode_b1_qk4_v8", 1), ("decode_b256_qk4_v8", 256)):
+        g = _to(ginp.decode_inputs(B, 4, 8, seed=1000 if B == 1 else 1001), dev)
+        us = median_call_us(lambda: gdec.run(g["q"], g["k"], g["v"], g["state"], g["A_log"],
+                                             g["a"], g["dt_bias"], g["b"], g["scale"]))
+        k = kernel_us.get(name)
+        res[name] = {"run_us": round(us, 1), "kernel_us": k,
+                     "host_overhead_us": None if k is None else round(us - k, 1)}
+    name = "prefill_t4096_n1_qk4_v8"
+    g = _to(ginp.prefill_inputs([4096], 4, 8, seed=1002), dev)
+    us = median_call_us(lambda: gpre.run(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
+                                         g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"]))
+    k = kernel_us.get(name)
+    res[name] = {"run_us": round(us, 1), "kernel_us": k,
+                 "host_overhead_us": None if k is None else round(us - k, 1)}
+    return res
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_decode_b1(budget_s=2.0):
+    """Oracle decode step in fp32 at batch 1 (the workload with one sequence,
+    qk4/v8): microseconds per step on the host cores."""
+    from oracle import gdn_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = ginp.decode_inputs(1, 4, 8, seed=1000)
+    args = [x[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b")]
+    for _ in range(3):
+        O.decode_step(*args, x["scale"], dtype=torch.float32)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.decode_step(*args, x["scale"], dtype=torch.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 2000:
+            break
+    return {"value": round(el / n * 1e6, 1), "unit": "us/step", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{n} fp32 oracle decode steps at B=1 qk4/v8 ({el:.1f} s)"}
+
+
 def cpu_baseline_decode(budget_s=12.0, B=256):
     """Oracle decode step in fp32 on the host cores (bounded sample of B=256)."""
     from oracle import gdn_oracle as O
@@ -225,6 +303,27 @@ def cpu_baseline_decode(budget_s=12.0, B=256):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{n} fp32 oracle decode steps at B=256 qk4/v8 ({el:.1f} s)"}
+
+
+def cpu_baseline_prefill_chunked():
+    """Chunked (64-token WY) fp32 oracle form over the whole 32 768-token
+    qk16 / v32 workload, once: the second CPU line beside the per-token form."""
+    from oracle import gdn_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    name = "prefill_varlen8_t32768_qk16_v32"
+    w = ginp.WORKLOADS[name]
+    lens = ginp.workload_lengths(name)
+    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
+    args = [x[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
+    t0 = time.perf_counter()
+    O.prefill_chunked(*args, x["scale"], dtype=torch.float32)
+    el = time.perf_counter() - t0
+    toks = sum(lens)
+    return {"value": round(toks / el, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"the full {toks}-token qk16/v32 workload once, fp32 chunked oracle "
+                      f"(64-token chunks) ({el:.1f} s)"}
 
 
 def cpu_baseline_prefill():
@@ -256,6 +355,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=30)
     ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-latency", action="store_true",
+                    help="skip the end-to-end run() latency measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 plain 256 MiB device copies (the reference kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE counter readings to bytes)")
@@ -367,6 +468,27 @@ def main():
                 "prefill_kernel_us": line["prefill"]["roofline"]["kernel_us"]}
             print(f"# prefill with q/k L2-norm: {r['kernel_ms'] * 1e3:.1f} us", file=sys.stderr,
                   flush=True)
+            # the two qk4/v8 prefill workloads: one 4096-token sequence, and 16
+            # varlen sequences (lengths ~ U[128, 8192]) with initial states
+            for name in ("prefill_t4096_n1_qk4_v8", "prefill_varlen16_qk4_v8"):
+                r = bench_prefill(dev, args.prefill_steps, PREFILL_WARMUP, name=name)
+                kus = r["kernel_ms"] * 1e3
+                tfl = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+                kernels = (["gdn_prefill_prep_kernel", "gdn_prefill_slice_kernel"]
+                           if r["path"].startswith("split") else ["gdn_prefill_chain_kernel"])
+                line[name] = {
+                    "workload": name, "tokens": r["T"], "sequences": r["N"], "qk_heads": r["HQ"],
+                    "v_heads": r["HV"], "path": r["path"], "kernel_us": round(kus, 2),
+                    "tokens_per_s": round(r["T"] / (r["kernel_ms"] * 1e-3), 1),
+                    "roofline": {"bound": "mfma", "achieved": round(tfl, 2),
+                                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4),
+                                 "flops_per_launch": r["flops"], "kernels": kernels,
+                                 "time_basis": "both launches of one call" if len(kernels) > 1
+                                 else "one launch"}}
+                print(f"# {name} ({r['path']}): {kus:.1f} us, {tfl:.1f} TFLOP/s "
+                      f"({tfl / MFMA_BF16_PEAK_TFLOPS * 100:.2f}% of bf16 MFMA peak)",
+                      file=sys.stderr, flush=True)
 
     if args.copy_calibration:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
@@ -376,10 +498,22 @@ def main():
         torch.cuda.synchronize()
         line["copy_calibration_bytes"] = src.numel() * 4
 
+    if args.only == "all" and not args.no_latency:
+        kus = {"decode_b256_qk4_v8": line.get("roofline", {}).get("kernel_us"),
+               "prefill_t4096_n1_qk4_v8": line.get("prefill_t4096_n1_qk4_v8", {}).get("kernel_us")}
+        r1 = bench_decode(dev, 50, 10, B=1, sets=1)
+        kus["decode_b1_qk4_v8"] = round(r1["kernel_ms"] * 1e3, 2)
+        line["run_latency"] = bench_run_latency(dev, kus)
+        print(f"# run latency: {json.dumps(line['run_latency'])}", file=sys.stderr, flush=True)
+
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode()
+        line["cpu_baseline"]["cpu_model"] = cpu_model()
+        line["cpu_baseline"]["decode_b1"] = cpu_baseline_decode_b1()
         if args.only in ("all", "prefill") and "error" not in line.get("prefill", {"error": 1}):
             line["prefill"]["cpu_baseline"] = cpu_baseline_prefill()
+            line["prefill"]["cpu_baseline"]["cpu_model"] = line["cpu_baseline"]["cpu_model"]
+            line["prefill"]["cpu_baseline"]["chunked"] = cpu_baseline_prefill_chunked()
     print(json.dumps(line), flush=True)
 
 

@@ -166,6 +166,13 @@ int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                        void* workspace, size_t workspace_bytes, int flags, void* stream);
 
 /*
+ * State slices per chain the automatic path selection of gdn_prefill_fwd uses
+ * for N sequences of HV v-heads on the current device: 8 or 4 (split path),
+ * or 0 (the fused chain kernel).
+ */
+int gdn_prefill_auto_slices(int N, int HV);
+
+/*
  * Workspace bytes of gdn_prefill_split_fwd: 14 080 bytes per (chunk, v-head)
  * and 18 432 per (chunk, qk-head) for an upper bound of T / 64 + N chunks.
  */

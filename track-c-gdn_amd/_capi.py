@@ -37,6 +37,7 @@ SIGNATURES = {
                              _P, _P, _P, _S, _P]),
     "gdn_prefill_ex_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                 _P, _P, _P, _S, _I, _P]),
+    "gdn_prefill_auto_slices": (_I, [_I, _I]),
     "gdn_prefill_split_workspace_bytes": (_S, [_I, _I, _I, _I]),
     "gdn_prefill_split_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                    _P, _P, _I, _P, _S, _I, _P]),

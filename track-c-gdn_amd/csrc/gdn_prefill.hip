@@ -1013,6 +1013,11 @@ extern "C" size_t gdn_prefill_workspace_bytes(int N, int T, int HQ, int HV) {
   return gdn::prefill_split_auto_slices(N, HV) > 0 ? gdn::prefill_split_workspace_bytes(N, T, HQ, HV) : 0;
 }
 
+extern "C" int gdn_prefill_auto_slices(int N, int HV) {
+  if (N <= 0 || HV <= 0) return 0;
+  return gdn::prefill_split_auto_slices(N, HV);
+}
+
 extern "C" size_t gdn_prefill_split_workspace_bytes(int N, int T, int HQ, int HV) {
   if (N <= 0 || T < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return 0;
   return gdn::prefill_split_workspace_bytes(N, T, HQ, HV);

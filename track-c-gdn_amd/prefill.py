@@ -83,6 +83,13 @@ def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
     return int(_capi.lib().gdn_prefill_workspace_bytes(N, T, HQ, HV))
 
 
+def auto_path(N: int, HV: int) -> str:
+    """The kernels the library's automatic choice runs for N sequences of HV
+    v-heads on the current device: ``"fused"`` or ``"split<slices>"``."""
+    s = int(_capi.lib().gdn_prefill_auto_slices(N, HV))
+    return f"split{s}" if s > 0 else "fused"
+
+
 def split_workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
     """Workspace of the split path (chunk preparation + state slices)."""
     return int(_capi.lib().gdn_prefill_split_workspace_bytes(N, T, HQ, HV))
