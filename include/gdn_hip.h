@@ -201,6 +201,27 @@ int gdn_prefill_split_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* 
                           void* workspace, size_t workspace_bytes, int flags, void* stream);
 
 /*
+ * gdn_prefill_split_fwd without a caller workspace and without any device
+ * allocation: no reference counterpart.  It serves callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops).  The
+ * workspace is a static device array of gdn_prefill_split_noalloc_max_bytes()
+ * (32 MiB) that each GPU the library runs on holds until the process ends;
+ * problems whose gdn_prefill_split_workspace_bytes exceed it return
+ * GDN_ERR_WORKSPACE before any launch (for example T = 4096, N = 1 at
+ * qk4 / v8 needs 12.1 MB).  All calls on one GPU share the array: calls that
+ * overlap on one GPU (other streams, other threads) race.  Results equal
+ * gdn_prefill_split_fwd's bit for bit.
+ */
+size_t gdn_prefill_split_noalloc_max_bytes(void);
+int gdn_prefill_split_noalloc_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                  const float* state, const float* A_log, const uint16_t* a,
+                                  const float* dt_bias, const uint16_t* b,
+                                  const void* cu_seqlens, int cu_is_int32, int N, int T,
+                                  int HQ, int HV, float scale,
+                                  uint16_t* out, float* final_state, int slices, int flags,
+                                  void* stream);
+
+/*
  * Number of 64-token chunks of a varlen batch, sum over n of
  * ceil(len_n / 64) with len_n from cu_seqlens clamped into [0, T] as the
  * kernels clamp it: the first dimension of the h output below.  Reads a HOST

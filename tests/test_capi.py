@@ -23,7 +23,8 @@ def test_header_declares_expected_entry_points():
         "gdn_abi_version", "gdn_error_string", "gdn_decode_fwd", "gdn_decode_pool_fwd",
         "gdn_decode_multi_fwd", "gdn_decode_ex_fwd", "gdn_prefill_workspace_bytes",
         "gdn_prefill_fwd", "gdn_prefill_ex_fwd", "gdn_prefill_chunk_count", "gdn_prefill_h_fwd",
-        "gdn_prefill_split_workspace_bytes", "gdn_prefill_split_fwd", "gdn_prefill_auto_slices"])
+        "gdn_prefill_split_workspace_bytes", "gdn_prefill_split_fwd", "gdn_prefill_auto_slices",
+        "gdn_prefill_split_noalloc_max_bytes", "gdn_prefill_split_noalloc_fwd"])
 
 
 def test_library_exports_every_declared_symbol():

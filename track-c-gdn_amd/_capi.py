@@ -41,6 +41,9 @@ SIGNATURES = {
     "gdn_prefill_split_workspace_bytes": (_S, [_I, _I, _I, _I]),
     "gdn_prefill_split_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                    _P, _P, _I, _P, _S, _I, _P]),
+    "gdn_prefill_split_noalloc_max_bytes": (_S, []),
+    "gdn_prefill_split_noalloc_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                                           _F, _P, _P, _I, _I, _P]),
     "gdn_prefill_chunk_count": (ctypes.c_longlong, [_P, _I, _I, _I]),
     "gdn_prefill_h_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                _P, _P, _P, _I, _P, _S, _I, _P]),

@@ -1065,6 +1065,29 @@ extern "C" int gdn_prefill_split_fwd(const uint16_t* q, const uint16_t* k, const
                                    static_cast<hipStream_t>(stream));
 }
 
+extern "C" size_t gdn_prefill_split_noalloc_max_bytes(void) { return gdn::prefill_scratch_bytes(); }
+
+extern "C" int gdn_prefill_split_noalloc_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                             const float* state, const float* A_log, const uint16_t* a,
+                                             const float* dt_bias, const uint16_t* b,
+                                             const void* cu_seqlens, int cu_is_int32, int N, int T,
+                                             int HQ, int HV, float scale, uint16_t* out,
+                                             float* final_state, int slices, int flags, void* stream) {
+  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
+                                    N, T, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if ((flags & ~GDN_FLAGS_ALL) || !gdn::prefill_split_slices_valid(slices)) return GDN_ERR_SHAPE;
+  if (gdn::prefill_split_workspace_bytes(N, T, HQ, HV) > gdn::prefill_scratch_bytes())
+    return GDN_ERR_WORKSPACE;
+  if (N == 0) return GDN_OK;
+  hipError_t err = hipSuccess;
+  void* ws = gdn::prefill_scratch(&err);
+  if (ws == nullptr) return -int(err);
+  return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
+                                   T, HQ, HV, scale, out, final_state, slices, ws, flags,
+                                   static_cast<hipStream_t>(stream));
+}
+
 extern "C" long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, int N,
                                              int T) {
   if (!cu_seqlens_host || N < 0 || T < 0) return -1;

@@ -21,6 +21,11 @@ int prefill_split_auto_slices(int N, int HV);
 
 bool prefill_split_slices_valid(int slices);
 
+// Size and current-device address of the library's static split-path
+// workspace (the allocation-free entry point's scratch).
+size_t prefill_scratch_bytes();
+void* prefill_scratch(hipError_t* err);
+
 // Enqueues both launches on st; workspace holds prefill_split_workspace_bytes.
 int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                          const float* A_log, const uint16_t* a, const float* dt_bias,

@@ -26,6 +26,8 @@
 // (gdn_prefill.hip): bf16 MFMA for A and P from the exact bf16 rows, fp16
 // operands on the state path, bf16 S for Q S^T, fp32 accumulation.
 
+#include <mutex>
+
 #include "gdn_prefill_common.h"
 #include "gdn_prefill_split.h"
 #include "../../include/gdn_hip.h"
@@ -803,6 +805,40 @@ int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   return e == hipSuccess ? GDN_OK : -int(e);
 }
 
+// Workspace of the allocation-free split entry point: a device array of
+// kScratchBytes that every GPU the library runs on holds until the process
+// ends.  Host code uses it only through the per-device address that
+// hipGetSymbolAddress returns (the array's name is a host-side stand-in).
+// Calls on one GPU share it: calls that overlap on one GPU race.  Nothing in
+// it has to start at zero (the preparation launch writes every byte the
+// slice launch reads).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of `scratch` on the current device (looked up once per device), or
+// NULL with *err set.
+void* scratch_address(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
 int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -836,6 +872,10 @@ int prefill_split_auto_slices(int N, int HV) {
 }
 
 bool prefill_split_slices_valid(int slices) { return slices == 4 || slices == 8; }
+
+size_t prefill_scratch_bytes() { return kScratchBytes; }
+
+void* prefill_scratch(hipError_t* err) { return scratch_address(err); }
 
 int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                          const float* A_log, const uint16_t* a, const float* dt_bias,
