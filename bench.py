@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 import __graft_entry__  # noqa: E402
 
 __graft_entry__.load_package()
+from track_c_gdn_amd import conv as gconv  # noqa: E402
 from track_c_gdn_amd import decode as gdec  # noqa: E402
 from track_c_gdn_amd import inputs as ginp  # noqa: E402
 from track_c_gdn_amd import prefill as gpre  # noqa: E402
@@ -263,6 +264,61 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def bench_conv(dev, steps, warmup, HQ=16, HV=32, W=4):
+    """q/k/v causal conv1d + SiLU over the 32 768-token, 8-sequence workload at
+    qk16 / v32 (C = 8192 channels), written as GDN's q, k, v.  Algorithmic
+    bytes: x read once, q/k/v written once, conv states read and written."""
+    lens = ginp.workload_lengths("prefill_varlen8_t32768_qk16_v32")
+    T, N = sum(lens), len(lens)
+    C = 256 * HQ + 128 * HV
+    gen = torch.Generator(device=dev).manual_seed(90)
+    x = torch.randn(T, C, device=dev, generator=gen).to(torch.bfloat16)
+    w = torch.randn(C, W, device=dev, generator=gen) * 0.5
+    st = torch.randn(N, C, W - 1, device=dev, generator=gen).to(torch.bfloat16)
+    cu = torch.zeros(N + 1, dtype=torch.int64)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    cu = cu.to(dev)
+    q = torch.empty(T, HQ, D, dtype=torch.bfloat16, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(T, HV, D, dtype=torch.bfloat16, device=dev)
+    fin = torch.empty_like(st)
+    lib = gconv._capi.lib()
+    p = gconv._capi.ptr
+    args = (p(x), p(w), None, p(cu), 0, N, T, C, W, p(st), p(fin), W - 1, p(q), p(k), p(v),
+            D * HQ, D * HQ, gconv._capi.GDN_ACT_SILU, gconv._capi.stream_handle(dev))
+
+    def launch(i):
+        lib.gdn_qkv_conv1d_fwd(*args)
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    nbytes = 2 * T * C * 2 + 2 * N * C * (W - 1) * 2
+    return dict(kernel_ms=kern_ms, bytes=nbytes, T=T, C=C)
+
+
+def bench_conv_update(dev, steps, warmup, B=1024, HQ=16, HV=32, W=4):
+    """Decode conv update at batch 1024, qk16 / v32: one token per sequence,
+    the [1024, 8192, 3] bf16 conv state updated in place."""
+    C = 256 * HQ + 128 * HV
+    gen = torch.Generator(device=dev).manual_seed(91)
+    x = torch.randn(B, C, device=dev, generator=gen).to(torch.bfloat16)
+    w = torch.randn(C, W, device=dev, generator=gen) * 0.5
+    st = torch.randn(B, C, W - 1, device=dev, generator=gen).to(torch.bfloat16)
+    q = torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(B, 1, HV, D, dtype=torch.bfloat16, device=dev)
+    lib = gconv._capi.lib()
+    p = gconv._capi.ptr
+    args = (p(x), p(w), None, p(st), W - 1, None, B, B, C, W, p(q), p(k), p(v), D * HQ, D * HQ,
+            gconv._capi.GDN_ACT_SILU, gconv._capi.stream_handle(dev))
+
+    def launch(i):
+        lib.gdn_qkv_conv1d_update(*args)
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    nbytes = 2 * B * C * 2 + 2 * B * C * (W - 1) * 2
+    return dict(kernel_ms=kern_ms, bytes=nbytes, B=B, C=C)
+
+
 def cpu_baseline_decode_b1(budget_s=2.0):
     """Oracle decode step in fp32 at batch 1 (the workload with one sequence,
     qk4/v8): microseconds per step on the host cores."""
@@ -353,7 +409,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--prefill-steps", type=int, default=30)
-    ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "conv"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-latency", action="store_true",
                     help="skip the end-to-end run() latency measurements")
@@ -497,6 +553,18 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         line["copy_calibration_bytes"] = src.numel() * 4
+
+    if args.only in ("all", "conv"):
+        for key, fn, wl in (("qkv_conv1d", bench_conv, "conv1d_varlen8_t32768_qk16_v32"),
+                            ("qkv_conv1d_update", bench_conv_update, "conv1d_update_b1024_qk16_v32")):
+            r = fn(dev, 30, 10)
+            gbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+            line[key] = {"workload": wl, "channels": r["C"], "kernel_us": round(r["kernel_ms"] * 1e3, 2),
+                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                      "bytes_per_launch": r["bytes"]}}
+            print(f"# {key}: {r['kernel_ms'] * 1e3:.1f} us, {gbs:.0f} GB/s "
+                  f"({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)", file=sys.stderr, flush=True)
 
     if args.only == "all" and not args.no_latency:
         kus = {"decode_b256_qk4_v8": line.get("roofline", {}).get("kernel_us"),

@@ -254,6 +254,56 @@ int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
                       void* workspace, size_t workspace_bytes, int flags, void* stream);
 
+/* Activations of the q/k/v convolution. */
+#define GDN_ACT_NONE 0
+#define GDN_ACT_SILU 1
+
+/*
+ * Short causal convolution ahead of GDN (no reference counterpart: the
+ * reference operators take q, k, v after it).  In a Qwen3-Next-style layer
+ * the q, k, v projections, concatenated channel-wise ("mixed_qkv"), pass
+ * through a depthwise causal conv1d of kernel size W and SiLU before GDN:
+ *   y[t, c] = act(bias[c] + sum_w weight[c, w] h[t - (W - 1) + w, c]),
+ * h being each sequence's inputs preceded by its conv state (or zeros).
+ *   x          : [T, C] bf16 (token-major, C a multiple of 8).
+ *   weight     : [C, W] fp32, W in 2..4;  bias : [C] fp32 or NULL.
+ *   cu_seqlens : as for gdn_prefill_fwd (int64, or int32 when cu_is_int32).
+ *   conv_state_in  : [N, C, state_len] bf16 (the inputs that preceded each
+ *                    sequence, oldest first) or NULL for zeros.
+ *   conv_state_out : [N, C, state_len] bf16 or NULL: the last state_len inputs
+ *                    of every sequence (its state entries where the sequence is
+ *                    shorter).  Must not alias conv_state_in.
+ *   state_len  : W - 1 .. 8.
+ *   out_q, out_k, out_v : the output split by channel into three row-major
+ *                    tensors of widths cq, ck and C - cq - ck (multiples of
+ *                    8): GDN's q [T, HQ, 128], k [T, HQ, 128], v [T, HV, 128]
+ *                    with cq = ck = 128 HQ.  With out_k = out_v = NULL the
+ *                    whole [T, C] output goes to out_q.
+ *   activation : GDN_ACT_SILU or GDN_ACT_NONE.
+ */
+int gdn_qkv_conv1d_fwd(const uint16_t* x, const float* weight, const float* bias,
+                       const void* cu_seqlens, int cu_is_int32, int N, int T, int C, int W,
+                       const uint16_t* conv_state_in, uint16_t* conv_state_out, int state_len,
+                       uint16_t* out_q, uint16_t* out_k, uint16_t* out_v, int cq, int ck,
+                       int activation, void* stream);
+
+/*
+ * One decode token per sequence through the same convolution, the conv state
+ * updated in place (shifted by one, the token appended).
+ *   x          : [B, C] bf16.
+ *   conv_state : [pool, C, state_len] bf16, state_len W - 1 or W (else
+ *                GDN_ERR_SHAPE); row slot_ids[b] (or b when
+ *                slot_ids is NULL, then pool_size >= B) serves sequence b.
+ *                Distinct slots; a slot outside [0, pool_size) leaves the
+ *                state untouched and yields a zero output row.
+ *   outputs, weight, bias, activation as for gdn_qkv_conv1d_fwd (B tokens).
+ * Equal bit for bit to gdn_qkv_conv1d_fwd over length-1 sequences.
+ */
+int gdn_qkv_conv1d_update(const uint16_t* x, const float* weight, const float* bias,
+                          uint16_t* conv_state, int state_len, const int32_t* slot_ids,
+                          int pool_size, int B, int C, int W, uint16_t* out_q, uint16_t* out_k,
+                          uint16_t* out_v, int cq, int ck, int activation, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,13 @@ How each function is pinned (tests/test_oracle.py):
 * qk_l2norm        -- torch.nn.functional.normalize where eps is negligible,
                       the closed form c/sqrt(c^2 + eps) on scaled unit vectors,
                       zero maps to zero, sign/permutation equivariance.
+* causal_conv1d, causal_conv1d_update -- the short causal convolution that
+                      precedes GDN in a Qwen3-Next-style layer (no reference
+                      counterpart): torch.nn.functional.conv1d with groups =
+                      channels and left zero padding, an elementwise
+                      brute-force loop, the impulse response (the reversed
+                      taps), split invariance through the returned state, and
+                      update == a length-1 sequence.
 """
 
 from __future__ import annotations
@@ -59,6 +66,8 @@ __all__ = [
     "prefill_chunk_states",
     "default_scale",
     "qk_l2norm",
+    "causal_conv1d",
+    "causal_conv1d_update",
 ]
 
 
@@ -384,3 +393,67 @@ def prefill_chunked(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None
             S = torch.exp(gl)[:, None, None] * S + rnd(Vd).transpose(1, 2) @ Kc
         final[n] = S
     return o, final
+
+
+# ---------------------------------------------------------------------------
+# Short causal convolution ahead of GDN (no reference counterpart).  In a
+# Qwen3-Next-style layer the q, k, v projections, concatenated channel-wise
+# (mixed_qkv), pass through a depthwise causal conv1d of kernel size W (4)
+# and SiLU before they become GDN's q, k, v; decode keeps the last inputs of
+# every sequence as a conv state.
+
+
+def _silu(y):
+    return y * torch.sigmoid(y)
+
+
+def causal_conv1d(x, weight, bias, cu_seqlens, conv_state=None, activation: Optional[str] = "silu",
+                  state_len: Optional[int] = None, dtype=torch.float64):
+    """Depthwise causal conv1d over packed varlen sequences.
+
+    ``x [T, C]`` (token-major), ``weight [C, W]``, ``bias [C]`` or ``None``,
+    ``cu_seqlens [N+1]``, ``conv_state [N, C, S]`` (S >= W - 1; the inputs
+    that preceded each sequence, oldest first) or ``None`` for zeros.  For a
+    sequence with history ``h = [state, x_bos .. x_eos-1]`` (index S + i for
+    token bos + i):
+
+        y[bos + i, c] = act(bias[c] + sum_w weight[c, w] h[S + i - (W - 1) + w, c])
+
+    Returns ``(y [T, C], final_state [N, C, S])``, the final state being the
+    last S entries of h.
+    """
+    T, C = x.shape
+    W = weight.shape[1]
+    N = cu_seqlens.numel() - 1
+    S = state_len if state_len is not None else (conv_state.shape[2] if conv_state is not None else W - 1)
+    assert S >= W - 1
+    xf = x.to(dtype)
+    wf = weight.to(dtype)
+    y = torch.zeros(T, C, dtype=dtype)
+    final = torch.zeros(N, C, S, dtype=dtype)
+    for n in range(N):
+        bos, eos = int(cu_seqlens[n]), int(cu_seqlens[n + 1])
+        st = conv_state[n].to(dtype) if conv_state is not None else torch.zeros(C, S, dtype=dtype)
+        h = torch.cat([st, xf[bos:eos].T], dim=1)                   # [C, S + L]
+        L = eos - bos
+        for i in range(L):
+            win = h[:, S + i - (W - 1): S + i + 1]                  # [C, W]
+            y[bos + i] = (win * wf).sum(dim=1)
+        final[n] = h[:, -S:]
+    if bias is not None:
+        y = y + bias.to(dtype)[None, :]
+    if activation == "silu":
+        y = _silu(y)
+    else:
+        assert activation is None
+    return y, final
+
+
+def causal_conv1d_update(x, conv_state, weight, bias, activation: Optional[str] = "silu",
+                         dtype=torch.float64):
+    """One decode token per sequence: ``x [B, C]``, ``conv_state [B, C, S]``.
+    Returns ``(y [B, C], new_state [B, C, S])`` (the state shifted by one,
+    x appended), the same as :func:`causal_conv1d` on length-1 sequences."""
+    B = x.shape[0]
+    cu = torch.arange(B + 1, dtype=torch.int64)
+    return causal_conv1d(x, weight, bias, cu, conv_state, activation, dtype=dtype)

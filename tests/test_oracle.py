@@ -345,3 +345,104 @@ def test_prefill_chunk_states_against_prefix_runs(lens, C):
             torch.testing.assert_close(h[slot], s_ref[0], atol=1e-12, rtol=1e-12)
     h0 = O.prefill_chunk_states(q, k, v, None, A_log, a, dt_bias, b, cu, chunk_size=C)
     assert float(h0[0].abs().max()) == 0.0
+
+
+# ---------------------------------------------------------------------------
+# causal conv1d (the short convolution ahead of GDN in a Qwen3-Next-style layer)
+
+
+def _conv_brute(x, w, bias, cu, state, act):
+    """Elementwise loops: y[t, c] = act(bias + sum_w w[c, w] * hist(t - (W-1) + w))."""
+    T, C = x.shape
+    W = w.shape[1]
+    N = cu.numel() - 1
+    S = state.shape[2] if state is not None else W - 1
+    y = torch.zeros(T, C, dtype=torch.float64)
+    for n in range(N):
+        bos, eos = int(cu[n]), int(cu[n + 1])
+        for t in range(bos, eos):
+            for c in range(C):
+                acc = float(bias[c]) if bias is not None else 0.0
+                for j in range(W):
+                    u = t - (W - 1) + j
+                    if u >= bos:
+                        val = float(x[u, c])
+                    else:
+                        si = S - (bos - u)
+                        val = float(state[n, c, si]) if (state is not None and si >= 0) else 0.0
+                    acc += float(w[c, j]) * val
+                y[t, c] = acc / (1.0 + math.exp(-acc)) if act == "silu" else acc
+    return y
+
+
+@pytest.mark.parametrize("W,S", [(4, 3), (4, 4), (3, 2), (2, 5)])
+def test_causal_conv1d_matches_brute_force(W, S):
+    gen = torch.Generator().manual_seed(31 + W + S)
+    lens = [0, 1, 2, 7, 3]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0).tolist()))
+    T, C, N = sum(lens), 6, len(lens)
+    x = torch.randn(T, C, generator=gen, dtype=torch.float64)
+    w = torch.randn(C, W, generator=gen, dtype=torch.float64)
+    bias = torch.randn(C, generator=gen, dtype=torch.float64)
+    state = torch.randn(N, C, S, generator=gen, dtype=torch.float64)
+    for act in ("silu", None):
+        y, fin = O.causal_conv1d(x, w, bias, cu, state, act)
+        torch.testing.assert_close(y, _conv_brute(x, w, bias, cu, state, act), rtol=1e-12, atol=1e-12)
+    # final state: the last S entries of [state, x_seq] per sequence
+    for n in range(N):
+        h = torch.cat([state[n], x[int(cu[n]):int(cu[n + 1])].T], dim=1)
+        assert torch.equal(fin[n], h[:, -S:])
+
+
+def test_causal_conv1d_matches_torch_conv1d():
+    """Library routine: F.conv1d with groups = C and W - 1 zeros of left padding
+    (no state) on each sequence."""
+    gen = torch.Generator().manual_seed(41)
+    lens = [5, 17, 1]
+    cu = torch.tensor([0, 5, 22, 23])
+    C, W = 8, 4
+    x = torch.randn(23, C, generator=gen, dtype=torch.float64)
+    w = torch.randn(C, W, generator=gen, dtype=torch.float64)
+    y, _ = O.causal_conv1d(x, w, None, cu, None, None)
+    for n in range(3):
+        seq = x[int(cu[n]):int(cu[n + 1])].T[None]                   # [1, C, L]
+        ref = torch.nn.functional.conv1d(seq, w[:, None, :], padding=W - 1, groups=C)[0, :, :lens[n]]
+        torch.testing.assert_close(y[int(cu[n]):int(cu[n + 1])], ref.T, rtol=1e-12, atol=1e-12)
+
+
+def test_causal_conv1d_impulse_and_linearity():
+    C, W = 4, 4
+    w = torch.arange(1, C * W + 1, dtype=torch.float64).reshape(C, W)
+    x = torch.zeros(6, C, dtype=torch.float64)
+    x[1] = 1.0
+    y, _ = O.causal_conv1d(x, w, None, torch.tensor([0, 6]), None, None)
+    # token 1 + d sees the impulse through tap W - 1 - d
+    for d in range(W):
+        torch.testing.assert_close(y[1 + d], w[:, W - 1 - d])
+    assert float(y[0].abs().max()) == 0.0 and float(y[5].abs().max()) == 0.0
+    gen = torch.Generator().manual_seed(43)
+    a, b = torch.randn(6, C, generator=gen, dtype=torch.float64), torch.randn(6, C, generator=gen, dtype=torch.float64)
+    ya, _ = O.causal_conv1d(a, w, None, torch.tensor([0, 6]), None, None)
+    yb, _ = O.causal_conv1d(b, w, None, torch.tensor([0, 6]), None, None)
+    yab, _ = O.causal_conv1d(2 * a - b, w, None, torch.tensor([0, 6]), None, None)
+    torch.testing.assert_close(yab, 2 * ya - yb)
+
+
+def test_causal_conv1d_split_invariance_and_update():
+    gen = torch.Generator().manual_seed(47)
+    C, W, S, T = 5, 4, 3, 11
+    x = torch.randn(T, C, generator=gen, dtype=torch.float64)
+    w = torch.randn(C, W, generator=gen, dtype=torch.float64)
+    s0 = torch.randn(1, C, S, generator=gen, dtype=torch.float64)
+    y, fin = O.causal_conv1d(x, w, None, torch.tensor([0, T]), s0, "silu")
+    for t in (1, 2, 6):
+        y1, s1 = O.causal_conv1d(x[:t], w, None, torch.tensor([0, t]), s0, "silu")
+        y2, s2 = O.causal_conv1d(x[t:], w, None, torch.tensor([0, T - t]), s1, "silu")
+        torch.testing.assert_close(torch.cat([y1, y2]), y)
+        torch.testing.assert_close(s2, fin)
+    # decode: token by token through the update form
+    st = s0.clone()
+    for t in range(T):
+        yt, st = O.causal_conv1d_update(x[t:t + 1], st, w, None, "silu")
+        torch.testing.assert_close(yt[0], y[t])
+    torch.testing.assert_close(st, fin)

@@ -9,10 +9,11 @@ FlashInfer-Bench style harness does with ``kernel.py::run``.
 
 Submodules:
   decode   -- decode ``run`` / ``run_dps`` / ``gdn_decode`` / ``decode_pool_``
-  prefill  -- prefill ``run`` / ``run_dps`` / ``gdn_prefill``
+  prefill  -- prefill ``run`` / ``run_dps`` / ``gdn_prefill`` (fused or split path)
+  conv     -- the short causal conv1d + SiLU ahead of GDN (q/k/v straight to GDN layout)
   inputs   -- seeded synthetic workloads
   build    -- hipcc recipe for libgdn_hip.so
   _capi    -- ctypes binding of include/gdn_hip.h
 """
 
-__all__ = ["decode", "prefill", "inputs", "build"]
+__all__ = ["decode", "prefill", "conv", "inputs", "build"]

@@ -19,6 +19,8 @@ GDN_ERR_NULL = -1001
 GDN_ERR_SHAPE = -1002
 GDN_ERR_WORKSPACE = -1003
 GDN_QK_L2NORM = 1
+GDN_ACT_NONE = 0
+GDN_ACT_SILU = 1
 
 # Every symbol include/gdn_hip.h declares, with (restype, argtypes).
 _P = ctypes.c_void_p
@@ -45,6 +47,10 @@ SIGNATURES = {
     "gdn_prefill_split_noalloc_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                                            _F, _P, _P, _I, _I, _P]),
     "gdn_prefill_chunk_count": (ctypes.c_longlong, [_P, _I, _I, _I]),
+    "gdn_qkv_conv1d_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I,
+                                _I, _P]),
+    "gdn_qkv_conv1d_update": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _I,
+                                   _P]),
     "gdn_prefill_h_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                _P, _P, _P, _I, _P, _S, _I, _P]),
 }
