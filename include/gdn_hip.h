@@ -254,6 +254,61 @@ int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
                       void* workspace, size_t workspace_bytes, int flags, void* stream);
 
+/*
+ * Backward of the prefill (no counterpart in the reference, which is
+ * forward-only: gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:1;
+ * it consumes the per-chunk states h that chunk_gated_delta_rule_fwd_h
+ * produces, kernel.py:1153-1160, here gdn_prefill_h_fwd).
+ *
+ * Device workspace bytes of gdn_prefill_bwd: per (64-token chunk slot,
+ * v-head) 128 KiB (the chunk's state-gradient transition and the gradient of
+ * the state leaving it), plus 2 T HV 512 B when HV > HQ.  0 for invalid
+ * sizes.
+ */
+size_t gdn_prefill_bwd_workspace_bytes(int N, int T, int HQ, int HV);
+
+/*
+ * Gradients of a loss L(out, final_state) of gdn_prefill_fwd with respect to
+ * its inputs, given dL/d out and dL/d final_state.
+ *   q, k, v, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ, HV,
+ *   scale      : the forward's inputs (scale as the forward used it).
+ *   h          : [h_chunks, HV, 128, 128] bf16, the states entering every
+ *                chunk as gdn_prefill_h_fwd wrote them for the same inputs;
+ *                h_chunks must be at least gdn_prefill_chunk_count(...).
+ *   d_out      : [T, HV, 128] bf16.
+ *   d_final_state : [N, HV, 128, 128] fp32, or NULL for zeros.
+ * Outputs (fp32, written whole):
+ *   dq, dk     : [T, HQ, 128] (summed over the v-heads sharing a qk-head).
+ *   dv         : [T, HV, 128].
+ *   dg, dbeta  : [T, HV]: gradients of the per-token log-decay
+ *                g = -exp(A_log) softplus(a + dt_bias) and of beta = sigmoid(b);
+ *                gdn_gate_bwd maps them to a, b, A_log, dt_bias.
+ *   d_initial_state : [N, HV, 128, 128], or NULL when not wanted.
+ * Products take bf16 operands with fp32 accumulation.  Three launches
+ * (plus one when HV > HQ) on `stream`: per-chunk state-gradient transitions
+ * (all chunks at once), the chain over each sequence's chunks in reverse,
+ * and the per-chunk gradients.  Not q/k L2-normalising (GDN_QK_L2NORM has no
+ * backward here).  GDN_ERR_WORKSPACE when the workspace is NULL or short.
+ */
+int gdn_prefill_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                    const float* A_log, const uint16_t* a, const float* dt_bias,
+                    const uint16_t* b, const void* cu_seqlens, int cu_is_int32, int N, int T,
+                    int HQ, int HV, float scale, const uint16_t* h, int h_chunks,
+                    const uint16_t* d_out, const float* d_final_state, float* dq, float* dk,
+                    float* dv, float* dg, float* dbeta, float* d_initial_state,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Gradients of the prefill gating (kernel.py:1706-1722) per token and v-head:
+ *   da = dg (-exp(A_log) sigmoid(a + dt_bias)),   db = dbeta beta (1 - beta),
+ *   dA_log = sum_t dg g,   ddt_bias = sum_t da    (fixed summation order).
+ * a, b: [T, HV] bf16; dg, dbeta, da, db: [T, HV] fp32; A_log, dt_bias,
+ * dA_log, ddt_bias: [HV] fp32.  No counterpart in the reference.
+ */
+int gdn_gate_bwd(const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
+                 const float* dg, const float* dbeta, int T, int HV, float* da, float* db,
+                 float* dA_log, float* ddt_bias, void* stream);
+
 /* Activations of the q/k/v convolution. */
 #define GDN_ACT_NONE 0
 #define GDN_ACT_SILU 1

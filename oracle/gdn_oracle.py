@@ -36,6 +36,13 @@ How each function is pinned (tests/test_oracle.py):
 * qk_l2norm        -- torch.nn.functional.normalize where eps is negligible,
                       the closed form c/sqrt(c^2 + eps) on scaled unit vectors,
                       zero maps to zero, sign/permutation equivariance.
+* prefill_backward -- central finite differences of <o, R1> + <S_final, R2>
+                      along random directions for every input, and
+                      torch.autograd through prefill_recurrent.
+* prefill_backward_chunked -- equals prefill_backward in float64 at chunk
+                      sizes 4, 16, 64 with ragged tails and empty sequences.
+* gate_backward    -- through the finite-difference and autograd checks of
+                      prefill_backward (a, b, A_log, dt_bias directions).
 * causal_conv1d, causal_conv1d_update -- the short causal convolution that
                       precedes GDN in a Qwen3-Next-style layer (no reference
                       counterpart): torch.nn.functional.conv1d with groups =
@@ -68,6 +75,9 @@ __all__ = [
     "qk_l2norm",
     "causal_conv1d",
     "causal_conv1d_update",
+    "prefill_backward",
+    "prefill_backward_chunked",
+    "gate_backward",
 ]
 
 
@@ -393,6 +403,233 @@ def prefill_chunked(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None
             S = torch.exp(gl)[:, None, None] * S + rnd(Vd).transpose(1, 2) @ Kc
         final[n] = S
     return o, final
+
+
+# ---------------------------------------------------------------------------
+# Backward of the prefill (no reference counterpart: the reference is
+# forward-only, PRE:1).  Gradients of a loss L(o, final_state) with respect to
+# q, k, v, the per-token log-decay g and beta, and the initial state, given
+# dL/do and dL/d(final_state); then through the gating to a, b, A_log and
+# dt_bias.
+
+
+def prefill_backward(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, d_out, d_final=None,
+                     dtype=torch.float64):
+    """Per-token reverse recurrence of :func:`prefill_recurrent`.
+
+    Forward per token (v-head h, state ``S [V, K]``)::
+
+        S' = e^{g_t} S_{t-1};  u = beta_t (v_t - S' k_t);  S_t = S' + u k_t^T;  o_t = scale S_t q_t
+
+    Reverse, with ``dS`` the gradient of ``S_t`` (``d_final`` after the last
+    token of a sequence, zeros if ``None``)::
+
+        dS += scale do_t q_t^T;        dq_t = scale S_t^T do_t
+        du  = dS k_t;                  dk_t = dS^T u
+        dbeta_t = du . (v_t - S' k_t); dv_t = beta_t du
+        dS' = dS - beta_t du k_t^T;    dk_t -= beta_t S'^T du
+        dg_t = <dS', S'>;              dS_{t-1} = e^{g_t} dS'
+
+    ``dq`` / ``dk`` are summed over the v-heads that share a qk-head.  Returns
+    a dict with ``dq, dk [T, HQ, D]``, ``dv [T, HV, D]``, ``dg, dbeta [T, HV]``
+    and ``dh0 [N, HV, V, K]``.  The states ``S_t`` are recomputed forward
+    from checkpoints at every 64th token.
+    """
+    T, HQ, HV, D, N = _check_prefill_shapes(q, k, v, state, a, b, cu_seqlens)
+    scale = default_scale(scale, D)
+    G = HV // HQ
+    ld, beta = prefill_log_decay_beta(a, b, A_log, dt_bias, dtype)
+    qh = _expand_heads(q.to(dtype), HV)
+    kh = _expand_heads(k.to(dtype), HV)
+    vh = v.to(dtype)
+    do = d_out.to(dtype)
+    dq = torch.zeros(T, HV, D, dtype=dtype)
+    dk = torch.zeros(T, HV, D, dtype=dtype)
+    dv = torch.zeros(T, HV, D, dtype=dtype)
+    dg = torch.zeros(T, HV, dtype=dtype)
+    db = torch.zeros(T, HV, dtype=dtype)
+    dh0 = torch.zeros(N, HV, D, D, dtype=dtype)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    bl = 64
+
+    def step(S, t):
+        Sp = torch.exp(ld[t])[:, None, None] * S
+        sk = torch.einsum("hvk,hk->hv", Sp, kh[t])
+        u = beta[t][:, None] * (vh[t] - sk)
+        return Sp, sk, u, Sp + u[:, :, None] * kh[t][:, None, :]
+
+    for n in range(N):
+        bos, eos = cu[n], cu[n + 1]
+        S = torch.zeros(HV, D, D, dtype=dtype) if state is None else state[n].to(dtype).clone()
+        ckpt = {}
+        for t in range(bos, eos):
+            if (t - bos) % bl == 0:
+                ckpt[t] = S.clone()
+            S = step(S, t)[3]
+        dS = torch.zeros(HV, D, D, dtype=dtype) if d_final is None else d_final[n].to(dtype).clone()
+        for blk in sorted(ckpt, reverse=True):
+            S = ckpt[blk]
+            rec = []
+            for t in range(blk, min(blk + bl, eos)):
+                Sp, sk, u, S = step(S, t)
+                rec.append((t, Sp, sk, u, S))
+            for t, Sp, sk, u, St in reversed(rec):
+                dS = dS + scale * do[t][:, :, None] * qh[t][:, None, :]
+                dq[t] = scale * torch.einsum("hvk,hv->hk", St, do[t])
+                du = torch.einsum("hvk,hk->hv", dS, kh[t])
+                dk[t] = torch.einsum("hvk,hv->hk", dS, u)
+                db[t] = (du * (vh[t] - sk)).sum(-1)
+                dv[t] = beta[t][:, None] * du
+                dsk = -beta[t][:, None] * du
+                dS = dS + dsk[:, :, None] * kh[t][:, None, :]
+                dk[t] += torch.einsum("hvk,hv->hk", Sp, dsk)
+                dg[t] = (dS * Sp).sum((-1, -2))
+                dS = torch.exp(ld[t])[:, None, None] * dS
+        dh0[n] = dS
+    dq = dq.view(T, HQ, G, D).sum(2)
+    dk = dk.view(T, HQ, G, D).sum(2)
+    return {"dq": dq, "dk": dk, "dv": dv, "dg": dg, "dbeta": db, "dh0": dh0}
+
+
+def prefill_backward_chunked(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, d_out,
+                             d_final=None, h=None, chunk_size: int = 64, dtype=torch.float64):
+    """Chunked backward: the algorithm of the HIP backward, in ``dtype``.
+
+    Per chunk (``gam`` chunk-local cumsum of g, ``E = e^gam``,
+    ``Dc = e^{gam_L - gam}``, ``S`` the state entering the chunk -- ``h``
+    from :func:`prefill_chunk_states` when not given -- and ``dSn`` the
+    gradient of the state leaving it), with the forward quantities
+    ``Ar = tril_strict(e^{gam_i-gam_j} K K^T)``, ``A = diag(beta) Ar``,
+    ``Tm = (I + A)^-1``, ``P = scale tril_incl(e^{gam_i-gam_j} Q K^T)``,
+    ``Xr = V - E K S^T``, ``X = beta Xr``, ``Vn = Tm X``:
+
+    1. the state-gradient chain, one product per chunk::
+
+           W2 = Tm^T Dc K;  M = e^{gam_L} I - W2^T (beta E K)
+           G1 = Tm^T P^T dO;  R = dO^T (scale E Q) - G1^T (beta E K)
+           dS_prev = dSn M + R
+
+    2. per chunk, given ``S`` and ``dSn``::
+
+           dVn = P^T dO + Dc K dSn^T;  dX = Tm^T dVn;  dV = beta dX
+           dP = dO Vn^T;  dTm = dVn X^T;  dA = -Tm^T dTm Tm^T (strictly lower)
+           dQ = scale E dO S + (scale e^{gam_i-gam_j} dP)_incl K
+           dK = Dc Vn dSn - beta E dX S + (...)_incl^T Q + dAb K + dAb^T K,
+                dAb = beta_i e^{gam_i-gam_j} dA
+           dbeta = rowsum(dA * Ar) + rowsum(dX * Xr)
+           dgam  = rowsum - colsum of (dP * P) and of (dA * A)
+                   + scale E rowsum(Q * (dO S)) - beta E rowsum(dX * K S^T)
+                   - Dc rowsum(Vn * K dSn^T);  dgam_L += sum(Dc rowsum(Vn * K dSn^T)) + e^{gam_L} <dSn, S>
+           dg = reverse cumsum of dgam over the chunk
+
+    Pinned equal to :func:`prefill_backward` in float64.
+    """
+    T, HQ, HV, D, N = _check_prefill_shapes(q, k, v, state, a, b, cu_seqlens)
+    scale = default_scale(scale, D)
+    G = HV // HQ
+    C = int(chunk_size)
+    if h is None:
+        h = prefill_chunk_states(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, C, dtype)
+    ld, beta = prefill_log_decay_beta(a, b, A_log, dt_bias, dtype)
+    qh = _expand_heads(q.to(dtype), HV)
+    kh = _expand_heads(k.to(dtype), HV)
+    vh = v.to(dtype)
+    do = d_out.to(dtype)
+    out = {n: torch.zeros(T, HV, D, dtype=dtype) for n in ("dq", "dk", "dv")}
+    dg = torch.zeros(T, HV, dtype=dtype)
+    db = torch.zeros(T, HV, dtype=dtype)
+    dh0 = torch.zeros(N, HV, D, D, dtype=dtype)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    slot = 0
+    for n in range(N):
+        starts = list(range(cu[n], cu[n + 1], C))
+        chunks = []
+        for i, s in enumerate(starts):
+            e = min(s + C, cu[n + 1])
+            L = e - s
+            gam = torch.cumsum(ld[s:e], 0).transpose(0, 1)                 # [HV, L]
+            bet = beta[s:e].transpose(0, 1)
+            E = torch.exp(gam)
+            Dc = torch.exp(gam[:, L - 1:L] - gam)
+            Kc, Qc = kh[s:e].transpose(0, 1), qh[s:e].transpose(0, 1)       # [HV, L, D]
+            Vc, dOc = vh[s:e].transpose(0, 1), do[s:e].transpose(0, 1)
+            dec = torch.exp(gam[:, :, None] - gam[:, None, :])
+            strict = torch.tril(torch.ones(L, L, dtype=torch.bool), -1)
+            incl = torch.tril(torch.ones(L, L, dtype=torch.bool), 0)
+            zero = torch.zeros((), dtype=dtype)
+            Ar = torch.where(strict, dec * (Kc @ Kc.transpose(1, 2)), zero)
+            A = bet[:, :, None] * Ar
+            eye = torch.eye(L, dtype=dtype).expand(HV, L, L)
+            Tm = torch.linalg.solve_triangular(eye + A, eye, upper=False, unitriangular=True)
+            P = scale * torch.where(incl, dec * (Qc @ Kc.transpose(1, 2)), zero)
+            BEK = (bet * E)[:, :, None] * Kc
+            W2 = Tm.transpose(1, 2) @ (Dc[:, :, None] * Kc)
+            M = torch.exp(gam[:, L - 1])[:, None, None] * torch.eye(D, dtype=dtype) \
+                - W2.transpose(1, 2) @ BEK
+            G1 = Tm.transpose(1, 2) @ (P.transpose(1, 2) @ dOc)
+            R = dOc.transpose(1, 2) @ ((scale * E)[:, :, None] * Qc) - G1.transpose(1, 2) @ BEK
+            chunks.append(dict(s=s, e=e, L=L, gam=gam, bet=bet, E=E, Dc=Dc, Kc=Kc, Qc=Qc, Vc=Vc,
+                               dOc=dOc, Ar=Ar, A=A, Tm=Tm, P=P, M=M, R=R, incl=incl, strict=strict,
+                               dec=dec, S=h[slot + i].to(dtype)))
+        dS = torch.zeros(HV, D, D, dtype=dtype) if d_final is None else d_final[n].to(dtype).clone()
+        for c in reversed(chunks):
+            c["dSn"] = dS
+            dS = dS @ c["M"] + c["R"]
+        dh0[n] = dS
+        slot += len(starts)
+        for c in chunks:
+            s, e, L = c["s"], c["e"], c["L"]
+            S, dSn, Tm, P, Kc, Qc = c["S"], c["dSn"], c["Tm"], c["P"], c["Kc"], c["Qc"]
+            bet, E, Dc, dOc, gam = c["bet"], c["E"], c["Dc"], c["dOc"], c["gam"]
+            KS = Kc @ S.transpose(1, 2)
+            Xr = c["Vc"] - E[:, :, None] * KS
+            X = bet[:, :, None] * Xr
+            Vn = Tm @ X
+            KdS = Kc @ dSn.transpose(1, 2)
+            dVn = P.transpose(1, 2) @ dOc + Dc[:, :, None] * KdS
+            dX = Tm.transpose(1, 2) @ dVn
+            dP = torch.where(c["incl"], dOc @ Vn.transpose(1, 2), torch.zeros((), dtype=dtype))
+            dTm = dVn @ X.transpose(1, 2)
+            dA = torch.where(c["strict"], -(Tm.transpose(1, 2) @ dTm @ Tm.transpose(1, 2)),
+                             torch.zeros((), dtype=dtype))
+            dPm = scale * c["dec"] * dP
+            dAb = bet[:, :, None] * c["dec"] * dA
+            dOS = dOc @ S
+            dQ = scale * E[:, :, None] * dOS + dPm @ Kc
+            dK = Dc[:, :, None] * (Vn @ dSn) - (bet * E)[:, :, None] * (dX @ S) \
+                + dPm.transpose(1, 2) @ Qc + dAb @ Kc + dAb.transpose(1, 2) @ Kc
+            dbet = (dA * c["Ar"]).sum(-1) + (dX * Xr).sum(-1)
+            pp = dP * P
+            aa = dA * c["A"]
+            vk = Dc * (Vn * KdS).sum(-1)
+            dgam = pp.sum(-1) - pp.sum(-2) + aa.sum(-1) - aa.sum(-2) \
+                + scale * E * (Qc * dOS).sum(-1) - bet * E * (dX * KS).sum(-1) - vk
+            dgam[:, L - 1] += vk.sum(-1) + torch.exp(gam[:, L - 1]) * (dSn * S).sum((-1, -2))
+            dgc = torch.flip(torch.cumsum(torch.flip(dgam, [1]), 1), [1])
+            out["dq"][s:e] = dQ.transpose(0, 1)
+            out["dk"][s:e] = dK.transpose(0, 1)
+            out["dv"][s:e] = (bet[:, :, None] * dX).transpose(0, 1)
+            dg[s:e] = dgc.transpose(0, 1)
+            db[s:e] = dbet.transpose(0, 1)
+    dq = out["dq"].view(T, HQ, G, D).sum(2)
+    dk = out["dk"].view(T, HQ, G, D).sum(2)
+    return {"dq": dq, "dk": dk, "dv": out["dv"], "dg": dg, "dbeta": db, "dh0": dh0}
+
+
+def gate_backward(A_log, a, dt_bias, b, dg, dbeta, dtype=torch.float64):
+    """Gradients of the prefill gating (PRE:1706-1722) given dL/dg and dL/dbeta.
+
+    ``g = -exp(A_log) softplus(x)``, ``x = a + dt_bias``, ``beta = sigmoid(b)``:
+    ``da = dg (-exp(A_log) sigmoid(x))``, ``ddt_bias = sum_t da``,
+    ``dA_log = sum_t dg g``, ``db = dbeta beta (1 - beta)``.
+    """
+    A_log = A_log.to(dtype)
+    x = a.to(dtype) + dt_bias.to(dtype)[None, :]
+    g = -torch.exp(A_log)[None, :] * softplus_stable(x)
+    da = dg.to(dtype) * (-torch.exp(A_log)[None, :] * torch.sigmoid(x))
+    beta = torch.sigmoid(b.to(dtype))
+    db = dbeta.to(dtype) * beta * (1.0 - beta)
+    return {"da": da, "db": db, "dA_log": (dg.to(dtype) * g).sum(0), "ddt_bias": da.sum(0)}
 
 
 # ---------------------------------------------------------------------------

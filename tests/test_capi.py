@@ -25,7 +25,8 @@ def test_header_declares_expected_entry_points():
         "gdn_prefill_fwd", "gdn_prefill_ex_fwd", "gdn_prefill_chunk_count", "gdn_prefill_h_fwd",
         "gdn_prefill_split_workspace_bytes", "gdn_prefill_split_fwd", "gdn_prefill_auto_slices",
         "gdn_prefill_split_noalloc_max_bytes", "gdn_prefill_split_noalloc_fwd",
-        "gdn_qkv_conv1d_fwd", "gdn_qkv_conv1d_update"])
+        "gdn_qkv_conv1d_fwd", "gdn_qkv_conv1d_update", "gdn_prefill_bwd_workspace_bytes",
+        "gdn_prefill_bwd", "gdn_gate_bwd"])
 
 
 def test_library_exports_every_declared_symbol():

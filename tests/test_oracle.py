@@ -446,3 +446,97 @@ def test_causal_conv1d_split_invariance_and_update():
         yt, st = O.causal_conv1d_update(x[t:t + 1], st, w, None, "silu")
         torch.testing.assert_close(yt[0], y[t])
     torch.testing.assert_close(st, fin)
+
+
+# --------------------------------------------------------------------------- prefill backward
+
+def _rand_prefill_bwd(lens, HQ=2, HV=4, D=6, seed=0, state=True):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    x = dict(
+        q=F.normalize(torch.randn(T, HQ, D, generator=g, dtype=DT), dim=-1),
+        k=F.normalize(torch.randn(T, HQ, D, generator=g, dtype=DT), dim=-1),
+        v=torch.randn(T, HV, D, generator=g, dtype=DT),
+        state=torch.randn(len(lens), HV, D, D, generator=g, dtype=DT) * 0.3 if state else None,
+        A_log=torch.rand(HV, generator=g, dtype=DT) * 2 - 2,
+        a=torch.randn(T, HV, generator=g, dtype=DT),
+        dt_bias=torch.randn(HV, generator=g, dtype=DT) * 0.1,
+        b=torch.randn(T, HV, generator=g, dtype=DT),
+        cu_seqlens=torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int64))
+    d_out = torch.randn(T, HV, D, generator=g, dtype=DT)
+    d_fin = torch.randn(len(lens), HV, D, D, generator=g, dtype=DT)
+    return x, d_out, d_fin
+
+
+def _loss(x, d_out, d_fin, scale):
+    o, fin = O.prefill_recurrent(x["q"], x["k"], x["v"], x["state"], x["A_log"], x["a"],
+                                 x["dt_bias"], x["b"], x["cu_seqlens"], scale)
+    return (o * d_out).sum() + (fin * d_fin).sum()
+
+
+def _all_grads(x, d_out, d_fin, scale):
+    gr = O.prefill_backward(x["q"], x["k"], x["v"], x["state"], x["A_log"], x["a"], x["dt_bias"],
+                            x["b"], x["cu_seqlens"], scale, d_out, d_fin)
+    gg = O.gate_backward(x["A_log"], x["a"], x["dt_bias"], x["b"], gr["dg"], gr["dbeta"])
+    return {"q": gr["dq"], "k": gr["dk"], "v": gr["dv"], "state": gr["dh0"], "a": gg["da"],
+            "b": gg["db"], "A_log": gg["dA_log"], "dt_bias": gg["ddt_bias"]}
+
+
+@pytest.mark.parametrize("lens,state", [([5, 0, 9], True), ([70], False), ([1, 3], True)])
+def test_prefill_backward_matches_finite_differences(lens, state):
+    """Central differences of L = <o, R1> + <S_final, R2> along random
+    directions, per input, against <grad, direction> (fp64, eps 1e-6)."""
+    x, d_out, d_fin = _rand_prefill_bwd(lens, seed=len(lens) + sum(lens), state=state)
+    scale = 0.37
+    grads = _all_grads(x, d_out, d_fin, scale)
+    gen = torch.Generator().manual_seed(5)
+    for name, gval in grads.items():
+        if x[name] is None:
+            continue
+        dirn = torch.randn(x[name].shape, generator=gen, dtype=DT)
+        eps = 1e-6
+        xp = dict(x); xp[name] = x[name] + eps * dirn
+        xm = dict(x); xm[name] = x[name] - eps * dirn
+        fd = (_loss(xp, d_out, d_fin, scale) - _loss(xm, d_out, d_fin, scale)) / (2 * eps)
+        an = (gval * dirn).sum()
+        assert abs(float(fd - an)) <= 1e-6 * max(1.0, abs(float(an))), (name, float(fd), float(an))
+
+
+def test_prefill_backward_matches_autograd():
+    """torch.autograd through the forward oracle gives the same gradients."""
+    x, d_out, d_fin = _rand_prefill_bwd([13, 6], HQ=1, HV=2, D=5, seed=3)
+    scale = -0.5
+    leaves = {n: x[n].clone().requires_grad_(True) for n in ("q", "k", "v", "state", "A_log", "a",
+                                                           "dt_bias", "b")}
+    xa = dict(x, **leaves)
+    L = _loss(xa, d_out, d_fin, scale)
+    auto = dict(zip(leaves, torch.autograd.grad(L, list(leaves.values()))))
+    mine = _all_grads(x, d_out, d_fin, scale)
+    for n in leaves:
+        torch.testing.assert_close(mine[n], auto[n], rtol=1e-10, atol=1e-12)
+
+
+def test_prefill_backward_zero_state_and_no_final_grad():
+    """With d_final = None and no initial state: the gradient of <o, R1> alone
+    (autograd), and dh0 equals the gradient through a zero initial state."""
+    x, d_out, _ = _rand_prefill_bwd([4, 8], HQ=2, HV=2, D=4, seed=9, state=False)
+    gr = O.prefill_backward(x["q"], x["k"], x["v"], None, x["A_log"], x["a"], x["dt_bias"], x["b"],
+                            x["cu_seqlens"], 1.0, d_out, None)
+    s0 = torch.zeros(2, 2, 4, 4, dtype=DT, requires_grad=True)
+    o, _ = O.prefill_recurrent(x["q"], x["k"], x["v"], s0, x["A_log"], x["a"], x["dt_bias"], x["b"],
+                               x["cu_seqlens"], 1.0)
+    (ds0,) = torch.autograd.grad((o * d_out).sum(), [s0])
+    torch.testing.assert_close(gr["dh0"], ds0, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("lens,C,state", [([5, 0, 9], 4, True), ([70, 33], 16, True),
+                                          ([130], 64, False), ([1, 64, 65], 64, True)])
+def test_prefill_backward_chunked_equals_per_token(lens, C, state):
+    """The chunked backward (state-gradient transitions M, R per chunk, then the
+    per-chunk gradients from S and dSn) equals the per-token reverse recurrence."""
+    x, d_out, d_fin = _rand_prefill_bwd(lens, HQ=2, HV=4, D=8, seed=1, state=state)
+    args = [x[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
+    r1 = O.prefill_backward(*args, 0.3, d_out, d_fin)
+    r2 = O.prefill_backward_chunked(*args, 0.3, d_out, d_fin, chunk_size=C)
+    for k in r1:
+        torch.testing.assert_close(r2[k], r1[k], rtol=1e-10, atol=1e-12)

@@ -11,9 +11,10 @@ Submodules:
   decode   -- decode ``run`` / ``run_dps`` / ``gdn_decode`` / ``decode_pool_``
   prefill  -- prefill ``run`` / ``run_dps`` / ``gdn_prefill`` (fused or split path)
   conv     -- the short causal conv1d + SiLU ahead of GDN (q/k/v straight to GDN layout)
+  backward -- prefill backward from the per-chunk states, gate gradients, autograd operator
   inputs   -- seeded synthetic workloads
   build    -- hipcc recipe for libgdn_hip.so
   _capi    -- ctypes binding of include/gdn_hip.h
 """
 
-__all__ = ["decode", "prefill", "conv", "inputs", "build"]
+__all__ = ["decode", "prefill", "conv", "backward", "inputs", "build"]

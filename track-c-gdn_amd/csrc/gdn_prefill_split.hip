@@ -71,60 +71,6 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
                :: "s"(lds), "v"(off), "s"(base) : "memory", "m0");
 }
 
-// Inclusive prefix sum of an int over the 64 lanes of a wave.
-__device__ __forceinline__ int wave_scan_incl(int x, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
-  return x;
-}
-
-// Sequence n and chunk i of chunk slot `slot` = chunk_offset(n) + i, where
-// chunk_offset(n) counts the 64-token chunks of sequences 0 .. n-1 (lengths
-// clamped as seq_bounds clamps them).  n = -1 past the last chunk.
-// Wave-uniform result.  The reference builds the same (sequence, chunk)
-// table on the host (prepare_chunk_indices, kernel.py:175-202).
-template <typename CuT>
-__device__ void locate_chunk(const CuT* cu, int N, int T, int slot, int lane, int& n, int& ci) {
-  int base = 0;
-  n = -1;
-  ci = 0;
-  for (int m0 = 0; m0 < N; m0 += 64) {
-    const int m = m0 + lane;
-    int cnt = 0;
-    if (m < N) {
-      int bm, lm;
-      seq_bounds(cu, m, T, bm, lm);
-      cnt = (lm + C - 1) / C;
-    }
-    const int incl = wave_scan_incl(cnt, lane);
-    const unsigned long long hit = __ballot(base + incl > slot);
-    if (hit) {
-      const int first = __ffsll((long long)hit) - 1;
-      n = m0 + first;
-      ci = slot - base - __shfl(incl - cnt, first);
-      return;
-    }
-    base += __shfl(incl, 63);
-  }
-}
-
-// chunk_offset(n) (wave-uniform): lanes take every 64th sequence, then a wave sum.
-template <typename CuT>
-__device__ int chunk_offset(const CuT* cu, int n, int T, int lane) {
-  int part = 0;
-  for (int m = lane; m < n; m += 64) {
-    int bm, lm;
-    seq_bounds(cu, m, T, bm, lm);
-    part += (lm + C - 1) / C;
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
-  return __builtin_amdgcn_readfirstlane(part);
-}
-
 // ---------------------------------------------------------------------------
 // Preparation of one chunk of one v-head.  Four waves:
 //   copies   raw K and Q rows (bf16) of the chunk into LDS, swizzled;
