@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 import __graft_entry__  # noqa: E402
 
 __graft_entry__.load_package()
+from track_c_gdn_amd import backward as gbwd  # noqa: E402
 from track_c_gdn_amd import conv as gconv  # noqa: E402
 from track_c_gdn_amd import decode as gdec  # noqa: E402
 from track_c_gdn_amd import inputs as ginp  # noqa: E402
@@ -206,6 +207,47 @@ def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
 
     total_ms, kern_ms = timed_launches(launch, steps, warmup)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, chunks=NT, h_bytes=h.numel() * 2)
+
+
+# MFMA products the backward executes per (64-token chunk, v-head): 656 in the
+# transition kernel, 256 in the reverse chain, 1360 in the gradient kernel,
+# each a 16x16x32 product of 16 384 flops (dense tiles as launched).
+BWD_MFMA_PER_CHUNK_HEAD = 656 + 256 + 1360
+
+
+def bench_backward(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
+    """Backward of the prefill (gdn_prefill_bwd: transition, reverse chain,
+    per-chunk gradients, head sums) from the forward's h, one C call per step."""
+    w = ginp.WORKLOADS[name]
+    lens = ginp.workload_lengths(name)
+    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
+    g = _to(x, dev)
+    T, N, HQ, HV = sum(lens), len(lens), w["HQ"], w["HV"]
+    args = [g[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
+    _, _, h = gpre.gdn_prefill_h(*args, g["scale"])
+    gen = torch.Generator(device=dev).manual_seed(17)
+    d_out = torch.randn(T, HV, D, device=dev, generator=gen).to(torch.bfloat16)
+    d_fin = torch.randn(N, HV, D, D, device=dev, generator=gen) * 0.1
+    outs = [torch.empty(T, HQ, D, device=dev), torch.empty(T, HQ, D, device=dev),
+            torch.empty(T, HV, D, device=dev), torch.empty(T, HV, device=dev),
+            torch.empty(T, HV, device=dev), torch.empty(N, HV, D, D, device=dev)]
+    need = gbwd.workspace_bytes(N, T, HQ, HV)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    lib = gpre._capi.lib()
+    p = gpre._capi.ptr
+    cu = g["cu_seqlens"]
+    call = (p(g["q"]), p(g["k"]), p(g["v"]), p(g["A_log"]), p(g["a"]), p(g["dt_bias"]), p(g["b"]),
+            p(cu), 1 if cu.dtype == torch.int32 else 0, N, T, HQ, HV, float(g["scale"]), p(h),
+            h.shape[0], p(d_out), p(d_fin), *[p(o) for o in outs], p(ws), need,
+            gpre._capi.stream_handle(dev))
+
+    def launch(i):
+        lib.gdn_prefill_bwd(*call)
+
+    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    flops = h.shape[0] * HV * BWD_MFMA_PER_CHUNK_HEAD * 16384
+    return dict(kernel_ms=kern_ms, T=T, N=N, HQ=HQ, HV=HV, chunks=h.shape[0], flops=flops,
+                ws_bytes=need)
 
 
 def bench_run_latency(dev, kernel_us, reps=50):
@@ -409,7 +451,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--prefill-steps", type=int, default=30)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "conv"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "conv", "backward"],
+                    default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-latency", action="store_true",
                     help="skip the end-to-end run() latency measurements")
@@ -545,6 +588,28 @@ def main():
                 print(f"# {name} ({r['path']}): {kus:.1f} us, {tfl:.1f} TFLOP/s "
                       f"({tfl / MFMA_BF16_PEAK_TFLOPS * 100:.2f}% of bf16 MFMA peak)",
                       file=sys.stderr, flush=True)
+
+    if args.only in ("all", "backward"):
+        for key, name in (("prefill_backward", "prefill_varlen8_t32768_qk16_v32"),
+                          ("prefill_backward_t4096_n1_qk4_v8", "prefill_t4096_n1_qk4_v8")):
+            r = bench_backward(dev, 10, 3, name=name)
+            kus = r["kernel_ms"] * 1e3
+            tfl = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+            line[key] = {
+                "workload": name, "tokens": r["T"], "sequences": r["N"], "qk_heads": r["HQ"],
+                "v_heads": r["HV"], "kernel_us": round(kus, 2),
+                "tokens_per_s": round(r["T"] / (r["kernel_ms"] * 1e-3), 1),
+                "kernels": ["gdn_bwd_prep_kernel", "gdn_bwd_chain_kernel", "gdn_bwd_grad_kernel",
+                            "gdn_bwd_head_sum_kernel"],
+                "roofline": {"bound": "mfma", "achieved": round(tfl, 2),
+                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "flops_per_launch": r["flops"],
+                             "flops_basis": "executed bf16 MFMA products, 2272 per chunk and v-head",
+                             "time_basis": "all launches of one call"}}
+            print(f"# backward {name}: {kus:.1f} us, {tfl:.1f} TFLOP/s "
+                  f"({tfl / MFMA_BF16_PEAK_TFLOPS * 100:.1f}% of bf16 MFMA peak)",
+                  file=sys.stderr, flush=True)
 
     if args.copy_calibration:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)

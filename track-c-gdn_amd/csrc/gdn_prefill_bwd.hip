@@ -113,7 +113,7 @@ __device__ __forceinline__ float group4_sum(float x) {
 constexpr int GB_GAM = 0, GB_BETA = C, GB_E = 2 * C, GB_DC = 3 * C, GB_L = 4 * C, GB_EL = 4 * C + 1;
 constexpr int GB_SZ = 4 * C + 4;
 
-__device__ void chunk_gates(const float* A_log, const uint16_t* a, const float* dt_bias,
+__device__ __forceinline__ void chunk_gates(const float* A_log, const uint16_t* a, const float* dt_bias,
                             const uint16_t* b, int HV, int hv, int t0, int len, int lane, float* gb) {
   float g = 0.f, be = 0.f;
   if (lane < len) {
@@ -133,42 +133,117 @@ __device__ void chunk_gates(const float* A_log, const uint16_t* a, const float* 
   }
 }
 
-// Rows [t0, t0 + len) of a [*, stride] bf16 tensor (128 columns from col0)
-// into a [64][LDK] LDS buffer, rows past len zero: 16 bytes per thread-step.
-__device__ __forceinline__ void load_rows(uint16_t* dst, const uint16_t* src, size_t stride, int t0,
-                                          int len, int tid, int nthreads) {
-  for (int x = tid; x < C * 16; x += nthreads) {
-    const int r = x >> 4, cc = (x & 15) * 8;
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (r < len) w = *reinterpret_cast<const uint4*>(src + size_t(t0 + r) * stride + cc);
-    *reinterpret_cast<uint4*>(dst + r * LDK + cc) = w;
+// Rows [t0, t0 + len) of a [*, stride] bf16 tensor (128 columns) into a
+// [64][LDK] LDS buffer, rows past len zero, in two steps so that the HBM
+// reads of several tensors are in flight together: rows_fetch issues this
+// thread's 16-byte reads (2 of the 1024 of a tensor, 512 threads), rows_store
+// writes them.
+__device__ __forceinline__ void rows_fetch(uint4 (&w)[2], const uint16_t* src, size_t stride, int t0,
+                                           int len, int tid) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int x = tid + it * kGradThreads, r = x >> 4, cc = (x & 15) * 8;
+    w[it] = r < len ? *reinterpret_cast<const uint4*>(src + size_t(t0 + r) * stride + cc)
+                    : make_uint4(0, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void rows_store(uint16_t* dst, const uint4 (&w)[2], int tid) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int x = tid + it * kGradThreads, r = x >> 4, cc = (x & 15) * 8;
+    *reinterpret_cast<uint4*>(dst + r * LDK + cc) = w[it];
+  }
+}
+
+// A 128 x 128 bf16 state (rows of 256 B in HBM) into a [128][LDK] LDS buffer,
+// in the same two steps (4 reads per thread).
+__device__ __forceinline__ void state_fetch(uint4 (&w)[4], const uint16_t* src, int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) w[it] = reinterpret_cast<const uint4*>(src)[tid + it * kGradThreads];
+}
+
+__device__ __forceinline__ void state_store(uint16_t* dst, const uint4 (&w)[4], int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int x = tid + it * kGradThreads, r = x >> 4, cc = (x & 15) * 8;
+    *reinterpret_cast<uint4*>(dst + r * LDK + cc) = w[it];
   }
 }
 
 // (I + A)^-1 of the strictly lower A = diag(beta) Ar (fp32 [64][LDA] in LDS,
-// zero on and above the diagonal) by forward substitution in fp32, lane j
-// computing column j:  x_i = delta_ij - beta_i sum_{l<i} Ar_il x_l.  Reads of
-// Ar past column i - 1 meet zeros (and entries of x still zero).  Written
-// bf16 [i][j].
-__device__ void unit_lower_inverse(const float* sAr, const float* gb, uint16_t* sTm, int lane) {
-  float x[C];
+// zero on and above the diagonal), one wave, in fp32:
+//   * the four diagonal 16 x 16 blocks by forward substitution, lane l taking
+//     column l % 16 of block l / 16:  x_r = delta_rc - beta_r sum_{m<r} Ar_rm x_m;
+//   * the blocks below them block-row by block-row,
+//     T_ij = -T_ii (sum_{j<=m<i} A_im T_mj), on fp32 MFMA 16x16x4, each
+//     product's sum staged through sZ (16 x 17 floats).
+// The fp32 blocks go to sT ([64][LDA]), the bf16 result (zero above the
+// diagonal) to sTm [i][j].  The wave's LDS operations complete in order, so
+// its own writes are visible to its later reads without a barrier.
+__device__ __forceinline__ void unit_lower_inverse(const float* sAr, const float* gb, float* sT,
+                                                   float* sZ, uint16_t* sTm, int lane) {
+  const int bi = lane >> 4, c = lane & 15;
+  {
+    float x[16];
 #pragma unroll
-  for (int i = 0; i < C; ++i) x[i] = 0.f;
+    for (int r = 0; r < 16; ++r) x[r] = 0.f;
 #pragma unroll
-  for (int i = 0; i < C; ++i) {
-    float acc = 0.f;
+    for (int r = 0; r < 16; ++r) {
+      const int row = 16 * bi + r;
+      float acc = 0.f;
 #pragma unroll
-    for (int l = 0; l < i; l += 4) {
-      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sAr[i * LDA + l]);
-      acc = fmaf(a4[0], x[l], acc);
-      acc = fmaf(a4[1], x[l + 1], acc);
-      acc = fmaf(a4[2], x[l + 2], acc);
-      acc = fmaf(a4[3], x[l + 3], acc);
+      for (int m = 0; m < r; m += 4) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sAr[row * LDA + 16 * bi + m]);
+        acc = fmaf(a4[0], x[m], acc);
+        acc = fmaf(a4[1], x[m + 1], acc);
+        acc = fmaf(a4[2], x[m + 2], acc);
+        acc = fmaf(a4[3], x[m + 3], acc);
+      }
+      x[r] = (r == c ? 1.f : 0.f) - gb[GB_BETA + row] * acc;
     }
-    x[i] = (i == lane ? 1.f : 0.f) - gb[GB_BETA + i] * acc;
-  }
 #pragma unroll
-  for (int i = 0; i < C; ++i) sTm[i * LDC + lane] = f32_to_bf16_bits(x[i]);
+    for (int r = 0; r < 16; ++r) {
+      const int row = 16 * bi + r;
+      sT[row * LDA + 16 * bi + c] = x[r];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        if (jb != bi) sTm[row * LDC + 16 * jb + c] = 0;
+      sTm[row * LDC + 16 * bi + c] = f32_to_bf16_bits(x[r]);
+    }
+  }
+  const int q = lane >> 4;
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+#pragma unroll
+    for (int j = i - 1; j >= 0; --j) {
+      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      const float be = gb[GB_BETA + 16 * i + c];
+#pragma unroll
+      for (int m = j; m < i; ++m)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const float a = be * sAr[(16 * i + c) * LDA + 16 * m + 4 * s4 + q];
+          const float b = sT[(16 * m + 4 * s4 + q) * LDA + 16 * j + c];
+          z = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, z, 0, 0, 0);
+        }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sZ[(4 * q + e) * 17 + c] = z[e];
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float a = sT[(16 * i + c) * LDA + 16 * i + 4 * s4 + q];
+        const float b = sZ[(4 * s4 + q) * 17 + c];
+        t = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, t, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * i + 4 * q + e;
+        sT[row * LDA + 16 * j + c] = -t[e];
+        sTm[row * LDC + 16 * j + c] = f32_to_bf16_bits(-t[e]);
+      }
+    }
+  }
 }
 
 // Decayed, masked K K^T (strict: Ar, fp32) or scaled Q K^T (inclusive: P,
@@ -229,6 +304,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
   __shared__ __align__(16) float sAr[C * LDA];    // Ar; then -G1 (bf16 [64][LDK])
   __shared__ __align__(16) uint16_t sP[kTB];
   __shared__ __align__(16) uint16_t sTm[kTB];
+  __shared__ __align__(16) float sT[C * LDA];     // fp32 Tm blocks (the inverse's own)
+  __shared__ __align__(16) float sZ[16 * 17];
   __shared__ __align__(16) float gb[GB_SZ];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -244,9 +321,15 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
   const int len = min(C, slen - C * ci);
   const int hq = hv / (HV / HQ);
 
-  load_rows(sK, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid, kGradThreads);
-  load_rows(sQ, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid, kGradThreads);
-  load_rows(sdO, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid, kGradThreads);
+  {
+    uint4 wk[2], wq[2], wo[2];
+    rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+    rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+    rows_fetch(wo, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
+    rows_store(sK, wk, tid);
+    rows_store(sQ, wq, tid);
+    rows_store(sdO, wo, tid);
+  }
   for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
   for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
   if (wave == 0) chunk_gates(A_log, a, dt_bias, b, HV, hv, t0, len, lane, gb);
@@ -278,7 +361,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
 
   // Tm (wave 0) while waves 1-7 form G0 = P^T dO [t][v] over sK (K is done)
   if (wave == 0) {
-    unit_lower_inverse(sAr, gb, sTm, lane);
+    unit_lower_inverse(sAr, gb, sT, sZ, sTm, lane);
   } else {
     for (int x = wave - 1; x < 32; x += 7) {
       const int tb = x & 3, vb = x >> 2;
@@ -360,7 +443,7 @@ __global__ __launch_bounds__(kChainThreads, 1) void gdn_bwd_chain_kernel(
     const CuT* __restrict__ cu, int N, int T, int HV, int h_chunks, const char* __restrict__ mrec,
     const char* __restrict__ rrec, const float* __restrict__ d_ht, uint16_t* __restrict__ dh,
     float* __restrict__ dh0) {
-  __shared__ __align__(16) uint16_t sM[2][D * D];
+  __shared__ __align__(16) uint16_t sM[3][D * D];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = blockIdx.x / HV, hv = blockIdx.x - (blockIdx.x / HV) * HV;
@@ -380,11 +463,10 @@ __global__ __launch_bounds__(kChainThreads, 1) void gdn_bwd_chain_kernel(
   }
   int last = nc - 1;
   if (coff + last >= h_chunks) last = -1;     // records past h_chunks were not formed
-  // M of the next chunk is copied into the other LDS buffer (HBM -> LDS) while
-  // the current one is used; R of the next chunk is loaded into registers
-  // before the products that consume the current one.
+  // M is copied HBM -> LDS and R loaded into registers two chunks ahead: three
+  // LDS buffers for M and three register sets for R, rotated by unrolling the
+  // chunk loop by three.
   constexpr int kMCopies = int(kMBytes / 16) / kChainThreads;
-  f32x4 rnext[8];
   auto rec_of = [&](int ch) { return size_t(coff + ch) * HV + hv; };
   auto copy_m = [&](int ch, int buf) {
     const char* ms = mrec + rec_of(ch) * kMBytes;
@@ -393,22 +475,20 @@ __global__ __launch_bounds__(kChainThreads, 1) void gdn_bwd_chain_kernel(
       lds_dma16_saddr(ms, uint32_t((x * kChainThreads + tid) * 16),
                       &sM[buf][(x * kChainThreads + wave * 64) * 8]);
   };
-  auto fetch_r = [&](int ch) {
+  auto fetch_r = [&](int ch, f32x4 (&r)[8]) {
     const char* rs = rrec + rec_of(ch) * kRBytes;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
-      rnext[kt] = *reinterpret_cast<const f32x4*>(rs + ((wave * 8 + kt) * 64 + lane) * 16);
+      r[kt] = *reinterpret_cast<const f32x4*>(rs + ((wave * 8 + kt) * 64 + lane) * 16);
   };
-  if (last >= 0) {
-    copy_m(last, 0);
-    fetch_r(last);
-  }
-  wait_vm<0>();
-  __syncthreads();
-  for (int ch = last, it = 0; ch >= 0; --ch, ++it) {
-    const int buf = it & 1;
-    if (ch > 0) copy_m(ch - 1, buf ^ 1);
-    // dSn of this chunk
+  // one chunk: dSn out, dS = dSn M + R (cur = R of chunk ch), and the copies
+  // for chunk ch - 2 (R into nxt2, M into LDS buffer (it + 2) % 3)
+  auto step = [&](int ch, int it, f32x4 (&cur)[8], f32x4 (&nxt2)[8]) {
+    const int buf = it % 3;
+    if (ch > 1) {
+      copy_m(ch - 2, (it + 2) % 3);
+      fetch_r(ch - 2, nxt2);
+    }
     uint16_t* hd = dh + rec_of(ch) * D * D;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
@@ -421,16 +501,34 @@ __global__ __launch_bounds__(kChainThreads, 1) void gdn_bwd_chain_kernel(
 #pragma unroll
     for (int s = 0; s < 4; ++s) bop[s] = pack2_bf(acc[2 * s], acc[2 * s + 1]);
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) acc[kt] = rnext[kt];
-    if (ch > 0) fetch_r(ch - 1);
-#pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
+      acc[kt] = cur[kt];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         acc[kt] = mfma16_bf(ld16_bf(&sM[buf][((kt * 4 + s) * 64 + lane) * 8]), bop[s], acc[kt]);
     }
-    wait_vm<0>();
+    // Vector memory operations complete in issue order: with at most this
+    // chunk's copies (M and R two chunks ahead) and its 8 dSn stores still
+    // outstanding, everything the next chunk reads has landed.
+    if (ch > 1) wait_vm<kMCopies + 8 + 8>();
+    else wait_vm<8>();
     __syncthreads();
+  };
+  f32x4 r0[8], r1[8], r2[8];
+  if (last >= 0) {
+    copy_m(last, 0);
+    fetch_r(last, r0);
+    if (last > 0) {
+      copy_m(last - 1, 1);
+      fetch_r(last - 1, r1);
+    }
+  }
+  wait_vm<0>();
+  __syncthreads();
+  for (int ch = last, it = 0; ch >= 0; ch -= 3, it += 3) {
+    step(ch, it, r0, r2);
+    if (ch >= 1) step(ch - 1, it + 1, r1, r0);
+    if (ch >= 2) step(ch - 2, it + 2, r2, r1);
   }
   if (dh0) {
 #pragma unroll
@@ -495,10 +593,11 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   const uint16_t* Sg = h + rec;
   const uint16_t* dSg = dh + rec;
 
-  load_rows(sK, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid, kGradThreads);
-  load_rows(sQ, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid, kGradThreads);
-  load_rows(sdO, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid, kGradThreads);
-  load_rows(sX, v + size_t(hv) * D, size_t(HV) * D, t0, len, tid, kGradThreads);
+  uint4 wk[2], wq[2], wo[2], wv[2];
+  rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+  rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+  rows_fetch(wo, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
+  rows_fetch(wv, v + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
   for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
   for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
   if (wave == 0) chunk_gates(A_log, a, dt_bias, b, HV, hv, t0, len, lane, gb);
@@ -523,6 +622,10 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
     if (lane == 0) pt.dot[wave] = part;
   }
+  rows_store(sK, wk, tid);
+  rows_store(sQ, wq, tid);
+  rows_store(sdO, wo, tid);
+  rows_store(sX, wv, tid);
   __syncthreads();
 
   ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
@@ -531,7 +634,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   const int tb = wave & 3, d0 = 4 * (wave >> 2);
   const int ib = wave >> 1, j0 = 2 * (wave & 1);
   f32x4 eks[4], xr[4], kds[4];
-  if (wave == 0) unit_lower_inverse(sAr, gb, sTm, lane);
+  // the inverse's fp32 blocks over sVn, its staging over sY (both unused until later)
+  if (wave == 0) unit_lower_inverse(sAr, gb, reinterpret_cast<float*>(sVn), reinterpret_cast<float*>(sY), sTm, lane);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int db = d0 + u;
@@ -643,6 +747,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   __syncthreads();
 
   // dA = -Tm^T Y (strictly lower), dP = dO Vn^T (inclusive lower): their dbeta / dgam terms
+  uint4 wst[4];
+  state_fetch(wst, Sg, tid);
   f32x4 dab[2], dpm[2];
   {
     float rg[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f};
@@ -695,13 +801,12 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     st_tile(sTm, LDC, 16 * ib, 16 * (j0 + u), dpm[u], lane);
   }
   // S -> LDS [v][LDK] over dVn and Ar (both read for the last time above)
-  for (int x = tid; x < D * 16; x += kGradThreads) {
-    const int r = x >> 4, cc = (x & 15) * 8;
-    *reinterpret_cast<uint4*>(&sS[r * LDK + cc]) = *reinterpret_cast<const uint4*>(Sg + r * D + cc);
-  }
+  state_store(sS, wst, tid);
   __syncthreads();
 
   // dQ = scale E dO S + dPm K;  dK (all but the dSn term) = -beta E dX S + dPm^T Q + dAb K + dAb^T K
+  uint4 wds[4];
+  state_fetch(wds, dSg, tid);
   f32x4 dkp[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -739,10 +844,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     dkp[u] = z;
   }
   __syncthreads();
-  for (int x = tid; x < D * 16; x += kGradThreads) {
-    const int r = x >> 4, cc = (x & 15) * 8;
-    *reinterpret_cast<uint4*>(&sS[r * LDK + cc]) = *reinterpret_cast<const uint4*>(dSg + r * D + cc);
-  }
+  state_store(sS, wds, tid);
   __syncthreads();
 
   // dK += Dc Vn dSn
@@ -795,19 +897,18 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
 }
 
 // dq / dk of the v-heads sharing a qk-head: out[t][hq] = sum_m ws[t][hq G + m].
+// Grid (ceil(HQ * 32 / 256), T): thread x of row t takes float4 x of out[t].
 __global__ __launch_bounds__(256) void gdn_bwd_head_sum_kernel(const float* __restrict__ ws,
                                                                float* __restrict__ out, int T, int HQ,
                                                                int G) {
-  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;     // float4 index of out
-  const size_t total = size_t(T) * HQ * (D / 4);
-  if (i >= total) return;
-  const size_t t = i / (size_t(HQ) * (D / 4));
-  const size_t rem = i - t * size_t(HQ) * (D / 4);
-  const size_t hq = rem / (D / 4), d4 = rem - hq * (D / 4);
-  const f32x4* src = reinterpret_cast<const f32x4*>(ws) + ((t * HQ + hq) * G) * (D / 4) + d4;
+  const int x = blockIdx.x * 256 + threadIdx.x;
+  if (x >= HQ * (D / 4)) return;
+  const int hq = x / (D / 4), d4 = x - hq * (D / 4);
+  const size_t t = blockIdx.y;
+  const f32x4* src = reinterpret_cast<const f32x4*>(ws) + (t * HQ + hq) * G * (D / 4) + d4;
   f32x4 acc = src[0];
-  for (int m = 1; m < G; ++m) acc += src[size_t(m) * (D / 4)];
-  reinterpret_cast<f32x4*>(out)[i] = acc;
+  for (int m = 1; m < G; ++m) acc += src[m * (D / 4)];
+  reinterpret_cast<f32x4*>(out)[t * HQ * (D / 4) + x] = acc;
 }
 
 // Gradients of the gating, per v-head (one workgroup each):
@@ -873,10 +974,9 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
                        dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h, h_chunks, dhr,
                        G > 1 ? dq_ws : dq, G > 1 ? dk_ws : dk, dv, dg, dbeta);
     if (G > 1) {
-      const size_t n4 = size_t(T) * HQ * (D / 4);
-      const unsigned blocks = unsigned((n4 + 255) / 256);
-      hipLaunchKernelGGL(gdn_bwd_head_sum_kernel, dim3(blocks), dim3(256), 0, st, dq_ws, dq, T, HQ, G);
-      hipLaunchKernelGGL(gdn_bwd_head_sum_kernel, dim3(blocks), dim3(256), 0, st, dk_ws, dk, T, HQ, G);
+      const dim3 sgrid{unsigned((HQ * (D / 4) + 255) / 256), unsigned(T), 1u};
+      hipLaunchKernelGGL(gdn_bwd_head_sum_kernel, sgrid, dim3(256), 0, st, dq_ws, dq, T, HQ, G);
+      hipLaunchKernelGGL(gdn_bwd_head_sum_kernel, sgrid, dim3(256), 0, st, dk_ws, dk, T, HQ, G);
     }
   }
   const hipError_t e = hipGetLastError();
