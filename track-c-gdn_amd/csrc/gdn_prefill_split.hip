@@ -26,6 +26,7 @@
 // (gdn_prefill.hip): bf16 MFMA for A and P from the exact bf16 rows, fp16
 // operands on the state path, bf16 S for Q S^T, fp32 accumulation.
 
+#include <algorithm>
 #include <mutex>
 
 #include "gdn_prefill_common.h"
@@ -98,49 +99,108 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
   __shared__ __align__(16) float gd[GSZ];
   __shared__ __align__(16) float nrm[2 * C];
 
-  const int slot = blockIdx.x, hv = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
-  int n, ci;
-  locate_chunk(cu_seqlens, N, T, slot, lane, n, ci);
-  if (n < 0) return;
-  int bos, len;
-  seq_bounds(cu_seqlens, n, T, bos, len);
-  const int t0 = bos + ci * C;
-  const int L = min(C, len - ci * C);
-  const int hq = hv / (HV / HQ);
   const size_t qk_stride = size_t(HQ) * D;
-  char* rec = blob + (size_t(slot) * HV + hv) * kBlob;
+  const int heads_per_qk = HV / HQ;
 
   // The upper 16x16 tiles inside the diagonal 32x32 blocks of Tm and P are
-  // part of the fragments and must be zero.
+  // part of the fragments and must be zero; nothing else writes them.
   for (int e = tid; e < 2 * 16 * 16; e += kPrepThreads) {
     const int blk = e >> 8, r = (e >> 4) & 15, cc = e & 15;
     const int R0 = 32 * blk + r, pc = p32(32 * blk + 16 + cc);
     sTm[R0 * TLD + pc] = (_Float16)0.f;
     sP[R0 * TLD + pc] = (_Float16)0.f;
   }
-  // Raw rows: 16 threads per row, one 16-byte piece each, into swizzled slots.
-#pragma unroll
-  for (int j = 0; j < (C * D / 8) / kPrepThreads; ++j) {
-    const int item = tid + kPrepThreads * j;
-    const int row = item >> 4, pc = item & 15;
-    const size_t src = size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * pc;
-    const uint4 kv = *reinterpret_cast<const uint4*>(k + src);
-    const uint4 qv = *reinterpret_cast<const uint4*>(q + src);
-    *reinterpret_cast<uint4*>(&rk[raw_off(row, 8 * pc)]) = kv;
-    *reinterpret_cast<uint4*>(&rq[raw_off(row, 8 * pc)]) = qv;
+
+  // Persistent workgroups: unit u = (slot u / HV, v-head u % HV), this
+  // workgroup taking u = blockIdx.x, + gridDim.x, ...  The raw K / Q rows and
+  // the gate inputs of the next unit are loaded into registers while the
+  // current one is processed.  Slots past the last chunk end the walk (a
+  // later unit has a later or equal slot).
+  const int n_units = n_slots * HV;
+  struct Unit { int slot, hv, t0, L; };
+  auto locate = [&](int u, Unit& x) {
+    x.slot = u / HV;
+    x.hv = u - x.slot * HV;
+    int n, ci;
+    locate_chunk(cu_seqlens, N, T, x.slot, lane, n, ci);
+    if (n < 0) return false;
+    int bos, len;
+    seq_bounds(cu_seqlens, n, T, bos, len);
+    x.t0 = bos + ci * C;
+    x.L = min(C, len - ci * C);
+    return true;
+  };
+  constexpr int kRowLoads = (C * D / 8) / kPrepThreads;
+  static_assert(kRowLoads == 4, "four 16-byte row pieces per thread");
+  uint4 pk0, pk1, pk2, pk3, pq0, pq1, pq2, pq3;
+  uint16_t pa = 0, pb = 0;
+  float pdt = 0.f, pal = 0.f;
+  auto fetch = [&](const Unit& x) {
+    const int hq_ = x.hv / heads_per_qk;
+    auto src = [&](int j) {
+      const int item = tid + kPrepThreads * j;
+      const int row = item >> 4, pc = item & 15;
+      return size_t(x.t0 + min(row, x.L - 1)) * qk_stride + size_t(hq_) * D + 8 * pc;
+    };
+    pk0 = *reinterpret_cast<const uint4*>(k + src(0));
+    pq0 = *reinterpret_cast<const uint4*>(q + src(0));
+    pk1 = *reinterpret_cast<const uint4*>(k + src(1));
+    pq1 = *reinterpret_cast<const uint4*>(q + src(1));
+    pk2 = *reinterpret_cast<const uint4*>(k + src(2));
+    pq2 = *reinterpret_cast<const uint4*>(q + src(2));
+    pk3 = *reinterpret_cast<const uint4*>(k + src(3));
+    pq3 = *reinterpret_cast<const uint4*>(q + src(3));
+    if (wave == 0) {
+      const size_t gi = size_t(x.t0 + min(lane, x.L - 1)) * HV + x.hv;
+      pa = a[gi];
+      pb = b[gi];
+      pdt = dt_bias[x.hv];
+      pal = A_log[x.hv];
+    }
+  };
+  int u = blockIdx.x;
+  Unit cur;
+  if (u >= n_units || !locate(u, cur)) return;
+  fetch(cur);
+  for (;;) {
+  const int slot = cur.slot, hv = cur.hv;
+  const int t0 = cur.t0, L = cur.L;
+  const int hq = hv / heads_per_qk;
+  char* rec = blob + (size_t(slot) * HV + hv) * kBlob;
+
+  // Raw rows (loaded a unit ahead): 16 threads per row, one 16-byte piece
+  // each, into swizzled slots.
+  {
+    auto put = [&](int j, const uint4& wk, const uint4& wq) {
+      const int item = tid + kPrepThreads * j;
+      const int row = item >> 4, pc = item & 15;
+      *reinterpret_cast<uint4*>(&rk[raw_off(row, 8 * pc)]) = wk;
+      *reinterpret_cast<uint4*>(&rq[raw_off(row, 8 * pc)]) = wq;
+    };
+    put(0, pk0, pq0);
+    put(1, pk1, pq1);
+    put(2, pk2, pq2);
+    put(3, pk3, pq3);
   }
+  const uint16_t ua = pa, ub = pb;
+  const float udt = pdt, ual = pal;
+  // the next unit's loads, in flight while this one is processed
+  Unit nxt;
+  const int un = u + int(gridDim.x);
+  const bool has_next = un < n_units && locate(un, nxt);
+  if (has_next) fetch(nxt);
+
   // Gates of the chunk's tokens (reference PRE:1706-1722 and the chunk-local
   // cumsum of PRE:1721): lane = token.
   if (wave == 0) {
     constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
-    const size_t gi = size_t(t0 + min(lane, L - 1)) * HV + hv;
-    const float xa = bf16_bits_to_f32(a[gi]) + dt_bias[hv];
-    const float xb = bf16_bits_to_f32(b[gi]);
-    const float a_log_exp = expf(A_log[hv]);
+    const float xa = bf16_bits_to_f32(ua) + udt;
+    const float xb = bf16_bits_to_f32(ub);
+    const float a_log_exp = expf(ual);
     float ld = 0.f, bt = 0.f;
     if (lane < L) {
       // softplus(x) = max(x, 0) + ln(1 + e^-|x|); sigmoid(y) = 1 / (1 + e^-y)
@@ -350,6 +410,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
     const int j = wave;
     const int off = j < 2 ? (16 * j + c) * TLD + 8 * g : (16 * j + c) * TLD + 32 + 8 * g;
     put_frag(BL_TM + j * kFrag, ld16(&sTm[off]));
+  }
+  __syncthreads();      // LDS of this unit read; the next unit overwrites it
+  if (!has_next) break;
+  u = un;
+  cur = nxt;
   }
 }
 
@@ -720,6 +785,8 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   }
 }
 
+int device_cu_count();
+
 template <typename CuT, bool kL2>
 int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                    const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
@@ -727,7 +794,11 @@ int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
                    float* final_state, int slices, char* ws, hipStream_t st) {
   const int nt_bound = T / C + N;
   if (nt_bound > 0) {
-    hipLaunchKernelGGL((gdn_prefill_prep_kernel<CuT, kL2>), dim3(nt_bound, HV), dim3(kPrepThreads), 0,
+    // persistent workgroups, two per CU (75.5 KB of LDS each)
+    const long long units = (long long)nt_bound * HV;
+    const int cus = device_cu_count();
+    const long long wgs = std::min<long long>(units, 2LL * (cus > 0 ? cus : 256));
+    hipLaunchKernelGGL((gdn_prefill_prep_kernel<CuT, kL2>), dim3(unsigned(wgs)), dim3(kPrepThreads), 0,
                        st, q, k, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale, ws, nt_bound);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return -int(e);
