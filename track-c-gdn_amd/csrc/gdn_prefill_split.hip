@@ -420,21 +420,23 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
 
 // ---------------------------------------------------------------------------
 // State slice of one chain: R = 16 NRG state rows per workgroup.  Each group
-// of 16 rows is carried by two waves that both hold those rows of S:
-//   state wave  : KS = K S^T;  X = beta (V - e^gam KS);  Vn_top = T_a X_top,
+// of 16 rows has a state wave and an output wave:
+//   state wave  : X = beta (V - e^gam KS);  Vn_top = T_a X_top,
 //                 Vn_bot = T_b (X_bot - A_ba Vn_top);  Vd = e^{gam_L - gam} Vn
-//                 -> Vn and Vd to LDS
-//   output wave : O^T = scale e^gam S Q^T, then (Vn from LDS) + Vn^T P^T,
-//                 stored as bf16 rows
-//   both        : S <- e^{gam_L} S + K^T Vd (the same operations in the same
-//                 order, so the two copies of S stay equal bit for bit)
+//                 -> Vn to LDS;  S <- e^{gam_L} S + K^T Vd;  the new S as a bf16
+//                 operand image to LDS;  KS = K S^T of the next chunk
+//   output wave : O^T = scale e^gam S Q^T (S from the bf16 image), then (Vn
+//                 from LDS) + Vn^T P^T, stored as bf16 rows
 // and one copy wave stages, by HBM -> LDS copies issued two chunks ahead into
 // three buffers each, the raw Q rows, the slice's V columns, the chunk's fp16
 // K image and its gate data.  The Tm, A_ba and P fragments of the chunk's
 // workspace record go straight into the registers of the waves that use
 // them, also two chunks ahead.  Two LDS barriers per chunk: after Vn is in
-// LDS, and at the end of the chunk.  State waves 0 .. NRG-1 and output waves
-// NRG .. 2 NRG - 1 land on different SIMDs pairwise.
+// LDS (by then the next chunk's copies have landed), and at the end of the
+// chunk.  After the first, the state wave updates S and forms the next
+// chunk's K S^T while the output wave finishes this chunk's rows, so the
+// next chunk's X does not wait for the update.  State waves 0 .. NRG-1 and
+// output waves NRG .. 2 NRG - 1 land on different SIMDs pairwise.
 template <int NRG>
 struct SliceCfg {
   static constexpr int R = 16 * NRG;            // state rows per workgroup
@@ -444,8 +446,12 @@ struct SliceCfg {
   static constexpr int kCopies = 16 + VS + kKcCopies + kGateCopies;   // copy instructions per chunk
   // LDS buffer sets (copies are issued kNB - 1 chunks ahead)
   static constexpr int kNB = NRG == 1 ? 4 : 3;
-  // chunks ahead that the record fragments are loaded (24 VGPRs a chunk)
-  static constexpr int kAhead = kNB - 1;
+  // chunks ahead that the record fragments are loaded (24 VGPRs a chunk),
+  // and the register ring they rotate through (kNB is a multiple of it, so
+  // the ring slot of a chunk follows from its LDS buffer set)
+  static constexpr int kAhead = NRG == 1 ? 1 : kNB - 1;
+  static constexpr int kFrRing = kAhead + 1;
+  static_assert(kNB % kFrRing == 0, "ring slot from the buffer set");
 };
 
 template <typename CuT, bool kL2, int NRG>
@@ -462,7 +468,10 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   __shared__ __align__(16) uint16_t rq[NB][C * D];
   __shared__ __align__(16) uint16_t rv[NB][C * R];
   __shared__ __align__(16) char gt[NB][kGateBytes];
-  __shared__ __align__(16) f16x8 xch[NRG][4][64];   // Vn (2 fragments) and Vd (2) per row group
+  __shared__ __align__(16) f16x8 xch[NRG][2][64];   // Vn (2 fragments) per row group
+  // bf16 operand image of each row group's state (the output waves' S Q^T),
+  // written by the state wave after its update
+  __shared__ __align__(16) bf16x8_t sSb[NRG][4][64];
 
   // Workgroup -> (unit = (sequence, qk-head), member m, slice s).  The G * S
   // workgroups of one unit read the same K, Q and (per member) records; they
@@ -505,12 +514,14 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
                                        : h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb)
-      Sacc[kb] = h0row ? *reinterpret_cast<const f32x4*>(h0row + 16 * kb + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+      Sacc[kb] = (h0row && !out_role) ? *reinterpret_cast<const f32x4*>(h0row + 16 * kb + 4 * g)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
     // Fragments of the chunk's record this wave multiplies with (state: T_a,
     // T_b, -A_ba; output: P), loaded kAhead chunks ahead.
     constexpr int kAhead = Cfg::kAhead;
     const int frag_base = out_role ? BL_P : BL_TM;
-    f16x8 fr[NB][6];
+    constexpr int FR = Cfg::kFrRing;
+    f16x8 fr[FR][6];
     auto load_frags = [&](int ch, f16x8 (&dst)[6]) {
       const char* rec = record(ch) + frag_base + 16 * lane;
 #pragma unroll
@@ -525,7 +536,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
     const int q_lane = c * D + 4 * (g & 1);
 
     // State update with the chunk's K^T fragments (transposing reads, a
-    // k-block ahead) and Vd (both waves of a row group, identical operations).
+    // k-block ahead) and Vd (state waves).
     auto update = [&](const _Float16* kc, float egL, const f16x8 (&vd)[2]) {
       auto load_kt = [&](int kb, f16x8 (&dst)[2]) {
         const int kq = p32(16 * kb + 4 * (c & 3));
@@ -537,19 +548,45 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           dst[p] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
       };
-      f16x8 fa[2][2];
+      f16x8 fa[3][2];
       load_kt(0, fa[0]);
+      load_kt(1, fa[1]);
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb) {
-        if (kb + 1 < 8) load_kt(kb + 1, fa[(kb + 1) & 1]);
+        if (kb + 2 < 8) load_kt(kb + 2, fa[(kb + 2) % 3]);
 #pragma unroll
-        for (int p = 0; p < 2; ++p) asm volatile("" : "+v"(fa[kb & 1][p]));
+        for (int p = 0; p < 2; ++p) asm volatile("" : "+v"(fa[kb % 3][p]));
         Sacc[kb] *= egL;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) Sacc[kb] = mfma16(fa[kb & 1][p], vd[p], Sacc[kb]);
+        for (int p = 0; p < 2; ++p) Sacc[kb] = mfma16(fa[kb % 3][p], vd[p], Sacc[kb]);
       }
     };
 
+    // K S^T with the rows of S this wave holds (fp16 operands: the fp16 K
+    // image, S packed from the accumulators), K fragments a column block ahead.
+    f32x4 KS[4];
+    auto ks_of = [&](const _Float16* kcb, f32x4 (&ks_out)[4]) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) ks_out[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      f16x8 kf[3][4];                         // K rows 16 tb + c, p32 positions 32 p + 8 g ..
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) kf[p][tb] = ld16(&kcb[(16 * tb + c) * KCLD + 32 * p + 8 * g]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        if (p + 2 < 4) {
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) kf[(p + 2) % 3][tb] = ld16(&kcb[(16 * tb + c) * KCLD + 32 * (p + 2) + 8 * g]);
+        }
+        const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          asm volatile("" : "+v"(kf[p % 3][tb]));
+          ks_out[tb] = mfma16(kf[p % 3][tb], sb, ks_out[tb]);
+        }
+      }
+    };
     // One chunk; b3c (0, 1, 2) is the buffer set as a compile-time constant,
     // so every LDS address is a loop-invariant lane offset plus an immediate.
     auto chunk = [&](auto b3c, int ch) {
@@ -558,28 +595,11 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
       const float* gd = reinterpret_cast<const float*>(gt[b3]);
       const _Float16* kc = Kc[b3];
       const float egL = gd[G_EG + L - 1];
-      if (ch + kAhead < n_chunks) load_frags(ch + kAhead, fr[(b3 + kAhead) % NB]);
+      if (ch + kAhead < n_chunks) load_frags(ch + kAhead, fr[(b3 + kAhead) % FR]);
       if (!out_role) {
-        // ---- K S^T (the state before this chunk), K fragments a column block ahead
-        f32x4 KS[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) KS[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        f16x8 kf[2][4];                         // K rows 16 tb + c, p32 positions 32 p + 8 g ..
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) kf[0][tb] = ld16(&kc[(16 * tb + c) * KCLD + 8 * g]);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          if (p + 1 < 4) {
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) kf[(p + 1) & 1][tb] = ld16(&kc[(16 * tb + c) * KCLD + 32 * (p + 1) + 8 * g]);
-          }
-          const f16x8 sb = pack2(Sacc[2 * p], Sacc[2 * p + 1]);
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) {
-            asm volatile("" : "+v"(kf[p & 1][tb]));
-            KS[tb] = mfma16(kf[p & 1][tb], sb, KS[tb]);
-          }
-        }
+        // K S^T of this chunk was formed at the end of the chunk before (the
+        // first chunk's here)
+        if (ch == 0) ks_of(kc, KS);
         // ---- X = beta (V - e^gam K S^T).  V[16 tb + 4 g + i][v0 + c] by one
         //      transposing read per tb: lane 4 mm + j reads columns vl + 4 j
         //      .. +3 of row 16 tb + 4 g + mm.
@@ -601,7 +621,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
         // ---- Vn = Tm X in 32-row blocks: Vn_top = T_a X_top, Vn_bot = T_b (X_bot - A_ba Vn_top)
         f16x8 vd[2];
         {
-          const f16x8* tf = fr[b3];             // T_a rows 0-15, 16-31; T_b rows 32-47, 48-63; -A_ba
+          const f16x8* tf = fr[b3 % FR];        // T_a rows 0-15, 16-31; T_b rows 32-47, 48-63; -A_ba
           f32x4 ed[4];
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) ed[tb] = *reinterpret_cast<const f32x4*>(&gd[G_ED + 16 * tb + 4 * g]);
@@ -621,11 +641,13 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           vd[1] = pack2(Vn[2] * ed[2], Vn[3] * ed[3]);
           xch[r][0][lane] = vn0;
           xch[r][1][lane] = vn1;
-          xch[r][2][lane] = vd[0];
-          xch[r][3][lane] = vd[1];
         }
-        lds_barrier();                          // Vn, Vd of every row group in LDS
+        lds_barrier();                          // Vn of every row group in LDS
         update(kc, egL, vd);
+        // the new state's bf16 image for the output wave, and K S^T of the next chunk
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sSb[r][p][lane] = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+        if (ch + 1 < n_chunks) ks_of(Kc[(b3 + 1) % NB], KS);
       } else {
         // ---- O^T = S Q^T (transposed output tile: lane (g, c) of OT[tb] holds
         //      token 16 tb + c, state rows v0 + 4 g .. +3)
@@ -646,7 +668,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           if (p + 1 < 4) load_q(p + 1, qf[(p + 1) & 1]);
-          const bf16x8_t sbf = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+          const bf16x8_t sbf = sSb[r][p][lane];
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
             asm volatile("" : "+v"(qf[p & 1][tb]));
@@ -660,14 +682,12 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           OT[tb] *= egs;
         }
         lds_barrier();                          // Vn, Vd of every row group in LDS
-        f16x8 vn[2], vd[2];
+        f16x8 vn[2];
         vn[0] = xch[r][0][lane];
         vn[1] = xch[r][1][lane];
-        vd[0] = xch[r][2][lane];
-        vd[1] = xch[r][3][lane];
         // ---- + Vn^T P^T, then the rows to HBM
         {
-          const f16x8* pf = fr[b3];             // P (token block, column block) 00 10 20 21 30 31
+          const f16x8* pf = fr[b3 % FR];        // P (token block, column block) 00 10 20 21 30 31
           constexpr int kPt[6] = {0, 1, 2, 2, 3, 3}, kPp[6] = {0, 0, 0, 1, 0, 1};
 #pragma unroll
           for (int f = 0; f < 6; ++f) OT[kPt[f]] = mfma16(vn[kPp[f]], pf[f], OT[kPt[f]]);
@@ -680,11 +700,14 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
                   uint2{cvt_pk_bf16(OT[tb][0], OT[tb][1]), cvt_pk_bf16(OT[tb][2], OT[tb][3])};
           }
         }
-        update(kc, egL, vd);
       }
       lds_barrier();                            // chunk ch+1 staged; buffers of ch free
     };
-    if (n_chunks > 0) lds_barrier();            // chunk 0 staged
+    if (!out_role) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) sSb[r][p][lane] = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+    }
+    if (n_chunks > 0) lds_barrier();            // chunk 0 staged, the initial state's image written
     for (int ch = 0; ch < n_chunks; ch += NB) {
       chunk(IC<0>{}, ch);
       if (ch + 1 < n_chunks) chunk(IC<1>{}, ch + 1);
@@ -778,8 +801,10 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
       // the chain reads chunk ch; copies(ch+1 .. ch+NB-2) are in flight,
       // copies(ch+NB-1) go into the buffers chunk ch-1 used
       if (ch + NB - 1 < n_chunks) issue_copies(ch + NB - 1);
+      // copies(ch+1) land before the middle barrier: the state waves form
+      // K S^T of chunk ch+1 after it
+      wait_ahead(min(n_chunks - 1, ch + NB - 1) - (ch + 1));
       lds_barrier();                            // Vn exchange of chunk ch
-      wait_ahead(min(n_chunks - 1, ch + NB - 1) - (ch + 1));   // copies(ch+1) landed
       lds_barrier();
     }
   }
