@@ -113,23 +113,39 @@ __device__ __forceinline__ float group4_sum(float x) {
 constexpr int GB_GAM = 0, GB_BETA = C, GB_E = 2 * C, GB_DC = 3 * C, GB_L = 4 * C, GB_EL = 4 * C + 1;
 constexpr int GB_SZ = 4 * C + 4;
 
-__device__ __forceinline__ void chunk_gates(const float* A_log, const uint16_t* a, const float* dt_bias,
-                            const uint16_t* b, int HV, int hv, int t0, int len, int lane, float* gb) {
+// The gate inputs of token `lane` of the chunk (wave 0): loaded early, used
+// by chunk_gates_calc once the chunk's rows are on their way.
+struct GateIn {
+  float a, b, dt, alog;
+};
+
+__device__ __forceinline__ GateIn gate_inputs(const float* A_log, const uint16_t* a, const float* dt_bias,
+                                              const uint16_t* b, int HV, int hv, int t0, int len, int lane) {
+  const size_t i = size_t(t0 + min(lane, len - 1)) * HV + hv;
+  return GateIn{bf16_bits_to_f32(a[i]), bf16_bits_to_f32(b[i]), dt_bias[hv], A_log[hv]};
+}
+
+// g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) per token (zero
+// past the chunk end), the chunk-local cumsum gam, e^gam and e^{gam_L - gam},
+// with the forward kernels' hardware exp2 / log2 forms.
+__device__ __forceinline__ void chunk_gates_calc(const GateIn& in, int len, int lane, float* gb) {
+  constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.69314718055994531f;
   float g = 0.f, be = 0.f;
   if (lane < len) {
-    const size_t i = size_t(t0 + lane) * HV + hv;
-    g = -expf(A_log[hv]) * softplus_stable(bf16_bits_to_f32(a[i]) + dt_bias[hv]);
-    be = sigmoidf_(bf16_bits_to_f32(b[i]));
+    const float x = in.a + in.dt;
+    const float sp = fmaxf(x, 0.f) + kLn2 * __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e));
+    g = -__builtin_amdgcn_exp2f(in.alog * kLog2e) * sp;
+    be = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-in.b * kLog2e));
   }
   const float gam = wave_inclusive_scan(g);
   const float gl = __shfl(gam, 63);
   gb[GB_GAM + lane] = gam;
   gb[GB_BETA + lane] = be;
-  gb[GB_E + lane] = expf(gam);
-  gb[GB_DC + lane] = expf(gl - gam);
+  gb[GB_E + lane] = __builtin_amdgcn_exp2f(gam * kLog2e);
+  gb[GB_DC + lane] = __builtin_amdgcn_exp2f((gl - gam) * kLog2e);
   if (lane == 0) {
     gb[GB_L] = gl;
-    gb[GB_EL] = expf(gl);
+    gb[GB_EL] = __builtin_amdgcn_exp2f(gl * kLog2e);
   }
 }
 
@@ -322,17 +338,19 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
   const int hq = hv / (HV / HQ);
 
   {
+    GateIn gi{};
+    if (wave == 0) gi = gate_inputs(A_log, a, dt_bias, b, HV, hv, t0, len, lane);
     uint4 wk[2], wq[2], wo[2];
     rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
     rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
     rows_fetch(wo, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
+    for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
+    for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
     rows_store(sK, wk, tid);
     rows_store(sQ, wq, tid);
     rows_store(sdO, wo, tid);
+    if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
   }
-  for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
-  for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
-  if (wave == 0) chunk_gates(A_log, a, dt_bias, b, HV, hv, t0, len, lane, gb);
   __syncthreads();
 
   // Ar, P; the scaled row copies
@@ -593,6 +611,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   const uint16_t* Sg = h + rec;
   const uint16_t* dSg = dh + rec;
 
+  GateIn gi{};
+  if (wave == 0) gi = gate_inputs(A_log, a, dt_bias, b, HV, hv, t0, len, lane);
   uint4 wk[2], wq[2], wo[2], wv[2];
   rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
   rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
@@ -600,32 +620,11 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   rows_fetch(wv, v + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
   for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
   for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
-  if (wave == 0) chunk_gates(A_log, a, dt_bias, b, HV, hv, t0, len, lane, gb);
-  {
-    // <dSn, S>: 32 elements of each per thread
-    float part = 0.f;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int e = (x * kGradThreads + tid) * 8;
-      const uint4 sw = *reinterpret_cast<const uint4*>(Sg + e);
-      const uint4 dw = *reinterpret_cast<const uint4*>(dSg + e);
-      const uint32_t ss[4] = {sw.x, sw.y, sw.z, sw.w}, dd[4] = {dw.x, dw.y, dw.z, dw.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float s0, s1, d0, d1;
-        unpack_bf16x2(ss[j], s0, s1);
-        unpack_bf16x2(dd[j], d0, d1);
-        part = fmaf(s0, d0, fmaf(s1, d1, part));
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
-    if (lane == 0) pt.dot[wave] = part;
-  }
   rows_store(sK, wk, tid);
   rows_store(sQ, wq, tid);
   rows_store(sdO, wo, tid);
   rows_store(sX, wv, tid);
+  if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
   __syncthreads();
 
   ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
@@ -842,6 +841,27 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       z = mfma16_bf(op_rm(sdT, LDC, 16 * tb, 32 * s, lane), kop, z);
     }
     dkp[u] = z;
+  }
+  {
+    // <dSn, S>: this thread's 32 elements of S (in LDS) against those of dSn
+    float part = 0.f;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int x = tid + it * kGradThreads, r = x >> 4, cc = (x & 15) * 8;
+      const uint4 sw = *reinterpret_cast<const uint4*>(&sS[r * LDK + cc]);
+      const uint32_t ss[4] = {sw.x, sw.y, sw.z, sw.w};
+      const uint32_t dd[4] = {wds[it].x, wds[it].y, wds[it].z, wds[it].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float s0, s1, d0, d1;
+        unpack_bf16x2(ss[j], s0, s1);
+        unpack_bf16x2(dd[j], d0, d1);
+        part = fmaf(s0, d0, fmaf(s1, d1, part));
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+    if (lane == 0) pt.dot[wave] = part;
   }
   __syncthreads();
   state_store(sS, wds, tid);
