@@ -181,6 +181,28 @@ __device__ __forceinline__ void store_b128_saddr(char* base, uint32_t off, u32x4
                : "memory");
 }
 
+// Raw buffer resource (stride 0) over `bytes` bytes from `base`, both made
+// wave-uniform.  A buffer access whose offset is at or past `bytes` is out of
+// range: a store there writes nothing.  Such stores mask rows without a
+// branch, so every path through a loop issues the same memory instructions
+// and the compiler's vmcnt waits for earlier loads stay exact.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_buffer(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  void* p = reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, short(0), int(__builtin_amdgcn_readfirstlane(bytes)), 0x00020000);
+}
+
+// Offset that lands out of range of every buffer uniform_buffer makes.
+constexpr uint32_t kBufferDrop = 0x80000000u;
+
+__device__ __forceinline__ void buffer_store_b64(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t lo,
+                                                 uint32_t hi) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, r, int(off), 0, 0);
+}
+
 // Tokens [bos, bos + len) of sequence n, clamped into [0, T].
 template <typename CuT>
 __host__ __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {

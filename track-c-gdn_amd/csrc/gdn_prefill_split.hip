@@ -527,9 +527,12 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 #pragma unroll
       for (int f = 0; f < 6; ++f) dst[f] = *reinterpret_cast<const f16x8*>(rec + f * kFrag);
     };
+    // (the chunk index is clamped: every chunk issues the same loads)
+    const int last_ch = n_chunks - 1;
+    if (n_chunks > 0) {
 #pragma unroll
-    for (int a = 0; a < kAhead; ++a)
-      if (a < n_chunks) load_frags(a, fr[a]);
+      for (int a = 0; a < kAhead; ++a) load_frags(min(a, last_ch), fr[a]);
+    }
     // Per-lane element offsets of the two 4-column pieces of a Q fragment
     // (raw row 16 tb + c, columns 32 p + 4 g .. and 32 p + 16 + 4 g ..).
     const int sw = (g >> 1) ^ c;
@@ -589,17 +592,16 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
     };
     // One chunk; b3c (0, 1, 2) is the buffer set as a compile-time constant,
     // so every LDS address is a loop-invariant lane offset plus an immediate.
-    auto chunk = [&](auto b3c, int ch) {
+    auto chunk = [&](auto b3c, auto rolec, int ch) __attribute__((always_inline)) {
       constexpr int b3 = decltype(b3c)::value;
+      constexpr bool kOut = decltype(rolec)::value != 0;
       const int L = chunk_len(ch);
       const float* gd = reinterpret_cast<const float*>(gt[b3]);
       const _Float16* kc = Kc[b3];
       const float egL = gd[G_EG + L - 1];
-      if (ch + kAhead < n_chunks) load_frags(ch + kAhead, fr[(b3 + kAhead) % FR]);
-      if (!out_role) {
-        // K S^T of this chunk was formed at the end of the chunk before (the
-        // first chunk's here)
-        if (ch == 0) ks_of(kc, KS);
+      load_frags(min(ch + kAhead, last_ch), fr[(b3 + kAhead) % FR]);
+      if constexpr (!kOut) {
+        // K S^T of this chunk was formed at the end of the chunk before
         // ---- X = beta (V - e^gam K S^T).  V[16 tb + 4 g + i][v0 + c] by one
         //      transposing read per tb: lane 4 mm + j reads columns vl + 4 j
         //      .. +3 of row 16 tb + 4 g + mm.
@@ -691,28 +693,47 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           constexpr int kPt[6] = {0, 1, 2, 2, 3, 3}, kPp[6] = {0, 0, 0, 1, 0, 1};
 #pragma unroll
           for (int f = 0; f < 6; ++f) OT[kPt[f]] = mfma16(vn[kPp[f]], pf[f], OT[kPt[f]]);
-          uint16_t* obase = out + size_t(bos + ch * C) * v_stride + size_t(hv) * D + v0 + 4 * g;
+          // the chunk's L rows as one buffer: stores of rows past L are dropped
+          const __amdgpu_buffer_rsrc_t orows =
+              uniform_buffer(out + size_t(bos + ch * C) * v_stride, uint32_t(L) * uint32_t(v_stride) * 2u);
+          const uint32_t ocol = uint32_t(hv * D + v0 + 4 * g) * 2u;
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
             const int t = 16 * tb + c;
-            if (t < L)
-              *reinterpret_cast<uint2*>(obase + size_t(t) * v_stride) =
-                  uint2{cvt_pk_bf16(OT[tb][0], OT[tb][1]), cvt_pk_bf16(OT[tb][2], OT[tb][3])};
+            buffer_store_b64(orows, t < L ? uint32_t(t) * uint32_t(v_stride) * 2u + ocol : kBufferDrop,
+                             cvt_pk_bf16(OT[tb][0], OT[tb][1]), cvt_pk_bf16(OT[tb][2], OT[tb][3]));
           }
         }
       }
       lds_barrier();                            // chunk ch+1 staged; buffers of ch free
     };
-    if (!out_role) {
+    // The chunk loop of one role.  Its body issues the same vector memory
+    // instructions on every path (clamped record loads; output rows as
+    // buffer stores), so the compiler's waits for the record fragments count
+    // exactly the loads issued after them instead of draining the queue;
+    // the last n_chunks % NB chunks run after the loop.
+    auto run = [&](auto rolec) __attribute__((always_inline)) {
+      constexpr bool kOut = decltype(rolec)::value != 0;
+      if constexpr (!kOut) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) sSb[r][p][lane] = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
-    }
-    if (n_chunks > 0) lds_barrier();            // chunk 0 staged, the initial state's image written
-    for (int ch = 0; ch < n_chunks; ch += NB) {
-      chunk(IC<0>{}, ch);
-      if (ch + 1 < n_chunks) chunk(IC<1>{}, ch + 1);
-      if (ch + 2 < n_chunks) chunk(IC<2>{}, ch + 2);
-      if (NB > 3 && ch + 3 < n_chunks) chunk(IC<(NB > 3 ? 3 : 0)>{}, ch + 3);
+        for (int p = 0; p < 4; ++p) sSb[r][p][lane] = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
+      }
+      lds_barrier();                            // chunk 0 staged, the initial state's image written
+      if constexpr (!kOut) ks_of(Kc[0], KS);
+      int ch = 0;
+      for (; ch + NB <= n_chunks; ch += NB) {
+        chunk(IC<0>{}, rolec, ch);
+        chunk(IC<1>{}, rolec, ch + 1);
+        chunk(IC<2>{}, rolec, ch + 2);
+        if constexpr (NB > 3) chunk(IC<(NB > 3 ? 3 : 0)>{}, rolec, ch + 3);
+      }
+      if (ch < n_chunks) chunk(IC<0>{}, rolec, ch);
+      if (ch + 1 < n_chunks) chunk(IC<1>{}, rolec, ch + 1);
+      if (NB > 3 && ch + 2 < n_chunks) chunk(IC<2>{}, rolec, ch + 2);
+    };
+    if (n_chunks > 0) {
+      if (out_role) run(IC<1>{});
+      else run(IC<0>{});
     }
     if (!out_role) {
       float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
