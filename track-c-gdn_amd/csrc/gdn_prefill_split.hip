@@ -61,6 +61,15 @@ constexpr int kGateBytes = kBlob - BL_G;
 constexpr int kGateCopies = (kGateBytes + kFrag - 1) / kFrag;
 
 constexpr int kPrepThreads = 256;
+// Batches of up to this many sequences have their slice workgroups ordered
+// longest sequence first (the preparation launch ranks the sequences).
+constexpr int kMaxOrdered = 4096;
+
+// The workspace: the (chunk, v-head) records, the fp16 K images of every
+// (chunk, qk-head), then the sequence order of the slice launch (N ints).
+__host__ __device__ inline size_t order_offset(int n_slots, int HQ, int HV) {
+  return size_t(n_slots) * (size_t(HV) * size_t(kBlob) + size_t(HQ) * size_t(kKcBytes));
+}
 
 // HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): from
 // base + off (base uniform, off a 32-bit lane offset) to LDS byte address
@@ -105,6 +114,26 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
   const int g = lane >> 4, c = lane & 15;
   const size_t qk_stride = size_t(HQ) * D;
   const int heads_per_qk = HV / HQ;
+
+  // order[r] = the sequence of rank r by descending length (ties: lower index
+  // first), read by the slice launch to start the longest chains first.
+  {
+    int* order = reinterpret_cast<int*>(blob + order_offset(n_slots, HQ, HV));
+    for (int n = blockIdx.x * kPrepThreads + tid; n < N; n += gridDim.x * kPrepThreads) {
+      int rank = n;
+      if (N <= kMaxOrdered) {
+        int b0, l0;
+        seq_bounds(cu_seqlens, n, T, b0, l0);
+        rank = 0;
+        for (int m = 0; m < N; ++m) {
+          int b1, l1;
+          seq_bounds(cu_seqlens, m, T, b1, l1);
+          rank += (l1 > l0 || (l1 == l0 && m < n)) ? 1 : 0;
+        }
+      }
+      order[rank] = n;
+    }
+  }
 
   // The upper 16x16 tiles inside the diagonal 32x32 blocks of Tm and P are
   // part of the fragments and must be zero; nothing else writes them.
@@ -476,15 +505,20 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   // Workgroup -> (unit = (sequence, qk-head), member m, slice s).  The G * S
   // workgroups of one unit read the same K, Q and (per member) records; they
   // get ids 8 apart, which puts them on one XCD (ids go round-robin over the
-  // 8 XCDs), so only the first read of each line goes to HBM.
+  // 8 XCDs), so only the first read of each line goes to HBM.  Units are
+  // taken longest sequence first (order[], from the preparation launch):
+  // unit position j of XCD x is sorted unit 8 j + x for even j and 8 j + 7 - x
+  // for odd j, which evens out the work per XCD, and the workgroups that wait
+  // for a CU land where the shortest of the first units ran.
   const int G = HV / HQ;
   const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
-  const int unit = 8 * (id_row / (G * S)) + xcd;
-  if (unit >= N * HQ) return;
-  const int within = id_row - (id_row / (G * S)) * (G * S);
+  const int jx = id_row / (G * S);
+  const int su = 8 * jx + ((jx & 1) ? 7 - xcd : xcd);
+  if (su >= N * HQ) return;
+  const int within = id_row - jx * (G * S);
   const int m = within / S, s = within - m * S;
-  const int n = unit / HQ;
-  const int hq = unit - n * HQ;
+  const int n = reinterpret_cast<const int*>(ws + order_offset(nt_bound, HQ, HV))[su / HQ];
+  const int hq = su - (su / HQ) * HQ;
   const int hv = hq * G + m;
   const int vb = R * s;                         // first state row of the slice
 
@@ -919,16 +953,17 @@ namespace gdn {
 
 size_t prefill_split_workspace_bytes(int N, int T, int HQ, int HV) {
   if (N <= 0 || T < 0 || HQ <= 0 || HV <= 0) return 0;
-  return size_t(T / C + N) * (size_t(HV) * size_t(kBlob) + size_t(HQ) * size_t(kKcBytes));
+  return order_offset(T / C + N, HQ, HV) + (size_t(N) * sizeof(int) + 255) / 256 * 256;
 }
 
 int prefill_split_auto_slices(int N, int HV) {
   const long long chains = (long long)N * HV;
   const int cus = device_cu_count();
   if (chains <= 0 || cus <= 0) return 0;
-  // 8 slices while they fit the CUs at once; 4 slices for up to two
-  // workgroups per CU (measured faster than one fused workgroup per chain at
-  // 128 chains on 256 CUs); past that the fused kernel.
+  // 8 slices while they fit the CUs at once; 4 slices while they fit in two
+  // rounds of one workgroup per CU (the longest chains first; measured faster
+  // than one fused workgroup per chain at 128 chains on 256 CUs); past that
+  // the fused kernel.
   if (chains * 8 <= cus) return 8;
   if (chains * 4 <= 2LL * cus) return 4;
   return 0;
