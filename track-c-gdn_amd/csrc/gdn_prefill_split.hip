@@ -456,23 +456,23 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
 //                 operand image to LDS;  KS = K S^T of the next chunk
 //   output wave : O^T = scale e^gam S Q^T (S from the bf16 image), then (Vn
 //                 from LDS) + Vn^T P^T, stored as bf16 rows
-// and one copy wave stages, by HBM -> LDS copies issued two chunks ahead into
-// three buffers each, the raw Q rows, the slice's V columns, the chunk's fp16
-// K image and its gate data.  The Tm, A_ba and P fragments of the chunk's
+// and two copy waves stage, by HBM -> LDS copies issued NB - 1 chunks ahead
+// into NB buffers each, the raw Q rows, the slice's V columns, the chunk's
+// fp16 K image and its gate data.  The Tm, A_ba and P fragments of the chunk's
 // workspace record go straight into the registers of the waves that use
 // them, also two chunks ahead.  Two LDS barriers per chunk: after Vn is in
 // LDS (by then the next chunk's copies have landed), and at the end of the
 // chunk.  After the first, the state wave updates S and forms the next
 // chunk's K S^T while the output wave finishes this chunk's rows, so the
 // next chunk's X does not wait for the update.  State waves 0 .. NRG-1 and
-// output waves NRG .. 2 NRG - 1 land on different SIMDs pairwise.
+// output waves NRG .. 2 NRG - 1 land on different SIMDs pairwise; the copy
+// waves are 2 NRG and 2 NRG + 1.
 template <int NRG>
 struct SliceCfg {
   static constexpr int R = 16 * NRG;            // state rows per workgroup
-  static constexpr int kThreads = 64 * (2 * NRG + 1);
+  static constexpr int kThreads = 64 * (2 * NRG + 2);
   static constexpr int VS = R / 8;              // 16-byte slots per V row
   static constexpr int VRows = 1024 / (2 * R);  // V rows per 1 KB copy instruction
-  static constexpr int kCopies = 16 + VS + kKcCopies + kGateCopies;   // copy instructions per chunk
   // LDS buffer sets (copies are issued kNB - 1 chunks ahead)
   static constexpr int kNB = NRG == 1 ? 4 : 3;
   // chunks ahead that the record fragments are loaded (24 VGPRs a chunk),
@@ -775,22 +775,14 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
       for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
     }
   } else {
-    // ======================= copy wave
+    // ======================= copy waves
+    // Copy wave 0 stages the raw Q rows and the gate data, copy wave 1 the fp16
+    // K image and the slice's V columns: about 20 copies a chunk each, so the
+    // NB - 1 chunks in flight stay within what one wave's vmcnt counts (63).
     // Per-lane byte offsets from a full chunk's first row: raw Q rows (4 rows
     // per instruction, lane l -> row 4 j + l / 16, slot l % 16 holding piece
     // (l % 16) ^ row) and V columns (lane l -> row VRows j + l / VS, slot
     // l % VS holding piece (l % VS) ^ (row % VS)).
-    uint32_t q_off[16], v_off[VS];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int row = 4 * j + (lane >> 4);
-      q_off[j] = uint32_t(row) * uint32_t(qk_stride * 2) + uint32_t((lane & 15) ^ (row & 15)) * 16u;
-    }
-#pragma unroll
-    for (int j = 0; j < VS; ++j) {
-      const int row = Cfg::VRows * j + lane / VS;
-      v_off[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane % VS) ^ (row & (VS - 1))) * 16u;
-    }
     const char* kc0 = ws + size_t(nt_bound) * HV * kBlob + (size_t(coff) * HQ + hq) * kKcBytes;
     const uint32_t lane16 = 16u * uint32_t(lane);
     // LDS byte address of a buffer, as a wave-uniform scalar.
@@ -798,70 +790,96 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
       return __builtin_amdgcn_readfirstlane(
           (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
     };
-    auto issue_copies = [&](int ch) {
-      const int t0 = bos + ch * C, L = chunk_len(ch);
-      const int b3 = ch % NB;
-      const uint32_t lq = lds_u32(rq[b3]), lv = lds_u32(rv[b3]);
-      if (L == C) {
-        const char* qb = reinterpret_cast<const char*>(q + size_t(t0) * qk_stride + size_t(hq) * D);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) dma16(qb, q_off[j], lq + uint32_t(kFrag * j));
-        const char* vbp = reinterpret_cast<const char*>(v + size_t(t0) * v_stride + size_t(hv) * D + vb);
-#pragma unroll
-        for (int j = 0; j < VS; ++j) dma16(vbp, v_off[j], lv + uint32_t(kFrag * j));
-      } else {
+    auto run_copies = [&](auto cwc) __attribute__((always_inline)) {
+      constexpr int CW = decltype(cwc)::value;
+      constexpr int kCopiesW = CW == 0 ? 16 + kGateCopies : kKcCopies + VS;   // copy instructions per chunk
+      static_assert(2 * kCopiesW <= 63 && (NB - 1) * kCopiesW <= 63, "copies in flight within vmcnt");
+      uint32_t q_off[16], v_off[VS];
+      if constexpr (CW == 0) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int row = 4 * j + (lane >> 4);
-          const int src_piece = (lane & 15) ^ (row & 15);
-          lds_dma16(q + size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_piece,
-                    &rq[b3][4 * j * D]);
+          q_off[j] = uint32_t(row) * uint32_t(qk_stride * 2) + uint32_t((lane & 15) ^ (row & 15)) * 16u;
         }
+      } else {
 #pragma unroll
         for (int j = 0; j < VS; ++j) {
           const int row = Cfg::VRows * j + lane / VS;
-          const int src_piece = (lane % VS) ^ (row & (VS - 1));
-          lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + vb + 8 * src_piece,
-                    &rv[b3][Cfg::VRows * j * R]);
+          v_off[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane % VS) ^ (row & (VS - 1))) * 16u;
         }
       }
-      const char* kcs = kc0 + size_t(ch) * HQ * kKcBytes;
-      const uint32_t lk = lds_u32(Kc[b3]);
+      auto issue_copies = [&](int ch) {
+        const int t0 = bos + ch * C, L = chunk_len(ch);
+        const int b3 = ch % NB;
+        if constexpr (CW == 0) {
+          const uint32_t lq = lds_u32(rq[b3]);
+          if (L == C) {
+            const char* qb = reinterpret_cast<const char*>(q + size_t(t0) * qk_stride + size_t(hq) * D);
 #pragma unroll
-      for (int j = 0; j < kKcCopies; ++j) dma16(kcs + kFrag * j, lane16, lk + uint32_t(kFrag * j));
-      const char* gsrc = record(ch) + BL_G;
-      const uint32_t lg = lds_u32(gt[b3]);
+            for (int j = 0; j < 16; ++j) dma16(qb, q_off[j], lq + uint32_t(kFrag * j));
+          } else {
 #pragma unroll
-      for (int j = 0; j < kGateCopies; ++j)
-        if (j < kGateCopies - 1 || kFrag * j + 16 * lane < kGateBytes)
-          dma16(gsrc + kFrag * j, lane16, lg + uint32_t(kFrag * j));
+            for (int j = 0; j < 16; ++j) {
+              const int row = 4 * j + (lane >> 4);
+              const int src_piece = (lane & 15) ^ (row & 15);
+              lds_dma16(q + size_t(t0 + min(row, L - 1)) * qk_stride + size_t(hq) * D + 8 * src_piece,
+                        &rq[b3][4 * j * D]);
+            }
+          }
+          const char* gsrc = record(ch) + BL_G;
+          const uint32_t lg = lds_u32(gt[b3]);
+#pragma unroll
+          for (int j = 0; j < kGateCopies; ++j)
+            if (j < kGateCopies - 1 || kFrag * j + 16 * lane < kGateBytes)
+              dma16(gsrc + kFrag * j, lane16, lg + uint32_t(kFrag * j));
+        } else {
+          const uint32_t lv = lds_u32(rv[b3]);
+          if (L == C) {
+            const char* vbp = reinterpret_cast<const char*>(v + size_t(t0) * v_stride + size_t(hv) * D + vb);
+#pragma unroll
+            for (int j = 0; j < VS; ++j) dma16(vbp, v_off[j], lv + uint32_t(kFrag * j));
+          } else {
+#pragma unroll
+            for (int j = 0; j < VS; ++j) {
+              const int row = Cfg::VRows * j + lane / VS;
+              const int src_piece = (lane % VS) ^ (row & (VS - 1));
+              lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + vb + 8 * src_piece,
+                        &rv[b3][Cfg::VRows * j * R]);
+            }
+          }
+          const char* kcs = kc0 + size_t(ch) * HQ * kKcBytes;
+          const uint32_t lk = lds_u32(Kc[b3]);
+#pragma unroll
+          for (int j = 0; j < kKcCopies; ++j) dma16(kcs + kFrag * j, lane16, lk + uint32_t(kFrag * j));
+        }
+      };
+      // copies(ch) land before the barrier that ends chunk ch - 1: at most
+      // (NB - 2) later chunks' copies are still in flight then.
+      auto wait_ahead = [&](int later) {        // wait until `later` chunks' copies remain
+        if (later >= 2 && NB > 3) wait_vm<2 * kCopiesW>();
+        else if (later >= 1) wait_vm<kCopiesW>();
+        else wait_vm<0>();
+      };
+      if (n_chunks > 0) {
+#pragma unroll
+        for (int a = 0; a < NB - 1; ++a)
+          if (a < n_chunks) issue_copies(a);
+        wait_ahead(min(n_chunks, NB - 1) - 1);  // copies(0) landed
+        lds_barrier();
+      }
+      for (int ch = 0; ch < n_chunks; ++ch) {
+        // the chain reads chunk ch; copies(ch+1 .. ch+NB-2) are in flight,
+        // copies(ch+NB-1) go into the buffers chunk ch-1 used
+        if (ch + NB - 1 < n_chunks) issue_copies(ch + NB - 1);
+        // copies(ch+1) land before the middle barrier: the state waves form
+        // K S^T of chunk ch+1 after it
+        wait_ahead(min(n_chunks - 1, ch + NB - 1) - (ch + 1));
+        lds_barrier();                          // Vn exchange of chunk ch
+        lds_barrier();
+      }
     };
-    // copies(ch) land before the barrier that ends chunk ch - 1: at most
-    // (NB - 2) later chunks' copies are still in flight then.
-    constexpr int kWait1 = Cfg::kCopies < 63 ? Cfg::kCopies : 63;
-    constexpr int kWait2 = 2 * Cfg::kCopies < 63 ? 2 * Cfg::kCopies : 63;
-    auto wait_ahead = [&](int later) {          // wait until `later` chunks' copies remain
-      if (later >= 2 && NB > 3) wait_vm<kWait2>();
-      else if (later >= 1) wait_vm<kWait1>();
-      else wait_vm<0>();
-    };
-    if (n_chunks > 0) {
-#pragma unroll
-      for (int a = 0; a < NB - 1; ++a)
-        if (a < n_chunks) issue_copies(a);
-      wait_ahead(min(n_chunks, NB - 1) - 1);    // copies(0) landed
-      lds_barrier();
-    }
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      // the chain reads chunk ch; copies(ch+1 .. ch+NB-2) are in flight,
-      // copies(ch+NB-1) go into the buffers chunk ch-1 used
-      if (ch + NB - 1 < n_chunks) issue_copies(ch + NB - 1);
-      // copies(ch+1) land before the middle barrier: the state waves form
-      // K S^T of chunk ch+1 after it
-      wait_ahead(min(n_chunks - 1, ch + NB - 1) - (ch + 1));
-      lds_barrier();                            // Vn exchange of chunk ch
-      lds_barrier();
-    }
+    if (wave == 2 * NRG) run_copies(IC<0>{});
+    else run_copies(IC<1>{});
   }
 }
 
