@@ -4,9 +4,11 @@ slices) against the CPU oracle (fp64) and against the fused chain kernel.
 Bars: output (bf16) within atol = rtol = 1e-2; final state relative error
 (Frobenius, per sequence and overall) <= 1e-3.  Without the L2-norm option
 the split path performs the state-path operations of the fused kernel in the
-same order: the final states must be equal bit for bit.  The outputs agree
-to within 1e-4 (in a few elements per million a P entry rounds to the other
-neighbouring fp16 value; both paths are equally close to the oracle there).
+same order: on the cases here the final states are equal bit for bit, and
+the outputs agree to within 1e-4 (in a few elements per million a P entry
+rounds to the other neighbouring fp16 value; both paths are equally close to
+the oracle there).  Over thousands of sequences one or two states also
+differ in the last places, so the many-sequence test compares within 1e-4.
 """
 
 import pytest
@@ -173,3 +175,39 @@ def test_split_workspace_errors(device):
     assert lib.gdn_prefill_split_fwd(*args, 8, p(ws), need, 0, st) == capi.GDN_OK
     torch.cuda.synchronize()
     _check(out, fs, *_oracle(x))
+
+
+@pytest.mark.parametrize("N", [4096, 4100])
+def test_split_many_sequences(device, N):
+    """Batches around the size limit of the longest-first ordering (ranked up
+    to 4096 sequences, index order beyond), with empty and one-token
+    sequences: the chain of each sequence gives the fused kernel's result."""
+    inp = pkg_module("inputs")
+    gen = torch.Generator().manual_seed(N)
+    lens = torch.randint(0, 80, (N,), generator=gen).tolist()
+    lens[:4] = [0, 1, 79, 64]
+    print(f"split many sequences N={N} T={sum(lens)}", flush=True)
+    x = inp.prefill_inputs(lens, HQ=1, HV=1, seed=N + 3, with_state=False, cu_dtype=torch.int32)
+    g = _to(x, device)
+    o, s = _run(g, path="split", slices=4)
+    of, sf = _run(g, path="fused")
+    torch.cuda.synchronize()
+    # Over thousands of sequences one or two final states differ from the
+    # fused kernel's in the last places (both equally close to the oracle):
+    # per-sequence relative difference <= 1e-4, ten times inside the oracle bar.
+    ds = (s - sf).flatten(1).norm(dim=1) / sf.flatten(1).norm(dim=1).clamp_min(1e-30)
+    assert float(ds.max()) <= 1e-4, float(ds.max())
+    assert int((ds > 0).sum()) <= max(2, N // 500)
+    do = (o.float() - of.float()).abs()
+    assert float(do.max()) <= 1e-3, float(do.max())
+    assert float(s[0].abs().max()) == 0.0
+    # a few sequences against the oracle on their own
+    cu = x["cu_seqlens"].long()
+    for n in (1, 2, 3, N - 1):
+        b, e = int(cu[n]), int(cu[n + 1])
+        xs = dict(x, q=x["q"][b:e], k=x["k"][b:e], v=x["v"][b:e], a=x["a"][b:e], b=x["b"][b:e],
+                  cu_seqlens=torch.tensor([0, e - b], dtype=torch.int64), state=None)
+        o_ref, s_ref = _oracle(xs)
+        torch.testing.assert_close(o[b:e].float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+        rel = float((s[n:n + 1].cpu().double() - s_ref).norm() / s_ref.norm().clamp_min(1e-300))
+        assert rel <= STATE_REL_BAR, (n, rel)
