@@ -20,9 +20,10 @@
 //        R = dO^T (scale E Q) - G1^T (beta E K),  G1 = Tm^T P^T dO      [V x K]
 //     so that dS = dSn M + R.  M is written as ready MFMA A-operand
 //     fragments, R in the accumulator layout of the chain kernel.
-//  2. gdn_bwd_chain_kernel, one workgroup per (sequence, v-head): walks the
-//     chunks from last to first with dS^T in MFMA accumulators, storing dSn
-//     of every chunk (bf16) and the gradient of the initial state.
+//  2. gdn_bwd_chain_kernel, one workgroup per (sequence, v-head), or per
+//     quarter of its state rows when the chains are few: walks the chunks
+//     from last to first with dS^T in MFMA accumulators, storing dSn of
+//     every chunk (bf16) and the gradient of the initial state.
 //  3. gdn_bwd_grad_kernel, one workgroup per (chunk, v-head): with S and dSn
 //     known, every gradient of the chunk:
 //        dVn = P^T dO + Dc K dSn^T,  dX = Tm^T dVn,  dV = beta dX,
@@ -47,6 +48,7 @@
 // their contributions vanish.
 
 #include "gdn_prefill_common.h"
+#include "gdn_prefill_split.h"
 #include "../../include/gdn_hip.h"
 
 namespace {
@@ -62,7 +64,6 @@ constexpr size_t kMBytes = size_t(D) * D * 2;   // M record (bf16 fragments)
 constexpr size_t kRBytes = size_t(D) * D * 4;   // R record (fp32 accumulators)
 constexpr size_t kHBytes = size_t(D) * D * 2;   // dSn record (bf16 [v][k])
 constexpr int kGradThreads = 512;
-constexpr int kChainThreads = 512;
 
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
 
@@ -454,23 +455,35 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
 // ---------------------------------------------------------------------------
 // 2. The state-gradient chain per (sequence, v-head), last chunk first:
 //    dh[chunk] = dSn (bf16 [v][k]);  dS = dSn M + R;  finally dh0 = dS.
-// Wave w keeps dS^T[k][v] for v in [16 w, 16 w + 16) as 8 accumulator tiles
-// (k blocks); the B operand of step s is the pair of tiles kt = 2 s, 2 s + 1.
-template <typename CuT>
-__global__ __launch_bounds__(kChainThreads, 1) void gdn_bwd_chain_kernel(
+// NW waves per workgroup, 128 / (16 NW) workgroups per chain.  A wave keeps
+// dS^T[k][v] for its 16 state rows v as 8 accumulator tiles (k blocks); the
+// B operand of step s is the pair of tiles kt = 2 s, 2 s + 1.
+template <typename CuT, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
     const CuT* __restrict__ cu, int N, int T, int HV, int h_chunks, const char* __restrict__ mrec,
     const char* __restrict__ rrec, const float* __restrict__ d_ht, uint16_t* __restrict__ dh,
     float* __restrict__ dh0) {
+  constexpr int S = 8 / NW;                    // slices (of 16 NW state rows) per chain
+  constexpr int kThreads = 64 * NW;
   __shared__ __align__(16) uint16_t sM[3][D * D];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = blockIdx.x / HV, hv = blockIdx.x - (blockIdx.x / HV) * HV;
+  // Workgroup -> (chain = (sequence, v-head), slice).  The rows of dS evolve
+  // independently (dS = dSn M + R row by row), so a chain splits over S
+  // workgroups that never exchange data; its slices get ids 8 apart, which
+  // puts them on one XCD, so M is read from HBM once per chain.
+  const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
+  const int chain = 8 * (id_row / S) + xcd;
+  if (chain >= N * HV) return;
+  const int slice = id_row - (id_row / S) * S;
+  const int n = chain / HV, hv = chain - n * HV;
   int bos, slen;
   seq_bounds(cu, n, T, bos, slen);
   const int nc = (slen + C - 1) / C;
   const int coff = chunk_offset(cu, n, T, lane);
   const int g = lane >> 4, c = lane & 15;
-  const int v = 16 * wave + c;                 // state row (v) of this lane's accumulator column
+  const int vb = slice * NW + wave;            // 16-row block of the state this wave holds
+  const int v = 16 * vb + c;                   // state row (v) of this lane's accumulator column
 
   f32x4 acc[8];
 #pragma unroll
@@ -484,20 +497,19 @@ __global__ __launch_bounds__(kChainThreads, 1) void gdn_bwd_chain_kernel(
   // M is copied HBM -> LDS and R loaded into registers two chunks ahead: three
   // LDS buffers for M and three register sets for R, rotated by unrolling the
   // chunk loop by three.
-  constexpr int kMCopies = int(kMBytes / 16) / kChainThreads;
+  constexpr int kMCopies = int(kMBytes / 16) / kThreads;
   auto rec_of = [&](int ch) { return size_t(coff + ch) * HV + hv; };
   auto copy_m = [&](int ch, int buf) {
     const char* ms = mrec + rec_of(ch) * kMBytes;
 #pragma unroll
     for (int x = 0; x < kMCopies; ++x)
-      lds_dma16_saddr(ms, uint32_t((x * kChainThreads + tid) * 16),
-                      &sM[buf][(x * kChainThreads + wave * 64) * 8]);
+      lds_dma16_saddr(ms, uint32_t((x * kThreads + tid) * 16), &sM[buf][(x * kThreads + wave * 64) * 8]);
   };
   auto fetch_r = [&](int ch, f32x4 (&r)[8]) {
     const char* rs = rrec + rec_of(ch) * kRBytes;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
-      r[kt] = *reinterpret_cast<const f32x4*>(rs + ((wave * 8 + kt) * 64 + lane) * 16);
+      r[kt] = *reinterpret_cast<const f32x4*>(rs + ((vb * 8 + kt) * 64 + lane) * 16);
   };
   // one chunk: dSn out, dS = dSn M + R (cur = R of chunk ch), and the copies
   // for chunk ch - 2 (R into nxt2, M into LDS buffer (it + 2) % 3)
@@ -987,8 +999,16 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
   const dim3 cgrid{unsigned(slots), unsigned(HV), 1u};
   hipLaunchKernelGGL((gdn_bwd_prep_kernel<CuT>), cgrid, dim3(kGradThreads), 0, st, q, k, A_log, a,
                      dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h_chunks, mrec, rrec);
-  hipLaunchKernelGGL((gdn_bwd_chain_kernel<CuT>), dim3(unsigned(N) * unsigned(HV)), dim3(kChainThreads),
-                     0, st, cu, N, T, HV, h_chunks, mrec, rrec, d_ht, dhr, dh0);
+  // The reverse chain: one workgroup of 8 waves per chain, or, when the
+  // chains leave most CUs idle, 4 workgroups of 2 waves (32 state rows) each.
+  const unsigned chain_ids = 8u * ((unsigned(N) * unsigned(HV) + 7u) / 8u);
+  const int cus = device_cus();
+  if (cus > 0 && 4LL * N * HV <= cus)
+    hipLaunchKernelGGL((gdn_bwd_chain_kernel<CuT, 2>), dim3(4u * chain_ids), dim3(128), 0, st, cu, N, T,
+                       HV, h_chunks, mrec, rrec, d_ht, dhr, dh0);
+  else
+    hipLaunchKernelGGL((gdn_bwd_chain_kernel<CuT, 8>), dim3(chain_ids), dim3(512), 0, st, cu, N, T, HV,
+                       h_chunks, mrec, rrec, d_ht, dhr, dh0);
   if (T > 0) {
     hipLaunchKernelGGL((gdn_bwd_grad_kernel<CuT>), cgrid, dim3(kGradThreads), 0, st, q, k, v, A_log, a,
                        dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h, h_chunks, dhr,

@@ -21,6 +21,9 @@ int prefill_split_auto_slices(int N, int HV);
 
 bool prefill_split_slices_valid(int slices);
 
+// CUs of the current device (looked up once per device), 0 on error.
+int device_cus();
+
 // Size and current-device address of the library's static split-path
 // workspace (the allocation-free entry point's scratch).
 size_t prefill_scratch_bytes();

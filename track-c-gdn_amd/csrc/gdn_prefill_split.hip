@@ -989,6 +989,8 @@ int prefill_split_auto_slices(int N, int HV) {
 
 bool prefill_split_slices_valid(int slices) { return slices == 4 || slices == 8; }
 
+int device_cus() { return device_cu_count(); }
+
 size_t prefill_scratch_bytes() { return kScratchBytes; }
 
 void* prefill_scratch(hipError_t* err) { return scratch_address(err); }
