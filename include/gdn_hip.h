@@ -174,7 +174,8 @@ int gdn_prefill_auto_slices(int N, int HV);
 
 /*
  * Workspace bytes of gdn_prefill_split_fwd: 14 080 bytes per (chunk, v-head)
- * and 18 432 per (chunk, qk-head) for an upper bound of T / 64 + N chunks.
+ * and 18 432 per (chunk, qk-head) for an upper bound of T / 64 + N chunks,
+ * plus the sequences' launch order (N ints, rounded up to 256 bytes).
  */
 size_t gdn_prefill_split_workspace_bytes(int N, int T, int HQ, int HV);
 

@@ -11,7 +11,8 @@ namespace gdn {
 
 // Workspace bytes of the split path for an upper bound of T / 64 + N chunks:
 // one 14 080-byte record per (chunk, v-head) and one 18 432-byte fp16 K image
-// per (chunk, qk-head).
+// per (chunk, qk-head), then the sequences' launch order (N ints, rounded up
+// to 256 bytes).
 size_t prefill_split_workspace_bytes(int N, int T, int HQ, int HV);
 
 // Slices per chain the split path uses on the current device for N * HV
