@@ -93,6 +93,14 @@ def ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device) -> int:
-    """The hipStream_t of torch's current stream on ``device``."""
+    """The hipStream_t of torch's current stream on ``device`` (torch's raw
+    accessor when it has one: a tenth of the cost of building the Stream
+    object)."""
+    if _raw_stream is not None:
+        idx = device.index if isinstance(device, torch.device) else None
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream

@@ -86,6 +86,13 @@ def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
     ``qk_l2norm=True`` uses q and k L2-normalised, ``x (sum x^2 + 1e-6)^-1/2``
     in fp32 inside the kernel (an option the reference does not have).
     """
+    return _decode_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output=output,
+                        new_state=new_state, qk_l2norm=qk_l2norm)
+
+
+def _decode_impl(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output=None,
+                 new_state=None, qk_l2norm: bool = False):
+    """:func:`gdn_decode` without its no-grad wrapper (the callers hold one)."""
     B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
     scale = _resolve_scale(scale, q.shape[-1])
     if state is not None:
@@ -123,7 +130,7 @@ def run(q, k, v, state, A_log, a, dt_bias, b, scale):
     assert out_dtype.is_floating_point
     q, k, v, a, b = (t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
                      for t in (q, k, v, a, b))
-    o, s = gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale)
+    o, s = _decode_impl(q, k, v, state, A_log, a, dt_bias, b, scale)
     return (o if out_dtype == torch.bfloat16 else o.to(out_dtype)), s
 
 
@@ -134,7 +141,7 @@ def run_dps(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
     assert k.shape[1:] == (1, HQ, D)
     assert v.shape[1:] == (1, HV, D)
     assert q.shape[0] == v.shape[0]
-    gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale, output=output, new_state=new_state)
+    _decode_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output=output, new_state=new_state)
 
 
 @torch.no_grad()
