@@ -133,6 +133,30 @@ def test_update_slot_pool(device):
     assert torch.equal(pg.cpu(), expect_pool)
 
 
+@pytest.mark.parametrize("B,with_bias", [(1024, True), (7, False)])
+def test_update_batch_qk16_v32_matches_oracle(device, B, with_bias):
+    """The decode update at the benchmark's width (qk16 / v32: 8192 channels,
+    four channel blocks of 2048 per row of workgroups) over a batch whose
+    size is and is not a multiple of the sequences a lane takes."""
+    conv = pkg_module("conv")
+    HQ, HV, W, S = 16, 32, 4, 3
+    C = 256 * HQ + 128 * HV
+    gen = torch.Generator().manual_seed(B + 5)
+    x = torch.randn(B, C, generator=gen).to(torch.bfloat16)
+    w = torch.randn(C, W, generator=gen) * 0.5
+    bias = torch.randn(C, generator=gen) * 0.1 if with_bias else None
+    st = torch.randn(B, C, S, generator=gen).to(torch.bfloat16)
+    sg = st.to(device)
+    q, k, v = conv.qkv_conv1d_update(x.to(device), sg, w.to(device),
+                                     None if bias is None else bias.to(device),
+                                     num_q_heads=HQ, num_v_heads=HV)
+    torch.cuda.synchronize()
+    y = torch.cat([q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1)], dim=1).cpu()
+    yr, sr = O.causal_conv1d_update(x, st, w, bias, "silu")
+    _close_bf16(y, yr)
+    assert torch.equal(sg.cpu(), sr.to(torch.bfloat16))
+
+
 def test_conv_then_prefill_matches_oracle_chain(device):
     """conv1d + SiLU -> GDN prefill with in-kernel q/k L2-norm, against the
     fp64 chain (oracle conv, rounded to bf16 as the kernel stores it, then

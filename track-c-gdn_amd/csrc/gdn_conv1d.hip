@@ -178,66 +178,97 @@ __global__ __launch_bounds__(kConvThreads) void gdn_qkv_conv1d_kernel(
   }
 }
 
-// Decode: one token per sequence b, grid (ceil(C / 2048), B); the state row
-// state[slot] (slot = slot_ids[b], or b) is read, shifted by one with the
-// token appended, and written back in place.  A slot outside [0, pool) leaves
-// the state untouched and yields a zero output row.  The state length S is a
+// Decode: one token per sequence b, grid (ceil(C / 2048), ceil(B / kUpdSeqs)):
+// a lane takes its 8 channels of kUpdSeqs sequences, so the channels' taps
+// and bias are loaded once for all of them; every sequence's input and state
+// words are issued before the first is used.  The state row state[slot]
+// (slot = slot_ids[b], or b) is read, shifted by one with the token appended,
+// and written back in place.  A slot outside [0, pool) leaves the state
+// untouched and yields a zero output row.  The state length S is a
 // compile-time W - 1 or W.
+constexpr int kUpdSeqs = 4;
+
 template <int W, int S, bool kSilu>
 __global__ __launch_bounds__(kConvThreads) void gdn_qkv_conv1d_update_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ bias,
-    uint16_t* __restrict__ state, const int32_t* __restrict__ slot_ids, int pool, int C,
+    uint16_t* __restrict__ state, const int32_t* __restrict__ slot_ids, int B, int pool, int C,
     QkvOut o) {
   const int c0 = 8 * (blockIdx.x * kConvThreads + threadIdx.x);
-  const int b = blockIdx.y;
   if (c0 >= C) return;
-  const int slot = slot_ids != nullptr ? slot_ids[b] : b;
-  float y[8];
-  if (slot < 0 || slot >= pool) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = 0.f;
-    store8(out_at(o, b, c0), y);
-    return;
-  }
-  float xc[8];
-  load8(x + size_t(b) * C + c0, xc);
-  // the lane's state block: channels c0 .. c0 + 7, S entries each, 16 S
-  // contiguous bytes (S 16-byte words)
-  uint16_t* st = state + (size_t(slot) * C + c0) * S;
-  uint4 raw[S];
-#pragma unroll
-  for (int i = 0; i < S; ++i) raw[i] = reinterpret_cast<const uint4*>(st)[i];
-  auto elem = [&](int idx) {                  // bf16 element idx of the block (idx constant)
-    const uint4 w = raw[idx >> 3];
-    const int q = idx & 7;
-    const uint32_t d = (q >> 1) == 0 ? w.x : (q >> 1) == 1 ? w.y : (q >> 1) == 2 ? w.z : w.w;
-    return (q & 1) ? (d >> 16) : (d & 0xffffu);
-  };
+  const int b0 = blockIdx.y * kUpdSeqs;
+  float wt[8][W], bs[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float acc = bias != nullptr ? bias[c0 + e] : 0.f;
+    bs[e] = bias != nullptr ? bias[c0 + e] : 0.f;
 #pragma unroll
-    for (int j = 0; j < W - 1; ++j)   // window input j: state entry S - (W - 1) + j
-      acc = fmaf(weight[(c0 + e) * W + j], bf16_bits_to_f32(elem(e * S + S - (W - 1) + j)), acc);
-    acc = fmaf(weight[(c0 + e) * W + W - 1], xc[e], acc);
-    y[e] = activate<kSilu>(acc);
+    for (int j = 0; j < W; ++j) wt[e][j] = weight[(c0 + e) * W + j];
   }
-  store8(out_at(o, b, c0), y);
-  // shifted block: entry si of channel e <- entry si + 1 (the token last)
-  uint32_t nw[8 * S];
+  int slot[kUpdSeqs];
+  bool live[kUpdSeqs];
+  uint4 xw[kUpdSeqs], raw[kUpdSeqs][S];
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
+  for (int u = 0; u < kUpdSeqs; ++u) {
+    const int b = b0 + u;
+    slot[u] = b < B ? (slot_ids != nullptr ? slot_ids[b] : b) : -1;
+    live[u] = slot[u] >= 0 && slot[u] < pool;
+    if (live[u]) {
+      xw[u] = *reinterpret_cast<const uint4*>(x + size_t(b) * C + c0);
+      // the lane's state block: channels c0 .. c0 + 7, S entries each, 16 S
+      // contiguous bytes (S 16-byte words)
+      const uint4* st = reinterpret_cast<const uint4*>(state + (size_t(slot[u]) * C + c0) * S);
 #pragma unroll
-    for (int si = 0; si < S; ++si)
-      nw[e * S + si] = si + 1 < S ? elem(e * S + si + 1) : uint32_t(f32_to_bf16_bits(xc[e]));
+      for (int i = 0; i < S; ++i) raw[u][i] = st[i];
+    }
+  }
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    uint4 w;
-    w.x = nw[8 * i + 0] | (nw[8 * i + 1] << 16);
-    w.y = nw[8 * i + 2] | (nw[8 * i + 3] << 16);
-    w.z = nw[8 * i + 4] | (nw[8 * i + 5] << 16);
-    w.w = nw[8 * i + 6] | (nw[8 * i + 7] << 16);
-    reinterpret_cast<uint4*>(st)[i] = w;
+  for (int u = 0; u < kUpdSeqs; ++u) {
+    const int b = b0 + u;
+    if (b >= B) break;
+    float y[8];
+    if (!live[u]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = 0.f;
+      store8(out_at(o, b, c0), y);
+      continue;
+    }
+    float xc[8];
+    unpack_bf16x2(xw[u].x, xc[0], xc[1]);
+    unpack_bf16x2(xw[u].y, xc[2], xc[3]);
+    unpack_bf16x2(xw[u].z, xc[4], xc[5]);
+    unpack_bf16x2(xw[u].w, xc[6], xc[7]);
+    auto elem = [&](int idx) {                // bf16 element idx of the block (idx constant)
+      const uint4 w = raw[u][idx >> 3];
+      const int q = idx & 7;
+      const uint32_t d = (q >> 1) == 0 ? w.x : (q >> 1) == 1 ? w.y : (q >> 1) == 2 ? w.z : w.w;
+      return (q & 1) ? (d >> 16) : (d & 0xffffu);
+    };
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = bs[e];
+#pragma unroll
+      for (int j = 0; j < W - 1; ++j)   // window input j: state entry S - (W - 1) + j
+        acc = fmaf(wt[e][j], bf16_bits_to_f32(elem(e * S + S - (W - 1) + j)), acc);
+      acc = fmaf(wt[e][W - 1], xc[e], acc);
+      y[e] = activate<kSilu>(acc);
+    }
+    store8(out_at(o, b, c0), y);
+    // shifted block: entry si of channel e <- entry si + 1 (the token last)
+    uint32_t nw[8 * S];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int si = 0; si < S; ++si)
+        nw[e * S + si] = si + 1 < S ? elem(e * S + si + 1) : uint32_t(f32_to_bf16_bits(xc[e]));
+    uint4* st = reinterpret_cast<uint4*>(state + (size_t(slot[u]) * C + c0) * S);
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      uint4 w;
+      w.x = nw[8 * i + 0] | (nw[8 * i + 1] << 16);
+      w.y = nw[8 * i + 2] | (nw[8 * i + 3] << 16);
+      w.z = nw[8 * i + 4] | (nw[8 * i + 5] << 16);
+      w.w = nw[8 * i + 6] | (nw[8 * i + 7] << 16);
+      st[i] = w;
+    }
   }
 }
 
@@ -277,24 +308,24 @@ void launch_conv(int W, dim3 grid, hipStream_t st, const uint16_t* x, const floa
 
 template <int W, bool kSilu>
 void launch_update_w(int S, dim3 grid, hipStream_t st, const uint16_t* x, const float* weight,
-                     const float* bias, uint16_t* state, const int32_t* slots, int pool, int C,
+                     const float* bias, uint16_t* state, const int32_t* slots, int B, int pool, int C,
                      QkvOut o) {
   if (S == W - 1)
     hipLaunchKernelGGL((gdn_qkv_conv1d_update_kernel<W, W - 1, kSilu>), grid, dim3(kConvThreads), 0, st, x,
-                       weight, bias, state, slots, pool, C, o);
+                       weight, bias, state, slots, B, pool, C, o);
   else
     hipLaunchKernelGGL((gdn_qkv_conv1d_update_kernel<W, W, kSilu>), grid, dim3(kConvThreads), 0, st, x,
-                       weight, bias, state, slots, pool, C, o);
+                       weight, bias, state, slots, B, pool, C, o);
 }
 
 template <bool kSilu>
 void launch_update(int W, int S, dim3 grid, hipStream_t st, const uint16_t* x, const float* weight,
-                   const float* bias, uint16_t* state, const int32_t* slots, int pool, int C,
+                   const float* bias, uint16_t* state, const int32_t* slots, int B, int pool, int C,
                    QkvOut o) {
   switch (W) {
-    case 2: launch_update_w<2, kSilu>(S, grid, st, x, weight, bias, state, slots, pool, C, o); break;
-    case 3: launch_update_w<3, kSilu>(S, grid, st, x, weight, bias, state, slots, pool, C, o); break;
-    default: launch_update_w<4, kSilu>(S, grid, st, x, weight, bias, state, slots, pool, C, o); break;
+    case 2: launch_update_w<2, kSilu>(S, grid, st, x, weight, bias, state, slots, B, pool, C, o); break;
+    case 3: launch_update_w<3, kSilu>(S, grid, st, x, weight, bias, state, slots, B, pool, C, o); break;
+    default: launch_update_w<4, kSilu>(S, grid, st, x, weight, bias, state, slots, B, pool, C, o); break;
   }
 }
 
@@ -352,11 +383,11 @@ extern "C" int gdn_qkv_conv1d_update(const uint16_t* x, const float* weight, con
   QkvOut o;
   const int rc = check_qkv(out_q, out_k, out_v, C, cq, ck, o);
   if (rc != GDN_OK) return rc;
-  const dim3 grid((C / 8 + kConvThreads - 1) / kConvThreads, B);
+  const dim3 grid((C / 8 + kConvThreads - 1) / kConvThreads, (B + kUpdSeqs - 1) / kUpdSeqs);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int pool = slot_ids != nullptr ? pool_size : B;
-  if (activation == GDN_ACT_SILU) launch_update<true>(W, state_len, grid, st, x, weight, bias, conv_state, slot_ids, pool, C, o);
-  else launch_update<false>(W, state_len, grid, st, x, weight, bias, conv_state, slot_ids, pool, C, o);
+  if (activation == GDN_ACT_SILU) launch_update<true>(W, state_len, grid, st, x, weight, bias, conv_state, slot_ids, B, pool, C, o);
+  else launch_update<false>(W, state_len, grid, st, x, weight, bias, conv_state, slot_ids, B, pool, C, o);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GDN_OK : -int(e);
 }
