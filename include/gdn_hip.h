@@ -188,8 +188,10 @@ size_t gdn_prefill_split_workspace_bytes(int N, int T, int HQ, int HV);
  * This is how the reference spreads its recurrence over the GPU: the
  * per-chunk kernels over all chunks, the recurrence over V-slices
  * (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:544, 1005, 1369).
- * The final state equals gdn_prefill_ex_fwd's bit for bit without
- * GDN_QK_L2NORM; outputs agree to within 1e-4.
+ * Without GDN_QK_L2NORM the state-path operations are gdn_prefill_ex_fwd's
+ * in the same order: final states equal bit for bit but for rare last-place
+ * differences (one or two sequences in thousands); outputs agree to within
+ * 1e-4.
  *   workspace : at least gdn_prefill_split_workspace_bytes(...) bytes, else
  *               GDN_ERR_WORKSPACE.  Other slice counts: GDN_ERR_SHAPE.
  */

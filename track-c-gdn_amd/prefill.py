@@ -129,7 +129,9 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     slices -- when the chains alone leave CUs idle, else the fused chain
     kernel), ``"fused"`` (one workgroup per chain) or ``"split"`` with
     ``slices`` in (4, 8) state slices per chain.  Without ``qk_l2norm`` the
-    two paths give the same final state bit for bit.
+    two paths perform the state-path operations in the same order: their
+    final states agree bit for bit but for rare last-place differences (one
+    or two sequences in thousands).
 
     Input range: the state path multiplies fp16 operands, so k, v, the state
     and the intermediate X and Vn must stay below 65504 in magnitude (far
