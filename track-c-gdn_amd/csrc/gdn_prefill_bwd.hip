@@ -45,7 +45,9 @@
 // transposing LDS reads (ds_read_b64_tr_b16) when the product reduces over
 // the other index.  Tm comes from an fp32 forward substitution.  Rows past a
 // chunk's end are zero with beta = 0 and g = 0, which makes every one of
-// their contributions vanish.
+// their contributions vanish.  The waves of a workgroup exchange data only
+// through LDS, so their barriers wait for LDS operations alone
+// (lds_barrier): global loads and stores stay in flight across them.
 
 #include "gdn_prefill_common.h"
 #include "gdn_prefill_split.h"
@@ -352,7 +354,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
     rows_store(sdO, wo, tid);
     if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Ar, P; the scaled row copies
   ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
     *reinterpret_cast<uint4*>(&sBEK[r * LDK + cc]) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
     *reinterpret_cast<uint4*>(&sEQ[r * LDK + cc]) = make_uint4(oq[0], oq[1], oq[2], oq[3]);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Tm (wave 0) while waves 1-7 form G0 = P^T dO [t][v] over sK (K is done)
   if (wave == 0) {
@@ -391,7 +393,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
       st_tile(sK, LDK, 16 * tb, 16 * vb, acc, lane);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // W2 = Tm^T Dc K -> sQ, -G1 = -Tm^T G0 -> sAr (as bf16 [64][LDK])
   uint16_t* sG1 = reinterpret_cast<uint16_t*>(sAr);
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
       st_tile(sG1, LDK, 16 * tb, 16 * db, -g1, lane);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // M = e^{gam_L} I - W2^T (beta E K): tiles (jt, kt); R^T = (scale E Q)^T dO + (beta E K)^T (-G1)
   const size_t rec = size_t(slot) * HV + hv;
@@ -542,7 +544,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
     // outstanding, everything the next chunk reads has landed.
     if (ch > 1) wait_vm<kMCopies + 8 + 8>();
     else wait_vm<8>();
-    __syncthreads();
+    lds_barrier();
   };
   f32x4 r0[8], r1[8], r2[8];
   if (last >= 0) {
@@ -554,7 +556,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
     }
   }
   wait_vm<0>();
-  __syncthreads();
+  lds_barrier();
   for (int ch = last, it = 0; ch >= 0; ch -= 3, it += 3) {
     step(ch, it, r0, r2);
     if (ch >= 1) step(ch - 1, it + 1, r1, r0);
@@ -637,10 +639,10 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   rows_store(sdO, wo, tid);
   rows_store(sX, wv, tid);
   if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
-  __syncthreads();
+  lds_barrier();
 
   ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
-  __syncthreads();
+  lds_barrier();
 
   const int tb = wave & 3, d0 = 4 * (wave >> 2);
   const int ib = wave >> 1, j0 = 2 * (wave & 1);
@@ -665,7 +667,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       xr[u][i] = bf16_bits_to_f32(sX[row * LDK + 16 * db + c16]) - eks[u][i];
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     f32x4 x;
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     for (int i = 0; i < 4; ++i) x[i] = gb[GB_BETA + 16 * tb + 4 * g4 + i] * xr[u][i];
     st_tile(sX, LDK, 16 * tb, 16 * (d0 + u), x, lane);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Vn = Tm X;  dVn = Dc K dSn^T + P^T dO
   f32x4 vn[4];
@@ -704,7 +706,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     const int row = 16 * tb + 4 * g4 + i;
     if (c16 == 0) pt.vk[wave >> 2][row] = gb[GB_DC + row] * t;
   }
-  __syncthreads();
+  lds_barrier();
 
   // dX = Tm^T dVn (dV, dbeta / dgam terms);  dTm = dVn X^T
   f32x4 dx[4];
@@ -734,7 +736,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       x = mfma16_bf(op_mr(sdV, LDK, 16 * ib, 32 * s, lane), op_mr(sX, LDK, 16 * (j0 + u), 32 * s, lane), x);
     st_tile(sdT, LDC, 16 * ib, 16 * (j0 + u), x, lane);
   }
-  __syncthreads();
+  lds_barrier();
 
   // -beta E dX -> sX;  Y = dTm Tm^T
 #pragma unroll
@@ -755,7 +757,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       x = mfma16_bf(op_mr(sdT, LDC, 16 * ib, 32 * s, lane), op_mr(sTm, LDC, 16 * (j0 + u), 32 * s, lane), x);
     st_tile(sY, LDC, 16 * ib, 16 * (j0 + u), x, lane);
   }
-  __syncthreads();
+  lds_barrier();
 
   // dA = -Tm^T Y (strictly lower), dP = dO Vn^T (inclusive lower): their dbeta / dgam terms
   uint4 wst[4];
@@ -805,7 +807,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     st_tile(sdT, LDC, 16 * ib, 16 * (j0 + u), dab[u], lane);
@@ -813,7 +815,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   }
   // S -> LDS [v][LDK] over dVn and Ar (both read for the last time above)
   state_store(sS, wst, tid);
-  __syncthreads();
+  lds_barrier();
 
   // dQ = scale E dO S + dPm K;  dK (all but the dSn term) = -beta E dX S + dPm^T Q + dAb K + dAb^T K
   uint4 wds[4];
@@ -875,9 +877,9 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
     if (lane == 0) pt.dot[wave] = part;
   }
-  __syncthreads();
+  lds_barrier();
   state_store(sS, wds, tid);
-  __syncthreads();
+  lds_barrier();
 
   // dK += Dc Vn dSn
 #pragma unroll
@@ -902,7 +904,7 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       pt.ab[wave >> 2][row] = tbv;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   if (wave == 0) {
     const int t = lane;
