@@ -353,35 +353,60 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       *reinterpret_cast<f32x4*>(&sm.A[(16 * ti + c) * ALD + 16 * tj + 4 * g]) = val;
     }
   };
-  // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the raw bf16 rows
+  // P tiles = scale tril_incl(e^{gam_i - gam_j} Q K^T) from the raw bf16 rows
   // (bf16 MFMA: the inputs are exact), formed transposed like the A tiles:
   // lane (g, c) holds row 16 ti + c, columns 16 tj + 4 g .. +3, which are 4
-  // adjacent positions of the p32 order.  Rows past the chunk end hold copies
-  // of its last row; they only reach output rows that are never stored.
-  auto tile_P = [&](auto tile_c, const float* gd, int pb) {
-    constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
-    constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
-    bf16x8_t fa[4], fb[4];
+  // adjacent positions of the p32 order.  The tiles (ti, 2 s) and (ti, 2 s + 1)
+  // are formed together (one set of Q fragments) and their 8 positions
+  // 32 s + 8 g .. +7 go out as one 16-byte write; a tile above the diagonal is
+  // written as zeros.  (Two 8-byte writes per lane down 16 rows of 160 bytes
+  // meet in the LDS banks; one 16-byte write per lane does not.)  Rows past
+  // the chunk end hold copies of its last row; they only reach output rows
+  // that are never stored.
+  auto tile_P_pair = [&](auto ti_c, auto s_c, const float* gd, int pb) {
+    constexpr int ti = decltype(ti_c)::value;
+    constexpr int tj0 = 2 * decltype(s_c)::value, tj1 = tj0 + 1;
+    constexpr bool two = tj1 <= ti;
+    bf16x8_t fa[4], fb0[4], fb1[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       fa[ks] = ld16_bf(&raw.q[pb][raw_lane[ks] + 16 * ti * D]);
-      fb[ks] = ld16_bf(&raw.k[pb][raw_lane[ks] + 16 * tj * D]);
+      fb0[ks] = ld16_bf(&raw.k[pb][raw_lane[ks] + 16 * tj0 * D]);
+      if constexpr (two) fb1[ks] = ld16_bf(&raw.k[pb][raw_lane[ks] + 16 * tj1 * D]);
     }
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
-    if (neg_scale) acc = -acc;
+    for (int ks = 0; ks < 4; ++ks) {
+      acc0 = mfma16_bf(fb0[ks], fa[ks], acc0);
+      if constexpr (two) acc1 = mfma16_bf(fb1[ks], fa[ks], acc1);
+    }
+    if (neg_scale) {
+      acc0 = -acc0;
+      acc1 = -acc1;
+    }
     const float gr = gd[G_L2 + 16 * ti + c] + scale_l2;
-    const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
-    if constexpr (kL2) acc *= nq(pb)[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk(pb)[16 * tj + 4 * g]);
-    f16x4_t val;
+    const f32x4 gcol0 = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj0 + 4 * g]);
+    f32x4 gcol1 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (two) gcol1 = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj1 + 4 * g]);
+    if constexpr (kL2) {
+      const float qn = nq(pb)[16 * ti + c];
+      acc0 *= qn * *reinterpret_cast<const f32x4*>(&nk(pb)[16 * tj0 + 4 * g]);
+      if constexpr (two) acc1 *= qn * *reinterpret_cast<const f32x4*>(&nk(pb)[16 * tj1 + 4 * g]);
+    }
+    f16x8 val;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float x = __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
-      if (ti == tj) x = (c >= 4 * g + i) ? x : 0.f;
-      val[i] = (_Float16)x;
+      float x0 = __builtin_amdgcn_exp2f(gr - gcol0[i]) * acc0[i];
+      if (ti == tj0) x0 = (c >= 4 * g + i) ? x0 : 0.f;
+      val[i] = (_Float16)x0;
+      float x1 = 0.f;
+      if constexpr (two) {
+        x1 = __builtin_amdgcn_exp2f(gr - gcol1[i]) * acc1[i];
+        if (ti == tj1) x1 = (c >= 4 * g + i) ? x1 : 0.f;
+      }
+      val[4 + i] = (_Float16)x1;
     }
-    *reinterpret_cast<f16x4_t*>(&sm.P[(16 * ti + c) * TLD + 32 * (tj >> 1) + 8 * g + 4 * (tj & 1)]) = val;
+    *reinterpret_cast<f16x8*>(&sm.P[(16 * ti + c) * TLD + 16 * tj0 + 8 * g]) = val;
   };
   // A tiles of the chunk of parity pb inside the diagonal 32-row blocks (the
   // inverse's input): 6 tiles over the 4 preparation waves.
@@ -454,17 +479,17 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // previous iteration), 4 in P1 of the chunk's own iteration.
   auto tiles_P1 = [&](const float* gd, int pb) {
     switch (pw) {
-      case 1: tile_P(IC<0>{}, gd, pb); tile_P(IC<8>{}, gd, pb); break;
-      case 2: tile_P(IC<2>{}, gd, pb); tile_P(IC<7>{}, gd, pb); break;
-      case 3: tile_P(IC<5>{}, gd, pb); tile_P(IC<6>{}, gd, pb); break;
+      case 1: tile_P_pair(IC<2>{}, IC<0>{}, gd, pb); break;    // (2, 0), (2, 1)
+      case 2: tile_P_pair(IC<3>{}, IC<0>{}, gd, pb); break;    // (3, 0), (3, 1)
+      case 3: tile_P_pair(IC<3>{}, IC<1>{}, gd, pb); break;    // (3, 2), (3, 3)
       default: break;
     }
   };
   auto tiles_P2 = [&](const float* gd, int pb) {
     switch (pw) {
-      case 1: tile_P(IC<9>{}, gd, pb); tile_P(IC<1>{}, gd, pb); break;
-      case 2: tile_P(IC<3>{}, gd, pb); break;
-      case 3: tile_P(IC<4>{}, gd, pb); break;
+      case 1: tile_P_pair(IC<1>{}, IC<0>{}, gd, pb); break;    // (1, 0), (1, 1)
+      case 2: tile_P_pair(IC<0>{}, IC<0>{}, gd, pb); break;    // (0, 0)
+      case 3: tile_P_pair(IC<2>{}, IC<1>{}, gd, pb); break;    // (2, 2)
       default: break;
     }
   };
