@@ -91,6 +91,13 @@ constexpr int kTiles = kRowsPerWave / 16;        // 16-row column tiles per chai
 // hout[chunk_offset(n) + ch][hv][v][k] (chunk_offset(n) = the chunks of the
 // sequences before n), skipping slots at or past h_chunks.  The values are
 // the bf16 fragments the chain forms anyway for S Q^T.
+// Slot swizzle of the raw V rows: 16-byte chunk c of row t sits in slot
+// c ^ vsw(t).  The chain reads V with transposing 8-byte reads; a read cycle
+// serves 8 rows with 4 lanes on 32 contiguous bytes (two slots) of each, and
+// with vsw(t) = 2 (t % 8) + (t / 8) % 2 the 8 rows' slot pairs are distinct
+// (with t % 16 two rows share each pair).
+__device__ __forceinline__ int vsw(int t) { return ((t & 7) << 1) | ((t >> 3) & 1); }
+
 template <typename CuT, bool kL2, bool kH>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -185,12 +192,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
   for (int j = 0; j < kMaxGroups; ++j) {
     const int row = group_row0(j) + (lane >> 4);
-    const uint32_t slot = uint32_t((lane & 15) ^ (row & 15)) * 16u;
-    dma_qk[j] = uint32_t(row) * uint32_t(qk_stride * 2) + slot;
-    dma_v[j] = uint32_t(row) * uint32_t(v_stride * 2) + slot;
+    dma_qk[j] = uint32_t(row) * uint32_t(qk_stride * 2) + uint32_t((lane & 15) ^ (row & 15)) * 16u;
+    dma_v[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane & 15) ^ vsw(row)) * 16u;
   }
   auto copy_rows = [&](const uint16_t* src, size_t stride, size_t col0, const uint32_t* offs, int ch,
-                       uint16_t* dst) {
+                       uint16_t* dst, bool is_v) {
     const int t0 = bos + ch * C;
     const int L = chunk_len(ch);
     if (L == C) {
@@ -204,16 +210,16 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         if (j < n_groups) {
           const int row0 = group_row0(j);
           const int row = row0 + (lane >> 4);
-          const int src_chunk = (lane & 15) ^ (row & 15);
+          const int src_chunk = (lane & 15) ^ (is_v ? vsw(row) : (row & 15));
           lds_dma16(src + size_t(t0 + min(row, L - 1)) * stride + col0 + 8 * src_chunk, &dst[row0 * D]);
         }
       }
     }
   };
-  auto copy_k = [&](int ch) { copy_rows(k, qk_stride, size_t(hq) * D, dma_qk, ch, raw.k[ch & 1]); };
-  auto copy_q = [&](int ch) { copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1]); };
+  auto copy_k = [&](int ch) { copy_rows(k, qk_stride, size_t(hq) * D, dma_qk, ch, raw.k[ch & 1], false); };
+  auto copy_q = [&](int ch) { copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1], false); };
   auto copy_kq = [&](int ch) { copy_k(ch); copy_q(ch); };
-  auto copy_v = [&](int ch) { copy_rows(v, v_stride, size_t(hv) * D, dma_v, ch, rawV); };
+  auto copy_v = [&](int ch) { copy_rows(v, v_stride, size_t(hv) * D, dma_v, ch, rawV, true); };
   // L2-norm factors of the 4 n_groups rows this wave copied into buf, from the
   // diagonal of their Gram matrix: two 16-row tiles, each one bf16 MFMA chain
   // with the same registers as both operands (squares exact, fp32 sums).  Tile
@@ -602,7 +608,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
             for (int tb = 0; tb < 4; ++tb) {
               const int t = 16 * tb + 4 * g + m;
               vv[u][tb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (__attribute__((address_space(3))) i16x4_t*)&rawV[t * D + 8 * ((col >> 3) ^ (t & 15)) + (col & 7)]);
+                  (__attribute__((address_space(3))) i16x4_t*)&rawV[t * D + 8 * ((col >> 3) ^ vsw(t)) + (col & 7)]);
             }
           }
         }
@@ -805,14 +811,23 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
             for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(OT[u][tb]));
           // The chunk's output tile is staged in the raw Q buffer of this chunk
           // (last read in P2; the Q copy of chunk ch+2 goes there in P1 of the
-          // next iteration), in the raw row layout: token t, 4 columns per lane
-          // (one 8-byte write); P3b stores whole rows from it.
+          // next iteration), in the raw row layout; P3b stores whole rows from
+          // it.  Lane (g, c) holds columns v0 + 16 u + 4 g .. +3 of token
+          // 16 tb + c in tile u; v_permlane16_swap trades tile 1 of the even
+          // 16-lane rows for tile 0 of the odd rows, which leaves the lane 8
+          // adjacent columns v0 + 16 (g % 2) + 8 (g / 2) .. +7 (tile g % 2): one
+          // 16-byte write, where two 8-byte writes down 16 rows meet in the
+          // LDS banks.
+          static_assert(kTiles == 2, "two column tiles per chain wave");
 #pragma unroll
-          for (int u = 0; u < kTiles; ++u)
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
-              *reinterpret_cast<uint2*>(&raw.q[kb_buf][raw_off(16 * tb + c, v0 + 16 * u + 4 * g)]) =
-                  uint2{cvt_pk_bf16(OT[u][tb][0], OT[u][tb][1]), cvt_pk_bf16(OT[u][tb][2], OT[u][tb][3])};
+          for (int tb = 0; tb < 4; ++tb) {
+            const uint32_t a0 = cvt_pk_bf16(OT[0][tb][0], OT[0][tb][1]), a1 = cvt_pk_bf16(OT[0][tb][2], OT[0][tb][3]);
+            const uint32_t b0 = cvt_pk_bf16(OT[1][tb][0], OT[1][tb][1]), b1 = cvt_pk_bf16(OT[1][tb][2], OT[1][tb][3]);
+            const auto s0 = __builtin_amdgcn_permlane16_swap(a0, b0, false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(a1, b1, false, false);
+            *reinterpret_cast<u32x4_t*>(&raw.q[kb_buf][raw_off(16 * tb + c, v0 + 16 * (g & 1) + 8 * (g >> 1))]) =
+                u32x4_t{s0[0], s1[0], s0[1], s1[1]};
+          }
           asm volatile("" ::: "memory");
         }
         if (half == 1) {
