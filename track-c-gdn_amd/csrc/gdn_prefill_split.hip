@@ -342,38 +342,61 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
       *reinterpret_cast<f32x4*>(&sA[(16 * ti + c) * ALD + 16 * tj + 4 * g]) = val;
     }
   };
-  // P tile = scale tril_incl(e^{gam_i - gam_j} Q K^T), formed transposed like
-  // the A tiles; |scale| enters the exponent, its sign the product.
-  auto tile_P = [&](auto tile_c) {
-    constexpr int ti = Tile16<decltype(tile_c)::value>::ti;
-    constexpr int tj = Tile16<decltype(tile_c)::value>::tj;
-    bf16x8_t fa[4], fb[4];
+  // P tiles = scale tril_incl(e^{gam_i - gam_j} Q K^T), formed transposed like
+  // the A tiles; |scale| enters the exponent, its sign the product.  The
+  // tiles (ti, 2 s) and (ti, 2 s + 1) are formed together and their 8 p32
+  // positions 32 s + 8 g .. +7 of row 16 ti + c go out as one 16-byte write
+  // per lane (two 8-byte writes down 16 rows meet in the LDS banks); a tile
+  // above the diagonal is written as zeros.
+  auto tile_P_pair = [&](auto ti_c, auto s_c) {
+    constexpr int ti = decltype(ti_c)::value;
+    constexpr int tj0 = 2 * decltype(s_c)::value, tj1 = tj0 + 1;
+    constexpr bool two = tj1 <= ti;
+    bf16x8_t fa[4], fb0[4], fb1[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       fa[ks] = ld16_bf(&rq[raw_lane[ks] + 16 * ti * D]);
-      fb[ks] = ld16_bf(&rk[raw_lane[ks] + 16 * tj * D]);
+      fb0[ks] = ld16_bf(&rk[raw_lane[ks] + 16 * tj0 * D]);
+      if constexpr (two) fb1[ks] = ld16_bf(&rk[raw_lane[ks] + 16 * tj1 * D]);
     }
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16_bf(fb[ks], fa[ks], acc);
-    if (neg_scale) acc = -acc;
+    for (int ks = 0; ks < 4; ++ks) {
+      acc0 = mfma16_bf(fb0[ks], fa[ks], acc0);
+      if constexpr (two) acc1 = mfma16_bf(fb1[ks], fa[ks], acc1);
+    }
+    if (neg_scale) {
+      acc0 = -acc0;
+      acc1 = -acc1;
+    }
     const float gr = gd[G_L2 + 16 * ti + c] + scale_l2;
-    const f32x4 gcol = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj + 4 * g]);
-    if constexpr (kL2) acc *= nq[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk[16 * tj + 4 * g]);
-    f16x4_t val;
+    const f32x4 gcol0 = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj0 + 4 * g]);
+    f32x4 gcol1 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (two) gcol1 = *reinterpret_cast<const f32x4*>(&gd[G_L2 + 16 * tj1 + 4 * g]);
+    if constexpr (kL2) {
+      acc0 *= nq[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk[16 * tj0 + 4 * g]);
+      if constexpr (two) acc1 *= nq[16 * ti + c] * *reinterpret_cast<const f32x4*>(&nk[16 * tj1 + 4 * g]);
+    }
+    f16x8 val;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float x = __builtin_amdgcn_exp2f(gr - gcol[i]) * acc[i];
-      if (ti == tj) x = (c >= 4 * g + i) ? x : 0.f;
-      val[i] = (_Float16)x;
+      float x0 = __builtin_amdgcn_exp2f(gr - gcol0[i]) * acc0[i];
+      if (ti == tj0) x0 = (c >= 4 * g + i) ? x0 : 0.f;
+      val[i] = (_Float16)x0;
+      float x1 = 0.f;
+      if constexpr (two) {
+        x1 = __builtin_amdgcn_exp2f(gr - gcol1[i]) * acc1[i];
+        if (ti == tj1) x1 = (c >= 4 * g + i) ? x1 : 0.f;
+      }
+      val[4 + i] = (_Float16)x1;
     }
-    *reinterpret_cast<f16x4_t*>(&sP[(16 * ti + c) * TLD + 32 * (tj >> 1) + 8 * g + 4 * (tj & 1)]) = val;
+    *reinterpret_cast<f16x8*>(&sP[(16 * ti + c) * TLD + 16 * tj0 + 8 * g]) = val;
   };
-  switch (wave) {
-    case 0: tile_A(IC<0>{}); tile_A(IC<4>{}); tile_A(IC<8>{}); tile_P(IC<0>{}); tile_P(IC<4>{}); break;
-    case 1: tile_A(IC<1>{}); tile_A(IC<5>{}); tile_A(IC<9>{}); tile_P(IC<1>{}); tile_P(IC<5>{}); break;
-    case 2: tile_A(IC<2>{}); tile_A(IC<6>{}); tile_P(IC<2>{}); tile_P(IC<6>{}); tile_P(IC<8>{}); break;
-    default: tile_A(IC<3>{}); tile_A(IC<7>{}); tile_P(IC<3>{}); tile_P(IC<7>{}); tile_P(IC<9>{}); break;
+  switch (wave) {   // P tile pairs: (1, 0) (1, 1); (2, 0) (2, 1); (3, 0) (3, 1) and (0, 0); (3, 2) (3, 3) and (2, 2)
+    case 0: tile_A(IC<0>{}); tile_A(IC<4>{}); tile_A(IC<8>{}); tile_P_pair(IC<1>{}, IC<0>{}); break;
+    case 1: tile_A(IC<1>{}); tile_A(IC<5>{}); tile_A(IC<9>{}); tile_P_pair(IC<2>{}, IC<0>{}); break;
+    case 2: tile_A(IC<2>{}); tile_A(IC<6>{}); tile_P_pair(IC<3>{}, IC<0>{}); tile_P_pair(IC<0>{}, IC<0>{}); break;
+    default: tile_A(IC<3>{}); tile_A(IC<7>{}); tile_P_pair(IC<3>{}, IC<1>{}); tile_P_pair(IC<2>{}, IC<1>{}); break;
   }
   __syncthreads();
 
