@@ -279,18 +279,27 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 
   // ---------------- preparation steps (state-independent)
   // Raw bf16 K rows of chunk ch -> fp16 operand rows Kc[ch & 1] [t][p32(k)],
-  // rows t >= L -> 0, by preparation waves 1-3: items (row, 8-column piece)
-  // ptid - 64 + 192 j, j = 0..5, below 1024.  Their LDS offsets are fixed per
-  // lane and computed once; columns cc + 4.. land 8 halves after cc.. (p32).
+  // rows t >= L -> 0, by preparation waves 1-3: items ptid - 64 + 192 j,
+  // j = 0..5, below 1024.  Item i fills the 16 bytes 8 s .. 8 s + 7 (p32
+  // positions, s = i % 16) of row cv_row(i / 16): columns 32 (s / 4) + 4 (s % 4)
+  // .. +3 and the same + 16, two 8-byte pieces of the raw row (16-byte slots
+  // 2 apart, so the second offset is the first ^ 32 bytes).  cv_row swaps the
+  // two low bits of the row index: a read cycle of 32 lanes covers rows r and
+  // r + 2, whose swizzled slot sets are disjoint (rows r and r + 1 share
+  // theirs), and every write is 16 bytes: no LDS bank conflicts either way.
   constexpr int kCvThreads = kPrepThreads - 64;
   constexpr int kCvItems = (C * (D / 8) + kCvThreads - 1) / kCvThreads;   // 6
+  auto cv_row = [](int item) {
+    const int r = item >> 4;
+    return (r & ~3) | ((r & 1) << 1) | ((r >> 1) & 1);
+  };
   uint32_t cv_src[kCvItems], cv_dst[kCvItems];    // byte offsets into a raw K buffer / a Kc buffer
 #pragma unroll
   for (int j = 0; j < kCvItems; ++j) {
     const int item = (ptid - 64) + kCvThreads * j;
-    const int row = item >> 4, cc = (item & 15) * 8;
-    cv_src[j] = uint32_t(raw_off(row, cc)) * 2u;
-    cv_dst[j] = uint32_t(row * KCLD + p32(cc)) * 2u;
+    const int row = cv_row(item), sl = item & 15;
+    cv_src[j] = uint32_t(raw_off(row, 32 * (sl >> 2) + 4 * (sl & 3))) * 2u;
+    cv_dst[j] = uint32_t(row * KCLD + 8 * sl) * 2u;
   }
   auto convert_k = [&](int ch) {
     const char* src = reinterpret_cast<const char*>(raw.k[ch & 1]);
@@ -299,22 +308,23 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
     for (int j = 0; j < kCvItems; ++j) {
       if (j == kCvItems - 1 && (ptid - 64) + kCvThreads * j >= C * (D / 8)) break;   // uniform per wave
-      uint4 w = *reinterpret_cast<const uint4*>(src + cv_src[j]);
+      uint2 wa = *reinterpret_cast<const uint2*>(src + cv_src[j]);
+      uint2 wb = *reinterpret_cast<const uint2*>(src + (cv_src[j] ^ 32u));
       if (L < C) {
-        const uint32_t m = ((ptid - 64) + kCvThreads * j) / 16 < L ? 0xffffffffu : 0u;
-        w.x &= m; w.y &= m; w.z &= m; w.w &= m;
+        const uint32_t m = cv_row((ptid - 64) + kCvThreads * j) < L ? 0xffffffffu : 0u;
+        wa.x &= m; wa.y &= m; wb.x &= m; wb.y &= m;
       }
       float f[8];
-      unpack_bf16x2(w.x, f[0], f[1]); unpack_bf16x2(w.y, f[2], f[3]);
-      unpack_bf16x2(w.z, f[4], f[5]); unpack_bf16x2(w.w, f[6], f[7]);
+      unpack_bf16x2(wa.x, f[0], f[1]); unpack_bf16x2(wa.y, f[2], f[3]);
+      unpack_bf16x2(wb.x, f[4], f[5]); unpack_bf16x2(wb.y, f[6], f[7]);
       if constexpr (kL2) {
-        const float r = nk(ch & 1)[((ptid - 64) + kCvThreads * j) / 16];
+        const float r = nk(ch & 1)[cv_row((ptid - 64) + kCvThreads * j)];
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] *= r;
       }
-      _Float16* d = reinterpret_cast<_Float16*>(dst + cv_dst[j]);
-      *reinterpret_cast<f16x4_t*>(d) = f16x4_t{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
-      *reinterpret_cast<f16x4_t*>(d + 8) = f16x4_t{(_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
+      *reinterpret_cast<f16x8*>(dst + cv_dst[j]) =
+          f16x8{(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3],
+                (_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
     }
   };
   // Per-lane swizzled offsets of the 8-column pieces this lane reads from a
