@@ -26,7 +26,7 @@ namespace {
 using namespace gdn;
 
 constexpr int kConvThreads = 256;
-constexpr int kConvTile = 32;        // tokens per lane in the prefill kernel
+constexpr int kConvTile = 64;        // tokens per lane in the prefill kernel
 constexpr int kMaxConvWidth = 4;
 constexpr int kMaxStateLen = 8;
 
