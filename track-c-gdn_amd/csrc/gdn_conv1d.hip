@@ -186,7 +186,7 @@ __global__ __launch_bounds__(kConvThreads) void gdn_qkv_conv1d_kernel(
 // and written back in place.  A slot outside [0, pool) leaves the state
 // untouched and yields a zero output row.  The state length S is a
 // compile-time W - 1 or W.
-constexpr int kUpdSeqs = 4;
+constexpr int kUpdSeqs = 8;
 
 template <int W, int S, bool kSilu>
 __global__ __launch_bounds__(kConvThreads) void gdn_qkv_conv1d_update_kernel(
