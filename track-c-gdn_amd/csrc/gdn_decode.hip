@@ -35,6 +35,11 @@ constexpr int kRowsPerLane = kRowsPerWave / 4;    // 4 (4 DPP rows per wave)
 constexpr int kThreadsPerHead = kWavesPerHead * kWave;
 static_assert(kRowsPerLane == 4, "v is read and o written as 4 bf16 per lane");
 constexpr int kTokBlock = 16;     // tokens staged in LDS at a time (multi-token decode)
+// Multi-token decode: 2 state rows per lane, so a workgroup of 8 waves holds
+// half a head (64 rows) and kMHeadParts = 2 workgroups share one (n, v-head).
+constexpr int kMRowsPerLane = 2;
+constexpr int kMHeadParts = kRowsPerLane / kMRowsPerLane;
+constexpr int kMRowsPerWave = 4 * kMRowsPerLane;   // 4 DPP rows per wave
 
 template <bool kNonTemporal>
 __device__ __forceinline__ f32x4 load_state(const f32x4* p) {
@@ -173,35 +178,37 @@ __global__ __launch_bounds__(kThreadsPerHead, kL2 ? 6 : 8) void gdn_decode_kerne
 // arithmetic is the single-step kernel's, in the same order, so T steps here
 // give the same bits as T launches of gdn_decode_kernel.
 template <bool kNonTemporal>
-__global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
+__global__ __launch_bounds__(kThreadsPerHead, 8) void gdn_decode_multi_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* state_in, float* state_out,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     uint16_t* __restrict__ out, int T, int HQ, int HV, float scale, int flags) {
   const int ratio = HV / HQ;
-  const int n = blockIdx.x / HV;
-  const int hv = blockIdx.x - n * HV;
+  const int part = blockIdx.x % kMHeadParts;
+  const int nh = blockIdx.x / kMHeadParts;
+  const int n = nh / HV;
+  const int hv = nh - n * HV;
   const int hq = hv / ratio;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int row0 = (wave % kWavesPerHead) * kRowsPerWave;
+  const int row0 = part * (D / kMHeadParts) + (wave % kWavesPerHead) * kMRowsPerWave;
   const int rsub = lane >> 4;
   const int c = lane & 15;
-  const int rbase = row0 + rsub * kRowsPerLane;
+  const int rbase = row0 + rsub * kMRowsPerLane;
   const size_t sbase = (size_t(n) * HV + hv) * size_t(D) * D;
 
-  f32x4 s[kRowsPerLane][2];
+  f32x4 s[kMRowsPerLane][2];
   if (state_in != nullptr) {
     const float* sp = state_in + sbase + size_t(rbase) * D;
 #pragma unroll
-    for (int j = 0; j < kRowsPerLane; ++j) {
+    for (int j = 0; j < kMRowsPerLane; ++j) {
       s[j][0] = load_state<kNonTemporal>(reinterpret_cast<const f32x4*>(sp + j * D + 4 * c));
       s[j][1] = load_state<kNonTemporal>(reinterpret_cast<const f32x4*>(sp + j * D + 64 + 4 * c));
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < kRowsPerLane; ++j) {
+    for (int j = 0; j < kMRowsPerLane; ++j) {
       s[j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
       s[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -271,26 +278,26 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
     }
     __syncthreads();
     for (int t = 0; t < nt; ++t) {
-      float kk[8], vv[kRowsPerLane];
+      float kk[8], vv[kMRowsPerLane];
       float qq[8];
       {
         const f32x4 k0 = *reinterpret_cast<const f32x4*>(&tk[t][0][4 * c]);
         const f32x4 k1 = *reinterpret_cast<const f32x4*>(&tk[t][0][64 + 4 * c]);
         const f32x4 q0 = *reinterpret_cast<const f32x4*>(&tk[t][1][4 * c]);
         const f32x4 q1 = *reinterpret_cast<const f32x4*>(&tk[t][1][64 + 4 * c]);
-        const f32x4 vw = *reinterpret_cast<const f32x4*>(&tk[t][2][rbase]);
+        const float2 vw = *reinterpret_cast<const float2*>(&tk[t][2][rbase]);
         kk[0] = k0.x; kk[1] = k0.y; kk[2] = k0.z; kk[3] = k0.w;
         kk[4] = k1.x; kk[5] = k1.y; kk[6] = k1.z; kk[7] = k1.w;
         qq[0] = q0.x; qq[1] = q0.y; qq[2] = q0.z; qq[3] = q0.w;
         qq[4] = q1.x; qq[5] = q1.y; qq[6] = q1.z; qq[7] = q1.w;
-        vv[0] = vw.x; vv[1] = vw.y; vv[2] = vw.z; vv[3] = vw.w;
+        vv[0] = vw.x; vv[1] = vw.y;
       }
       const float g = tab[t][0];
       const float beta = tab[t][1];
       const float kq = tab[t][2];
-      float o_out[kRowsPerLane];
+      float o_out[kMRowsPerLane];
 #pragma unroll
-      for (int j = 0; j < kRowsPerLane; ++j) {
+      for (int j = 0; j < kMRowsPerLane; ++j) {
         float x[8] = {s[j][0].x, s[j][0].y, s[j][0].z, s[j][0].w,
                       s[j][1].x, s[j][1].y, s[j][1].z, s[j][1].w};
         float pk = 0.f, pq = 0.f;
@@ -309,17 +316,14 @@ __global__ __launch_bounds__(kThreadsPerHead, 5) void gdn_decode_multi_kernel(
         s[j][0] = f32x4{x[0], x[1], x[2], x[3]};
         s[j][1] = f32x4{x[4], x[5], x[6], x[7]};
       }
-      if (c == 0) {
-        uint2 w;
-        w.x = pack_bf16x2(o_out[0], o_out[1]);
-        w.y = pack_bf16x2(o_out[2], o_out[3]);
-        *reinterpret_cast<uint2*>(out + ((size_t(n) * T + t0 + t) * HV + hv) * D + rbase) = w;
-      }
+      if (c == 0)
+        *reinterpret_cast<uint32_t*>(out + ((size_t(n) * T + t0 + t) * HV + hv) * D + rbase) =
+            pack_bf16x2(o_out[0], o_out[1]);
     }
   }
   float* dst = state_out + sbase + size_t(rbase) * D;
 #pragma unroll
-  for (int j = 0; j < kRowsPerLane; ++j) {
+  for (int j = 0; j < kMRowsPerLane; ++j) {
     store_state<kNonTemporal>(reinterpret_cast<f32x4*>(dst + j * D + 4 * c), s[j][0]);
     store_state<kNonTemporal>(reinterpret_cast<f32x4*>(dst + j * D + 64 + 4 * c), s[j][1]);
   }
@@ -359,7 +363,7 @@ int launch_decode_multi(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         const uint16_t* a, const float* dt_bias, const uint16_t* b, uint16_t* out,
                         int B, int T, int HQ, int HV, float scale, int flags, void* stream) {
   if (B == 0) return GDN_OK;
-  const dim3 grid(unsigned(B) * unsigned(HV));
+  const dim3 grid(unsigned(B) * unsigned(HV) * kMHeadParts);
   const dim3 block(kThreadsPerHead);
   hipLaunchKernelGGL(gdn_decode_multi_kernel<true>, grid, block, 0, static_cast<hipStream_t>(stream),
                      q, k, v, state_in, state_out, A_log, a, dt_bias, b, out, T, HQ, HV, scale,
