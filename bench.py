@@ -185,7 +185,35 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk
     return dict(total_ms=total_ms, kernel_ms=kern_ms, T=T, N=N, lens=lens, HQ=w["HQ"],
                 HV=w["HV"], flops=prefill_flops(T, w["HV"]),
                 flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True),
-                path=gpre.auto_path(N, w["HV"]))
+                path=call.path)
+
+
+# Fused prefill over sequences of one length, qk16/v32: the chunk period at
+# 32 / 128 / 256 chains, and the launch's fixed cost (one chunk per chain).
+OCCUPANCY_WORKLOADS = (("1x5348", [5348]), ("4x5348", [5348] * 4), ("8x5348", [5348] * 8),
+                       ("8x64", [64] * 8))
+
+
+def bench_prefill_occupancy(dev, steps, warmup, HQ=16, HV=32):
+    res = {}
+    for tag, lens in OCCUPANCY_WORKLOADS:
+        x = ginp.prefill_inputs(lens, HQ, HV, seed=1004, with_state=True)
+        g = _to(x, dev)
+        T, N = sum(lens), len(lens)
+        out = torch.empty(T, HV, D, dtype=torch.bfloat16, device=dev)
+        fs = torch.empty(N, HV, D, D, dtype=torch.float32, device=dev)
+        args = [g[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b",
+                               "cu_seqlens")]
+        _, kern_ms = timed_launches(
+            lambda i: gpre.gdn_prefill(*args, g["scale"], output=out, final_state=fs,
+                                       validate=False, path="fused"), steps, warmup)
+        chunks = max((n + C - 1) // C for n in lens)
+        res[tag] = {"chains": N * HV, "chunks_per_chain": chunks,
+                    "kernel_us": round(kern_ms * 1e3, 2),
+                    "us_per_chunk": round(kern_ms * 1e3 / chunks, 3)}
+        print(f"# occupancy {tag}: {N * HV} chains, {kern_ms * 1e3:.1f} us, "
+              f"{kern_ms * 1e3 / chunks:.2f} us per chunk", file=sys.stderr, flush=True)
+    return res
 
 
 def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
@@ -451,8 +479,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--prefill-steps", type=int, default=30)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "conv", "backward"],
-                    default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "conv", "backward",
+                                       "occupancy"],
+                    default="all",
+                    help="occupancy (never part of 'all'): the fused prefill's chunk period at "
+                         "32 / 128 / 256 chains of equal length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-latency", action="store_true",
                     help="skip the end-to-end run() latency measurements")
@@ -630,6 +661,10 @@ def main():
                                       "bytes_per_launch": r["bytes"]}}
             print(f"# {key}: {r['kernel_ms'] * 1e3:.1f} us, {gbs:.0f} GB/s "
                   f"({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)", file=sys.stderr, flush=True)
+
+    if args.only == "occupancy":
+        line["prefill_occupancy"] = bench_prefill_occupancy(dev, args.prefill_steps,
+                                                            PREFILL_WARMUP)
 
     if args.only == "all" and not args.no_latency:
         kus = {"decode_b256_qk4_v8": line.get("roofline", {}).get("kernel_us"),

@@ -173,6 +173,24 @@ int gdn_prefill_ex_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
 int gdn_prefill_auto_slices(int N, int HV);
 
 /*
+ * The path choice from the sequence lengths, for callers that hold
+ * cu_seqlens on the host (reads a HOST copy, N+1 entries): 8 or 4 state
+ * slices per chain (gdn_prefill_split_fwd) or 0 (the fused chain kernel:
+ * gdn_prefill_ex_fwd without a workspace), whichever a cost model of the
+ * launches (cycles per chunk of each kernel measured on MI355X, the split
+ * path's preparation per (chunk, v-head), the slice workgroups scheduled
+ * longest sequence first on `cus` CUs, one per CU) finishes first.  Only
+ * batches of at most one chain per CU are considered for the split path.
+ * `cus` <= 0: the current device's CU count.  -1 on a NULL pointer or
+ * negative N / T or HV <= 0.  gdn_prefill_auto_slices decides from N and HV
+ * alone and may pick the split path where the fused kernel is faster (four
+ * 5348-token sequences at 32 v-heads: split 390 us, fused 267 us).  No
+ * reference counterpart (the reference has one path).
+ */
+int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int N, int T, int HV,
+                              int cus);
+
+/*
  * Workspace bytes of gdn_prefill_split_fwd: 14 080 bytes per (chunk, v-head)
  * and 18 432 per (chunk, qk-head) for an upper bound of T / 64 + N chunks,
  * plus the sequences' launch order (N ints, rounded up to 256 bytes).

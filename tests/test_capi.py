@@ -26,7 +26,7 @@ def test_header_declares_expected_entry_points():
         "gdn_prefill_split_workspace_bytes", "gdn_prefill_split_fwd", "gdn_prefill_auto_slices",
         "gdn_prefill_split_noalloc_max_bytes", "gdn_prefill_split_noalloc_fwd",
         "gdn_qkv_conv1d_fwd", "gdn_qkv_conv1d_update", "gdn_prefill_bwd_workspace_bytes",
-        "gdn_prefill_bwd", "gdn_gate_bwd"])
+        "gdn_prefill_bwd", "gdn_gate_bwd", "gdn_prefill_choose_slices"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -99,3 +99,41 @@ def test_chunk_count_matches_chunk_offsets(seed):
                  for i in range(bad.numel() - 1))
     n = lib.gdn_prefill_chunk_count(bad.data_ptr(), 0, bad.numel() - 1, T)
     assert n == expect
+
+
+def _choose(lens, HV, cus=256, dt=None):
+    import torch
+    lib = pkg_module("_capi").lib()
+    cu = torch.tensor([0] + list(__import__("itertools").accumulate(lens)),
+                      dtype=dt or torch.int64)
+    return lib.gdn_prefill_choose_slices(cu.data_ptr(), int(cu.dtype == torch.int32),
+                                         cu.numel() - 1, int(cu[-1]), HV, cus)
+
+
+def test_choose_slices_on_measured_batches():
+    """The length-aware path choice on batches whose three options were timed
+    on MI355X (256 CUs): one 4096-token sequence at qk4/v8 (split 8 slices
+    78 us, 4 slices 94 us, fused 199 us); 16 varlen sequences at qk4/v8
+    (4 slices 279 us, 8 slices 400 us, fused ~370 us); one 5348-token
+    sequence at qk16/v32 (8 slices 129 us, fused 257 us); four of them
+    (fused 267 us, 4 slices 390 us); the 8-sequence 32k batch (fused)."""
+    inp = pkg_module("inputs")
+    assert _choose([4096], 8) == 8
+    assert _choose([4096], 8, dt=__import__("torch").int32) == 8
+    assert _choose(inp.workload_lengths("prefill_varlen16_qk4_v8"), 8) == 4
+    assert _choose([5348], 32) == 8
+    assert _choose([5348] * 4, 32) == 0
+    assert _choose(inp.workload_lengths("prefill_varlen8_t32768_qk16_v32"), 32) == 0
+    # past one chain per CU: always the fused kernel
+    assert _choose([100] * 64, 8) == 0
+
+
+def test_choose_slices_edges():
+    import torch
+    lib = pkg_module("_capi").lib()
+    assert lib.gdn_prefill_choose_slices(None, 0, 1, 64, 8, 256) == -1
+    cu = torch.zeros(1, dtype=torch.int64)
+    assert lib.gdn_prefill_choose_slices(cu.data_ptr(), 0, 0, 0, 8, 256) == 0
+    assert lib.gdn_prefill_choose_slices(cu.data_ptr(), 0, 0, 0, 0, 256) == -1
+    # empty sequences only: no chunks; any answer is valid, none may fail
+    assert _choose([0, 0, 0], 8) in (0, 4, 8)

@@ -47,6 +47,7 @@ SIGNATURES = {
     "gdn_prefill_split_noalloc_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                                            _F, _P, _P, _I, _I, _P]),
     "gdn_prefill_chunk_count": (ctypes.c_longlong, [_P, _I, _I, _I]),
+    "gdn_prefill_choose_slices": (_I, [_P, _I, _I, _I, _I, _I]),
     "gdn_qkv_conv1d_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I,
                                 _I, _P]),
     "gdn_qkv_conv1d_update": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _I,

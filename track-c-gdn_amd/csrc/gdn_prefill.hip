@@ -40,6 +40,11 @@
 #include "gdn_prefill_split.h"
 #include "../../include/gdn_hip.h"
 
+#include <algorithm>
+#include <functional>
+#include <queue>
+#include <vector>
+
 namespace {
 
 using namespace gdn;
@@ -1136,6 +1141,69 @@ extern "C" int gdn_prefill_split_noalloc_fwd(const uint16_t* q, const uint16_t* 
   return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
                                    T, HQ, HV, scale, out, final_state, slices, ws, flags,
                                    static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+// Cost model of gdn_prefill_choose_slices, in GPU cycles measured on MI355X
+// (qk16/v32 and qk4/v8 batches): per chunk of a chain, the fused kernel 7 600,
+// the slice kernel 2 550 with 16 state rows (8 slices) and 3 600 with 32 rows
+// (4 slices, the GPU filled); the split path's preparation launch 25 cycles per
+// (chunk, v-head) on 256 CUs (scaled by 256 / CUs); either path's start-up
+// about 24 000 cycles.
+constexpr double kFusedChunkCycles = 7600.0;
+constexpr double kSlice8ChunkCycles = 2550.0;
+constexpr double kSlice4ChunkCycles = 3600.0;
+constexpr double kPrepUnitCycles256 = 25.0 * 256.0;
+constexpr double kStartupCycles = 24000.0;
+
+// Finish time of workgroups that each hold one CU for `chunks * period`
+// cycles, started in the given order as CUs free up, `per_seq` workgroups
+// per sequence.
+double makespan(const std::vector<int>& chunks, int per_seq, double period, int cus) {
+  std::priority_queue<double, std::vector<double>, std::greater<double>> cu_free;
+  for (int i = 0; i < cus; ++i) cu_free.push(0.0);
+  double end = 0.0;
+  for (int n : chunks)
+    for (int j = 0; j < per_seq; ++j) {
+      const double t = cu_free.top() + n * period;
+      cu_free.pop();
+      cu_free.push(t);
+      end = std::max(end, t);
+    }
+  return end;
+}
+
+}  // namespace
+
+extern "C" int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int N, int T,
+                                         int HV, int cus) {
+  if (!cu_seqlens_host || N < 0 || T < 0 || HV <= 0) return -1;
+  if (cus <= 0) cus = gdn::device_cus();
+  const long long chains = (long long)N * HV;
+  // Past one chain per CU the fused kernel fills the GPU and the split path
+  // would need 4 or 8 times as many workgroups.
+  if (N == 0 || cus <= 0 || chains > cus) return 0;
+  std::vector<int> chunks(N);
+  double units = 0.0;
+  for (int m = 0; m < N; ++m) {
+    int bm, lm;
+    if (cu_is_int32) seq_bounds(static_cast<const int32_t*>(cu_seqlens_host), m, T, bm, lm);
+    else seq_bounds(static_cast<const int64_t*>(cu_seqlens_host), m, T, bm, lm);
+    chunks[m] = (lm + C - 1) / C;
+    units += double(chunks[m]) * HV;
+  }
+  // one fused workgroup per chain, all resident at once (chains <= CUs)
+  const double fused = kStartupCycles + *std::max_element(chunks.begin(), chunks.end()) *
+                                            kFusedChunkCycles;
+  // the slice launch takes the sequences longest first
+  std::sort(chunks.begin(), chunks.end(), std::greater<int>());
+  const double prep = std::max(kStartupCycles, units * kPrepUnitCycles256 / cus);
+  const double split8 = prep + makespan(chunks, HV * 8, kSlice8ChunkCycles, cus);
+  const double split4 = prep + makespan(chunks, HV * 4, kSlice4ChunkCycles, cus);
+  if (split8 <= split4 && split8 < fused) return 8;
+  if (split4 < fused) return 4;
+  return 0;
 }
 
 extern "C" long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, int N,

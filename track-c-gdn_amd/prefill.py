@@ -45,11 +45,12 @@ def _resolve_scale(scale) -> float:
 
 def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                     num_q_heads: int = NUM_Q_HEADS, num_v_heads: int = NUM_V_HEADS,
-                    check_total: bool = True) -> None:
+                    check_total: bool = True) -> Optional[torch.Tensor]:
     """The checks of PRE:1635-1667, raising AssertionError before any launch.
 
     ``check_total`` keeps the reference's ``cu_seqlens[-1] == T`` check
-    (PRE:1665), which reads one value back to the host.
+    (PRE:1665) and returns the host copy of ``cu_seqlens`` it reads for it
+    (one device-to-host copy); else None.
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda
     assert A_log.is_cuda and a.is_cuda and dt_bias.is_cuda and b.is_cuda and cu_seqlens.is_cuda
@@ -71,10 +72,13 @@ def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
     assert b.shape == (q.shape[0], num_v_heads)
     assert cu_seqlens.dtype in (torch.int64, torch.int32)
     assert cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 1
-    if check_total:
-        assert int(cu_seqlens[-1].item()) == q.shape[0]
     if state is not None:
         assert state.shape == (cu_seqlens.numel() - 1, num_v_heads, HEAD_SIZE, HEAD_SIZE)
+    if check_total:
+        cu_host = cu_seqlens.detach().to("cpu").contiguous()
+        assert int(cu_host[-1]) == q.shape[0]
+        return cu_host
+    return None
 
 
 def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
@@ -88,6 +92,19 @@ def auto_path(N: int, HV: int) -> str:
     v-heads on the current device: ``"fused"`` or ``"split<slices>"``."""
     s = int(_capi.lib().gdn_prefill_auto_slices(N, HV))
     return f"split{s}" if s > 0 else "fused"
+
+
+def choose_slices(cu_host: torch.Tensor, T: int, HV: int) -> int:
+    """Path choice from the sequence lengths (``cu_host``: ``cu_seqlens`` in
+    host memory): 8 or 4 state slices per chain (the split path) or 0 (the
+    fused chain kernel), whichever the library's cost model of the launches
+    on the current device finishes first (``gdn_prefill_choose_slices``)."""
+    cu = cu_host.contiguous()
+    assert not cu.is_cuda and cu.dtype in (torch.int64, torch.int32) and cu.dim() == 1
+    s = int(_capi.lib().gdn_prefill_choose_slices(
+        cu.data_ptr(), 1 if cu.dtype == torch.int32 else 0, cu.numel() - 1, int(T), int(HV), 0))
+    assert s in (0, 4, 8), s
+    return s
 
 
 def split_workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
@@ -124,10 +141,11 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     (``NT = num_chunks(cu_seqlens, T)``), also receives the state entering
     every chunk; the output and final state are the same bit for bit.
 
-    ``path`` selects the kernels: ``"auto"`` (the library's choice: the split
-    path -- a parallel chunk-preparation launch and ``HV * N * slices`` state
-    slices -- when the chains alone leave CUs idle, else the fused chain
-    kernel), ``"fused"`` (one workgroup per chain) or ``"split"`` with
+    ``path`` selects the kernels: ``"auto"`` (the split path -- a parallel
+    chunk-preparation launch and ``HV * N * slices`` state slices -- or the
+    fused chain kernel, whichever :func:`choose_slices` expects to finish
+    first for these sequence lengths; with ``validate=False`` the lengths are
+    not read and the library decides from N and HV alone), ``"fused"`` (one workgroup per chain) or ``"split"`` with
     ``slices`` in (4, 8) state slices per chain.  Without ``qk_l2norm`` the
     two paths perform the state-path operations in the same order: their
     final states agree bit for bit but for rare last-place differences (one
@@ -138,18 +156,19 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     above normalised q / k and states of ordinary size; the reference's bf16
     intermediates reach 3e38).
     """
-    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, q.shape[1], v.shape[1],
-                    check_total=validate)
+    cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, q.shape[1],
+                              v.shape[1], check_total=validate)
     return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
                    final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h,
-                   path=path, slices=slices)
+                   path=path, slices=slices, cu_host=cu_host)
 
 
 def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, output=None,
             final_state=None, workspace=None, qk_l2norm: bool = False, h=None,
-            path: str = "auto", slices: int = 8):
+            path: str = "auto", slices: int = 8, cu_host: Optional[torch.Tensor] = None):
     """Allocation, layout and the C call behind :func:`gdn_prefill` (inputs
-    already validated)."""
+    already validated; ``cu_host``, when given, is the host copy of
+    ``cu_seqlens`` the automatic path choice reads)."""
     T, nq, d = q.shape
     nv = v.shape[1]
     assert nv % nq == 0
@@ -171,6 +190,9 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
     assert final_state.dtype == torch.float32 and final_state.is_contiguous()
     assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
     assert path in ("auto", "fused", "split"), path
+    if path == "auto" and h is None and cu_host is not None:
+        chosen = choose_slices(cu_host, T, nv)
+        path, slices = ("split", chosen) if chosen else ("fused", slices)
     if path == "split":
         assert h is None, "the per-chunk states are written by the fused kernel only"
         ws_need = split_workspace_bytes(N, T, nq, nv)
@@ -239,33 +261,35 @@ def gdn_prefill_h(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, 
 def run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale):
     """Reference-compatible prefill entry (PRE:1762-1802), qk4 / v8 / d128.
 
-    Validates once, as PRE:1635-1667 does (one host read of
-    ``cu_seqlens[-1]``), then launches."""
-    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
-    return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale)
+    Validates once, as PRE:1635-1667 does (one host read of ``cu_seqlens``,
+    which also feeds the path choice), then launches."""
+    cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
+    return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, cu_host=cu_host)
 
 
 @torch.no_grad()
 def run_dps(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, final_state):
     """Destination-passing prefill: writes ``output`` / ``final_state``, returns None."""
-    validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
+    cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
     _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
-            final_state=final_state)
+            final_state=final_state, cu_host=cu_host)
 
 
 class PreparedPrefill:
     """A prefill call on fixed buffers, validated once and launched by one C call.
 
     ``cu_seqlens`` is read back once here (the reference's ``cu_seqlens[-1]
-    == T`` check); ``__call__`` only enqueues the kernel on the stream that
-    was current at construction.  ``qk_l2norm`` as for :func:`gdn_prefill`.
+    == T`` check, and the path choice of :func:`choose_slices`: ``path`` is
+    ``"fused"``, ``"split4"`` or ``"split8"``); ``__call__`` only enqueues
+    the launches on the stream that was current at construction.
+    ``qk_l2norm`` as for :func:`gdn_prefill`.
     """
 
     def __init__(self, q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
                  final_state, *, qk_l2norm: bool = False):
         T, nq, _ = q.shape
         nv = v.shape[1]
-        validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv)
+        cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv)
         N = cu_seqlens.numel() - 1
         for t in (q, k, v, a, b, cu_seqlens, A_log, dt_bias):
             assert t.is_contiguous()
@@ -274,19 +298,28 @@ class PreparedPrefill:
         assert output.shape == (T, nv, HEAD_SIZE)
         assert final_state.dtype == torch.float32 and final_state.is_contiguous()
         assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
-        ws = workspace_bytes(N, T, nq, nv)
+        # the path the sequence lengths favour: 8 / 4 state slices or fused
+        self.slices = choose_slices(cu_host, T, nv) if N > 0 else 0
+        self.path = f"split{self.slices}" if self.slices else "fused"
+        ws = split_workspace_bytes(N, T, nq, nv) if self.slices else 0
         self._ws = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
         self._keep = (q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, final_state)
-        self._fn = _capi.lib().gdn_prefill_ex_fwd
-        self._args = (
+        head = (
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
             _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu_seqlens),
             1 if cu_seqlens.dtype == torch.int32 else 0, N, T, nq, nv,
-            float(_resolve_scale(scale)), _capi.ptr(output), _capi.ptr(final_state),
-            _capi.ptr(self._ws), ws, _capi.GDN_QK_L2NORM if qk_l2norm else 0,
-            _capi.stream_handle(q.device))
+            float(_resolve_scale(scale)), _capi.ptr(output), _capi.ptr(final_state))
+        tail = (_capi.ptr(self._ws), ws, _capi.GDN_QK_L2NORM if qk_l2norm else 0,
+                _capi.stream_handle(q.device))
+        if self.slices:
+            self._name = "gdn_prefill_split_fwd"
+            self._args = head + (self.slices,) + tail
+        else:
+            self._name = "gdn_prefill_ex_fwd"
+            self._args = head + tail
+        self._fn = getattr(_capi.lib(), self._name)
 
     def __call__(self) -> None:
         rc = self._fn(*self._args)
         if rc:
-            _capi.check(rc, "gdn_prefill_ex_fwd")
+            _capi.check(rc, self._name)
