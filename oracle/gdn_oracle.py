@@ -1,6 +1,6 @@
 """CPU oracle for the Gated DeltaNet (GDN) decode and prefill operators.
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker the HIP kernels are held
+TEST INFRASTRUCTURE ONLY.  This module is the oracle the HIP kernels are held
 against: only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU
 baseline leg may import it.  No product code path routes through it.
 

@@ -1,5 +1,5 @@
-"""Runs the reference-side ctypes binding printed in INTEGRATION.md, as
-written, through the plain C entry points gdn_decode_fwd and gdn_prefill_fwd:
+"""Runs the reference-side ctypes binding of the repository's integration
+guide (the block between its binding markers), as written, through the plain C entry points gdn_decode_fwd and gdn_prefill_fwd:
 with q a strided view of a fused qkv projection and A_log in bf16, the two
 cases in which the binding converts or copies an argument.  Bars: outputs
 within atol = rtol = 1e-2 and final states within 1e-3 relative error of the
@@ -21,7 +21,7 @@ def _binding():
     code = re.search(r"<!-- binding:begin -->\s*```python\n(.*?)```\s*<!-- binding:end -->", text,
                      re.S).group(1)
     ns = {"LIB_PATH": str(pkg_module("_capi").LIB_PATH)}
-    exec(compile(code, "INTEGRATION.md", "exec"), ns)
+    exec(compile(code, "integration_binding", "exec"), ns)
     return ns
 
 
