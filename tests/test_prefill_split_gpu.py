@@ -211,3 +211,32 @@ def test_split_many_sequences(device, N):
         torch.testing.assert_close(o[b:e].float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
         rel = float((s[n:n + 1].cpu().double() - s_ref).norm() / s_ref.norm().clamp_min(1e-300))
         assert rel <= STATE_REL_BAR, (n, rel)
+
+
+@pytest.mark.parametrize("lens,expect", [([4096], "split8"), ([1500, 700, 2900, 64], "split8"),
+                                         ([200] * 40, "fused")])
+def test_prepared_prefill_follows_length_choice(device, lens, expect):
+    """PreparedPrefill and gdn_prefill take the path choose_slices picks from
+    the sequence lengths (qk4/v8: 8, 32 and 320 chains), and its results equal
+    the fused kernel's (states bit for bit but for rare last-place
+    differences, outputs within 1e-4)."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs(lens, seed=1011)
+    g = _to(x, device)
+    T, N = sum(lens), len(lens)
+    print(f"path choice lens={lens[:4]}... N={N} T={T} expect={expect}", flush=True)
+    slices = pre.choose_slices(x["cu_seqlens"], T, 8)
+    assert (f"split{slices}" if slices else "fused") == expect
+    out = torch.empty(T, 8, 128, dtype=torch.bfloat16, device=device)
+    fs = torch.empty(N, 8, 128, 128, dtype=torch.float32, device=device)
+    call = pre.PreparedPrefill(*[g[n] for n in NAMES], g["scale"], out, fs)
+    assert call.path == expect
+    call()
+    of, sf = _run(g, path="fused")
+    o, s = _run(g)                                # run-style automatic choice
+    torch.cuda.synchronize()
+    d = (out.float() - of.float()).abs()
+    assert float(d.max()) <= 1e-4, float(d.max())
+    assert float((fs - sf).norm() / sf.norm()) <= 1e-5
+    assert torch.equal(o, out) and torch.equal(s, fs)
