@@ -167,7 +167,8 @@ def bench_decode_multi(dev, steps, warmup, B=256, T=4, HQ=4, HV=8, sets=4):
 def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk_l2norm=False):
     w = ginp.WORKLOADS[name]
     lens = ginp.workload_lengths(name)
-    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
+    x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"],
+                            cu_dtype=w.get("cu_dtype", torch.int64))
     g = _to(x, dev)
     T = sum(lens)
     N = len(lens)

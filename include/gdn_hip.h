@@ -343,7 +343,11 @@ int gdn_gate_bwd(const float* A_log, const uint16_t* a, const float* dt_bias, co
  * h being each sequence's inputs preceded by its conv state (or zeros).
  *   x          : [T, C] bf16 (token-major, C a multiple of 8).
  *   weight     : [C, W] fp32, W in 2..4;  bias : [C] fp32 or NULL.
- *   cu_seqlens : as for gdn_prefill_fwd (int64, or int32 when cu_is_int32).
+ *   cu_seqlens : as for gdn_prefill_fwd (int64, or int32 when cu_is_int32),
+ *                N >= 1 when T > 0 (else GDN_ERR_SHAPE).  Tokens outside
+ *                every sequence (a padded batch with cu_seqlens[N] < T, or
+ *                ranges that run backwards) get zero outputs; reads stay in
+ *                bounds.
  *   conv_state_in  : [N, C, state_len] bf16 (the inputs that preceded each
  *                    sequence, oldest first) or NULL for zeros.
  *   conv_state_out : [N, C, state_len] bf16 or NULL: the last state_len inputs

@@ -214,3 +214,26 @@ def test_backward_capi_errors(device):
                             st) == capi.GDN_ERR_NULL
     assert call() == capi.GDN_OK
     torch.cuda.synchronize()
+
+
+def test_backward_overlapping_ranges_stay_in_bounds(device):
+    """cu_seqlens = [0, T, 0, T]: the batch counts 2 T / 64 chunks (and h as
+    many) against the T / 64 + N chunk records of the workspace.  The call
+    ends normally and the first sequence, whose records all fit, gets the
+    initial-state gradient of the same sequence alone, bit for bit; the empty
+    second sequence passes its final-state gradient through (the third
+    sequence's gradients, and the token gradients both write, are
+    unspecified)."""
+    T = 4096
+    print(f"backward overlapping cu_seqlens [0, {T}, 0, {T}]", flush=True)
+    x, d_out, _ = _case([T], 4, 8, 77, True, False)
+    gen = torch.Generator().manual_seed(78)
+    x["state"] = torch.randn(3, 8, 128, 128, generator=gen) * 0.02
+    d_fin = torch.randn(3, 8, 128, 128, generator=gen) * 0.1
+    single = dict(x, state=x["state"][:1], cu_seqlens=torch.tensor([0, T], dtype=torch.int64))
+    x["cu_seqlens"] = torch.tensor([0, T, 0, T], dtype=torch.int64)
+    r = _gpu_backward(_to(x, device), d_out, d_fin, device)
+    r1 = _gpu_backward(_to(single, device), d_out, d_fin[:1], device)
+    torch.cuda.synchronize()
+    assert torch.equal(r["dh0"][0], r1["dh0"][0])
+    assert torch.equal(r["dh0"][1].cpu(), d_fin[1].float())

@@ -71,6 +71,13 @@ def test_argument_errors_return_before_launch():
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, None, 0, 2, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 6, 1.0, P, P, P, 1, None, 0, 0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_chunk_count(None, 0, 1, 1) == -1
+    # the allocation-free split prefill: a workspace above its static array
+    assert lib.gdn_prefill_split_workspace_bytes(8, 32768, 4, 8) > lib.gdn_prefill_split_noalloc_max_bytes()
+    assert lib.gdn_prefill_split_noalloc_fwd(P, P, P, 0, P, P, P, P, P, 0, 8, 32768, 4, 8, 1.0, P, P, 8,
+                                             0, None) == capi.GDN_ERR_WORKSPACE
+    # conv1d: tokens with no sequence to hold them (N = 0, T > 0)
+    assert lib.gdn_qkv_conv1d_fwd(P, P, None, P, 0, 0, 5, 512, 4, None, None, 3, P, None, None,
+                                  0, 0, 1, None) == capi.GDN_ERR_SHAPE
 
 
 @pytest.mark.parametrize("seed", range(4))

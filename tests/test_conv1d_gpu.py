@@ -82,6 +82,39 @@ def test_qkv_split_equals_single_output(device):
     assert torch.equal(fin, fin2)
 
 
+def test_padded_batch_tokens_past_last_sequence(device):
+    """cu_seqlens[-1] < T (a padded batch): the sequences' tokens and states
+    match the unpadded call bit for bit, the padding rows are zero, and the
+    launch ends (the tile holding the last sequence end continues past it)."""
+    capi = pkg_module("_capi")
+    HQ, HV, W, S = 1, 2, 4, 3
+    C = 256 * HQ + 128 * HV
+    lens = [50, 7, 0, 20]
+    T_used, pad = sum(lens), 70                       # 77 tokens in sequences, 70 padding rows
+    print(f"conv padded batch lens={lens} pad={pad}", flush=True)
+    x, w, b, cu, st = _inputs(lens, C, W, S, True, True, seed=17, cu_dtype=torch.int32)
+    gen = torch.Generator().manual_seed(18)
+    xp = torch.cat([x, torch.randn(pad, C, generator=gen).to(torch.bfloat16)])
+    x, xp, w, b, cu, st = (t.to(device) for t in (x, xp, w, b, cu, st))
+    p = capi.ptr
+    stream = capi.stream_handle(device)
+    out = torch.empty(T_used, C, dtype=torch.bfloat16, device=device)
+    fin = torch.empty(len(lens), C, S, dtype=torch.bfloat16, device=device)
+    rc = capi.lib().gdn_qkv_conv1d_fwd(p(x), p(w), p(b), p(cu), 1, len(lens), T_used, C, W, p(st),
+                                       p(fin), S, p(out), None, None, 0, 0, capi.GDN_ACT_SILU, stream)
+    assert rc == 0
+    outp = torch.full((T_used + pad, C), 7.0, dtype=torch.bfloat16, device=device)
+    finp = torch.empty_like(fin)
+    rc = capi.lib().gdn_qkv_conv1d_fwd(p(xp), p(w), p(b), p(cu), 1, len(lens), T_used + pad, C, W,
+                                       p(st), p(finp), S, p(outp), None, None, 0, 0,
+                                       capi.GDN_ACT_SILU, stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(outp[:T_used], out)
+    assert torch.equal(finp, fin)
+    assert not bool(outp[T_used:].float().abs().sum() > 0)
+
+
 @pytest.mark.parametrize("S", [3, 4])
 def test_update_equals_prefill_token_by_token(device, S):
     """T decode updates (state in place) reproduce the prefill conv over the

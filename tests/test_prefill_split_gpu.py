@@ -240,3 +240,29 @@ def test_prepared_prefill_follows_length_choice(device, lens, expect):
     assert float(d.max()) <= 1e-4, float(d.max())
     assert float((fs - sf).norm() / sf.norm()) <= 1e-5
     assert torch.equal(o, out) and torch.equal(s, fs)
+
+
+@pytest.mark.parametrize("path", ["split", "fused"])
+def test_overlapping_ranges_stay_in_bounds(device, path):
+    """cu_seqlens = [0, T, 0, T]: the third sequence repeats the first, so the
+    batch counts 2 T / 64 chunks against the T / 64 + N chunk slots the split
+    workspace holds.  The call ends normally; the first sequence, whose chunk
+    slots are all inside the workspace, keeps its exact final state and the
+    empty second sequence its initial state (the third sequence's results,
+    and the outputs both write, are unspecified)."""
+    inp = pkg_module("inputs")
+    T = 4096
+    print(f"overlapping cu_seqlens [0, {T}, 0, {T}] path={path}", flush=True)
+    x = inp.prefill_inputs([T], seed=4242, with_state=True)
+    gen = torch.Generator().manual_seed(4243)
+    x["state"] = torch.randn(3, 8, 128, 128, generator=gen) * 0.02
+    x["cu_seqlens"] = torch.tensor([0, T, 0, T], dtype=torch.int64)
+    g = _to(x, device)
+    o, s = _run(g, path=path, slices=8)
+    torch.cuda.synchronize()
+    one = dict(x, state=x["state"][:1], cu_seqlens=torch.tensor([0, T], dtype=torch.int64))
+    _, s_ref = _oracle(one)
+    s = s.cpu().double()
+    rel = float((s[0] - s_ref[0]).norm() / s_ref[0].norm())
+    assert rel <= STATE_REL_BAR, rel
+    assert torch.equal(s[1].float(), x["state"][1].float())

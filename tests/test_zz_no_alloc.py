@@ -60,12 +60,23 @@ def test_noalloc_matches_workspace_entry_twice(device):
 
 
 def test_noalloc_rejects_oversized_problem(device):
+    """A problem whose workspace exceeds the static array is rejected before
+    any launch.  The buffers are real device tensors of the problem's sizes,
+    so the call reads nothing out of bounds even if it went further."""
     capi = pkg_module("_capi")
     pre = pkg_module("prefill")
     lib = capi.lib()
     T, N = 32768, 8
     assert pre.split_workspace_bytes(N, T, 4, 8) > lib.gdn_prefill_split_noalloc_max_bytes()
-    P = 0x1000  # never dereferenced: the size check fails first
-    rc = lib.gdn_prefill_split_noalloc_fwd(P, P, P, 0, P, P, P, P, P, 0, N, T, 4, 8, 1.0, P, P, 8,
-                                           0, capi.stream_handle(device))
+    z = lambda *shape, dt=torch.bfloat16: torch.zeros(*shape, dtype=dt, device=device)
+    q, k, v, out = z(T, 4, 128), z(T, 4, 128), z(T, 8, 128), z(T, 8, 128)
+    a, b = z(T, 8), z(T, 8)
+    A_log, dt_bias = z(8, dt=torch.float32), z(8, dt=torch.float32)
+    state, fs = z(N, 8, 128, 128, dt=torch.float32), z(N, 8, 128, 128, dt=torch.float32)
+    cu = torch.arange(0, T + 1, T // N, dtype=torch.int64, device=device)
+    p = capi.ptr
+    rc = lib.gdn_prefill_split_noalloc_fwd(p(q), p(k), p(v), p(state), p(A_log), p(a), p(dt_bias),
+                                           p(b), p(cu), 0, N, T, 4, 8, 1.0, p(out), p(fs), 8, 0,
+                                           capi.stream_handle(device))
     assert rc == capi.GDN_ERR_WORKSPACE
+    torch.cuda.synchronize()

@@ -133,12 +133,29 @@ __global__ __launch_bounds__(kConvThreads) void gdn_qkv_conv1d_kernel(
     bs[e] = bias != nullptr ? bias[c0 + e] : 0.f;
   }
   // the tile in segments that lie in one sequence; within a segment the
-  // inputs of eight tokens are loaded before their outputs are formed
+  // inputs of eight tokens are loaded before their outputs are formed.
+  // Tokens outside every sequence (before cu[0], at or past cu[N], or where
+  // the ranges run backwards) get zero outputs; each pass of the loop
+  // advances t, so the loop ends whatever cu holds.
   constexpr int kBatch = 8;
+  auto zero_rows = [&](int u0, int u1) {
+    const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int u = u0; u < u1; ++u) store8(out_at(o, u, c0), z);
+  };
   for (int t = t0; t < t1;) {
     const int n = seq_of(cu, N, T, t);
     const int bos = clamp_cu(cu, n, T), eos = clamp_cu(cu, n + 1, T);
+    if (t < bos) {                            // before the sequence's first token
+      const int tb = min(t1, bos);
+      zero_rows(t, tb);
+      t = tb;
+      continue;
+    }
     const int te = min(t1, eos);
+    if (te <= t) {                            // past the sequence's last token
+      zero_rows(t, t1);
+      break;
+    }
     float hist[kMaxConvWidth - 1][8];         // hist[j]: input at token u - (W - 1) + j
 #pragma unroll
     for (int j = 0; j < W - 1; ++j) hist_at(t - (W - 1) + j, n, bos, hist[j]);
@@ -341,6 +358,7 @@ extern "C" int gdn_qkv_conv1d_fwd(const uint16_t* x, const float* weight, const 
   if (activation != GDN_ACT_NONE && activation != GDN_ACT_SILU) return GDN_ERR_SHAPE;
   if (!cu_seqlens) return GDN_ERR_NULL;
   if (conv_state_out != nullptr && conv_state_out == conv_state_in) return GDN_ERR_SHAPE;
+  if (N == 0 && T > 0) return GDN_ERR_SHAPE;   // tokens but no sequence to hold them
   if (T > 0 && (!x || !weight)) return GDN_ERR_NULL;
   if (N > 0 && conv_state_out != nullptr && !weight) return GDN_ERR_NULL;
   QkvOut o;

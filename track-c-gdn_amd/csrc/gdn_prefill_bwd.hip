@@ -53,6 +53,8 @@
 #include "gdn_prefill_split.h"
 #include "../../include/gdn_hip.h"
 
+#include <algorithm>
+
 namespace {
 
 using namespace gdn;
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
                    : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   int last = nc - 1;
-  if (coff + last >= h_chunks) last = -1;     // records past h_chunks were not formed
+  if (coff + last >= h_chunks) last = -1;     // records at or past h_chunks (clamped to the workspace's slots) were not formed
   // M is copied HBM -> LDS and R loaded into registers two chunks ahead: three
   // LDS buffers for M and three register sets for R, rotated by unrolling the
   // chunk loop by three.
@@ -992,6 +994,11 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
                const float* d_ht, float* dq, float* dk, float* dv, float* dg, float* dbeta, float* dh0,
                char* ws, hipStream_t st) {
   const size_t slots = size_t(T) / C + size_t(N);
+  // The workspace holds `slots` chunk records per v-head.  Well-formed
+  // cu_seqlens give at most that many chunks; with overlapping ranges the
+  // chunk count (and h_chunks) can exceed it, and every kernel then stops at
+  // the last slot the workspace holds (results unspecified, accesses in bounds).
+  h_chunks = int(std::min<size_t>(size_t(h_chunks), slots));
   char* mrec = ws;
   char* rrec = mrec + slots * HV * kMBytes;
   uint16_t* dhr = reinterpret_cast<uint16_t*>(rrec + slots * HV * kRBytes);

@@ -551,11 +551,15 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   const int g = lane >> 4, c = lane & 15;
   int bos, len;
   seq_bounds(cu_seqlens, n, T, bos, len);
-  const int n_chunks = (len + C - 1) / C;
   const size_t qk_stride = size_t(HQ) * D;
   const size_t v_stride = size_t(HV) * D;
   auto chunk_len = [&](int ch) { return min(C, len - ch * C); };
   const int coff = chunk_offset(cu_seqlens, n, T, lane);
+  // The workspace holds nt_bound chunk slots, enough for every chunk of
+  // well-formed cu_seqlens.  Ranges that overlap can count more chunks: the
+  // chain then stops at the last slot the workspace holds (results
+  // unspecified, every record and K image read in bounds).
+  const int n_chunks = min((len + C - 1) / C, max(0, nt_bound - coff));
   // workspace record of chunk ch of this chain
   auto record = [&](int ch) { return ws + (size_t(coff + ch) * HV + hv) * kBlob; };
 

@@ -115,7 +115,7 @@ WORKLOADS = {
     "prefill_t4096_n1_qk4_v8": dict(kind="prefill", lengths=[4096], HQ=4, HV=8, seed=1002,
                                     with_state=False),
     "prefill_varlen16_qk4_v8": dict(kind="prefill", lengths=None, HQ=4, HV=8, seed=1003,
-                                    with_state=True),
+                                    with_state=True, cu_dtype=torch.int32),
     "prefill_varlen8_t32768_qk16_v32": dict(kind="prefill", lengths=None, HQ=16, HV=32,
                                             seed=1004, with_state=True),
     "decode_pool_b1024_qk16_v32": dict(kind="decode_pool", B=1024, HQ=16, HV=32, seed=1004),
