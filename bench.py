@@ -617,6 +617,10 @@ def main():
                                  "flops_per_launch": r["flops"], "kernels": kernels,
                                  "time_basis": "both launches of one call" if len(kernels) > 1
                                  else "one launch"}}
+                if r["path"].startswith("split"):
+                    tr = _traffic("gdn_prefill_split_" + name[len("prefill_"):])
+                    if tr is not None:
+                        line[name]["roofline"]["traffic"] = tr
                 print(f"# {name} ({r['path']}): {kus:.1f} us, {tfl:.1f} TFLOP/s "
                       f"({tfl / MFMA_BF16_PEAK_TFLOPS * 100:.2f}% of bf16 MFMA peak)",
                       file=sys.stderr, flush=True)
@@ -639,6 +643,10 @@ def main():
                              "flops_per_launch": r["flops"],
                              "flops_basis": "executed bf16 MFMA products, 2272 per chunk and v-head",
                              "time_basis": "all launches of one call"}}
+            if key == "prefill_backward":
+                tr = _traffic("gdn_prefill_bwd_t32768_qk16_v32")
+                if tr is not None:
+                    line[key]["roofline"]["traffic"] = tr
             print(f"# backward {name}: {kus:.1f} us, {tfl:.1f} TFLOP/s "
                   f"({tfl / MFMA_BF16_PEAK_TFLOPS * 100:.1f}% of bf16 MFMA peak)",
                   file=sys.stderr, flush=True)
