@@ -217,8 +217,10 @@ def bench_prefill_occupancy(dev, steps, warmup, HQ=16, HV=32):
     return res
 
 
-def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
-    """The prefill that also writes the state entering every chunk (bf16 h)."""
+def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", path="fused",
+                    slices=8):
+    """The prefill that also writes the state entering every chunk (bf16 h), on
+    the given path (the split path with its workspace allocated once)."""
     w = ginp.WORKLOADS[name]
     lens = ginp.workload_lengths(name)
     x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])
@@ -230,9 +232,14 @@ def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     NT = gpre.num_chunks(g["cu_seqlens"], T)
     h = torch.empty(NT, w["HV"], D, D, dtype=torch.bfloat16, device=dev)
     args = [g[n] for n in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")]
+    ws = None
+    if path == "split":
+        ws = torch.empty(gpre.split_workspace_bytes(N, T, w["HQ"], w["HV"]), dtype=torch.uint8,
+                         device=dev)
 
     def launch(i):
-        gpre.gdn_prefill(*args, g["scale"], output=out, final_state=fs, validate=False, h=h)
+        gpre.gdn_prefill(*args, g["scale"], output=out, final_state=fs, validate=False, h=h,
+                         path=path, slices=slices, workspace=ws)
 
     total_ms, kern_ms = timed_launches(launch, steps, warmup)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, chunks=NT, h_bytes=h.numel() * 2)
@@ -281,9 +288,14 @@ def bench_backward(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
 
 def bench_run_latency(dev, kernel_us, reps=50):
     """End-to-end latency of the reference-compatible ``run`` entry points
-    (validation, allocation of the outputs and workspace, the ctypes call,
-    the kernel) with a synchronisation after every call: the median over
-    ``reps`` calls, beside the kernel time alone."""
+    (validation, allocation of the outputs, the ctypes call, the kernels):
+    ``run_us`` with a synchronisation after every call (the median over
+    ``reps`` calls), ``back_to_back_us`` per call over ``reps`` calls issued
+    back to back with one synchronisation at the end (the host work of a call
+    overlaps the previous call's kernels), beside the kernel time alone.
+    Prefill ``run`` reads cu_seqlens back once per tensor and version (the
+    reference's ``cu_seqlens[-1] == T`` check), so repeated calls on the same
+    inputs do not synchronise."""
     res = {}
 
     def median_call_us(fn):
@@ -299,20 +311,32 @@ def bench_run_latency(dev, kernel_us, reps=50):
         ts.sort()
         return ts[len(ts) // 2]
 
+    def back_to_back_us(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / reps
+
+    def record(name, fn):
+        us = median_call_us(fn)
+        b2b = back_to_back_us(fn)
+        k = kernel_us.get(name)
+        res[name] = {"run_us": round(us, 1), "back_to_back_us": round(b2b, 1), "kernel_us": k,
+                     "host_overhead_us": None if k is None else round(us - k, 1)}
+
     for name, B in (("decode_b1_qk4_v8", 1), ("decode_b256_qk4_v8", 256)):
         g = _to(ginp.decode_inputs(B, 4, 8, seed=1000 if B == 1 else 1001), dev)
-        us = median_call_us(lambda: gdec.run(g["q"], g["k"], g["v"], g["state"], g["A_log"],
-                                             g["a"], g["dt_bias"], g["b"], g["scale"]))
-        k = kernel_us.get(name)
-        res[name] = {"run_us": round(us, 1), "kernel_us": k,
-                     "host_overhead_us": None if k is None else round(us - k, 1)}
-    name = "prefill_t4096_n1_qk4_v8"
-    g = _to(ginp.prefill_inputs([4096], 4, 8, seed=1002), dev)
-    us = median_call_us(lambda: gpre.run(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
-                                         g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"]))
-    k = kernel_us.get(name)
-    res[name] = {"run_us": round(us, 1), "kernel_us": k,
-                 "host_overhead_us": None if k is None else round(us - k, 1)}
+        record(name, lambda: gdec.run(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
+                                      g["dt_bias"], g["b"], g["scale"]))
+    for name in ("prefill_t4096_n1_qk4_v8", "prefill_varlen16_qk4_v8"):
+        w = ginp.WORKLOADS[name]
+        x = ginp.prefill_inputs(ginp.workload_lengths(name), w["HQ"], w["HV"], seed=w["seed"],
+                                with_state=w["with_state"], cu_dtype=w.get("cu_dtype", torch.int64))
+        g = _to(x, dev)
+        record(name, lambda: gpre.run(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
+                                      g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"]))
     return res
 
 
@@ -592,6 +616,16 @@ def main():
             print(f"# prefill with h (bf16, {r['chunks']} chunks, {r['h_bytes'] / 1e6:.0f} MB): "
                   f"{kus:.1f} us against {line['prefill']['roofline']['kernel_us']:.1f} us without",
                   file=sys.stderr, flush=True)
+            # the same at one 4096-token sequence (qk4/v8), on the split path the
+            # length-based choice takes (the training forward of a few long chains)
+            r = bench_prefill_h(dev, args.prefill_steps, PREFILL_WARMUP,
+                                name="prefill_t4096_n1_qk4_v8", path="split", slices=8)
+            line["prefill_h_t4096_n1_qk4_v8"] = {
+                "workload": "prefill_t4096_n1_qk4_v8", "path": "split8", "chunks": r["chunks"],
+                "h_bytes": r["h_bytes"], "kernel_us": round(r["kernel_ms"] * 1e3, 2),
+                "time_basis": "both launches of one call"}
+            print(f"# prefill with h, 4096 tokens (split8): {r['kernel_ms'] * 1e3:.1f} us",
+                  file=sys.stderr, flush=True)
             # the in-kernel q/k L2-normalisation option on the same inputs
             r = bench_prefill(dev, args.prefill_steps, PREFILL_WARMUP, qk_l2norm=True)
             line["prefill_qk_l2norm"] = {
@@ -677,7 +711,8 @@ def main():
 
     if args.only == "all" and not args.no_latency:
         kus = {"decode_b256_qk4_v8": line.get("roofline", {}).get("kernel_us"),
-               "prefill_t4096_n1_qk4_v8": line.get("prefill_t4096_n1_qk4_v8", {}).get("kernel_us")}
+               "prefill_t4096_n1_qk4_v8": line.get("prefill_t4096_n1_qk4_v8", {}).get("kernel_us"),
+               "prefill_varlen16_qk4_v8": line.get("prefill_varlen16_qk4_v8", {}).get("kernel_us")}
         r1 = bench_decode(dev, 50, 10, B=1, sets=1)
         kus["decode_b1_qk4_v8"] = round(r1["kernel_ms"] * 1e3, 2)
         line["run_latency"] = bench_run_latency(dev, kus)

@@ -265,7 +265,13 @@ long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, 
  *   h        : device [h_chunks, HV, 128, 128] bf16.
  *   h_chunks : capacity of h in chunks; gdn_prefill_chunk_count(...) gives
  *              the number written.  Slots at or past h_chunks are skipped.
- * out / final_state are those of gdn_prefill_ex_fwd, bit for bit.
+ *   workspace: as for gdn_prefill_ex_fwd: with few chains and the workspace
+ *              of gdn_prefill_workspace_bytes the split path runs (the
+ *              reference writes h from its V-split recurrence grid at any
+ *              batch size, kernel.py:1369), else one fused workgroup per
+ *              chain.
+ * out / final_state are those of gdn_prefill_ex_fwd on the same path, bit
+ * for bit; h is the bf16 image of the state the path forms either way.
  */
 int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       const float* state, const float* A_log, const uint16_t* a,
@@ -274,6 +280,23 @@ int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                       int HQ, int HV, float scale,
                       uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
                       void* workspace, size_t workspace_bytes, int flags, void* stream);
+
+/*
+ * gdn_prefill_h_fwd forced onto the split path with `slices` (4 or 8) state
+ * slices per chain, as gdn_prefill_split_fwd (the counterpart of
+ * chunk_gated_delta_rule_fwd_h's V-split grid, kernel.py:1365-1393, with h
+ * stored per chunk as at kernel.py:1153-1160).  The workspace is that of
+ * gdn_prefill_split_workspace_bytes; GDN_ERR_WORKSPACE when NULL or short,
+ * GDN_ERR_SHAPE for another slice count.
+ */
+int gdn_prefill_split_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            const float* state, const float* A_log, const uint16_t* a,
+                            const float* dt_bias, const uint16_t* b,
+                            const void* cu_seqlens, int cu_is_int32, int N, int T,
+                            int HQ, int HV, float scale,
+                            uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
+                            int slices, void* workspace, size_t workspace_bytes, int flags,
+                            void* stream);
 
 /*
  * Backward of the prefill (no counterpart in the reference, which is

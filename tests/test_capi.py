@@ -26,7 +26,7 @@ def test_header_declares_expected_entry_points():
         "gdn_prefill_split_workspace_bytes", "gdn_prefill_split_fwd", "gdn_prefill_auto_slices",
         "gdn_prefill_split_noalloc_max_bytes", "gdn_prefill_split_noalloc_fwd",
         "gdn_qkv_conv1d_fwd", "gdn_qkv_conv1d_update", "gdn_prefill_bwd_workspace_bytes",
-        "gdn_prefill_bwd", "gdn_gate_bwd", "gdn_prefill_choose_slices"])
+        "gdn_prefill_bwd", "gdn_gate_bwd", "gdn_prefill_choose_slices", "gdn_prefill_split_h_fwd"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -71,6 +71,9 @@ def test_argument_errors_return_before_launch():
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, None, 0, 2, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 6, 1.0, P, P, P, 1, None, 0, 0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_chunk_count(None, 0, 1, 1) == -1
+    assert lib.gdn_prefill_split_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 1, 8, P, 1 << 30, 0, None) == capi.GDN_ERR_NULL
+    assert lib.gdn_prefill_split_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, 6, P, 1 << 30, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_split_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, 8, None, 0, 0, None) == capi.GDN_ERR_WORKSPACE
     # the allocation-free split prefill: a workspace above its static array
     assert lib.gdn_prefill_split_workspace_bytes(8, 32768, 4, 8) > lib.gdn_prefill_split_noalloc_max_bytes()
     assert lib.gdn_prefill_split_noalloc_fwd(P, P, P, 0, P, P, P, P, P, 0, 8, 32768, 4, 8, 1.0, P, P, 8,

@@ -1,9 +1,12 @@
 """Runs the reference-side ctypes binding of the repository's integration
-guide (the block between its binding markers), as written, through the plain C entry points gdn_decode_fwd and gdn_prefill_fwd:
-with q a strided view of a fused qkv projection and A_log in bf16, the two
-cases in which the binding converts or copies an argument.  Bars: outputs
-within atol = rtol = 1e-2 and final states within 1e-3 relative error of the
-fp64 oracle."""
+guide (the block between its binding markers), as written: decode through
+gdn_decode_fwd with q a strided view of a fused qkv projection and A_log in
+bf16 (the cases in which the binding converts or copies an argument);
+prefill with the reference's validation and the length-based path choice
+(gdn_prefill_choose_slices, then gdn_prefill_split_fwd or gdn_prefill_fwd).
+Bars: outputs within atol = rtol = 1e-2 and final states within 1e-3
+relative error of the fp64 oracle; the fused-path case equal bit for bit to
+the package's fused call."""
 
 import re
 
@@ -47,20 +50,57 @@ def test_binding_decode(device):
     assert float((s.cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
 
 
-@pytest.mark.parametrize("lens", [[4096], [300, 0, 77]])
-def test_binding_prefill(device, lens):
+@pytest.mark.parametrize("lens,path", [([4096], 8), ([300, 0, 77], 8)])
+def test_binding_prefill(device, lens, path):
+    """qk4/v8 through the binding, q a strided view: the lengths choose the
+    split path (8 state slices per chain)."""
     ns = _binding()
     inp = pkg_module("inputs")
     x = inp.prefill_inputs(lens, seed=602, with_state=True)
     g = _to(x, device)
+    assert ns["prefill_slices"](x["cu_seqlens"], sum(lens), 8) == path
     qk = torch.cat([g["q"], g["k"]], dim=-1)                              # [T, 4, 256]
     q = qk[..., :128]
     assert not q.is_contiguous()
-    o, s = ns["prefill_run"](q, g["k"], g["v"], g["state"], g["A_log"].to(torch.bfloat16), g["a"],
+    o, s = ns["prefill_run"](q, g["k"], g["v"], g["state"], g["A_log"], g["a"],
                              g["dt_bias"], g["b"], g["cu_seqlens"], None)
     torch.cuda.synchronize()
     names = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
-    xr = dict(x, A_log=x["A_log"].to(torch.bfloat16).float())
-    o_ref, s_ref = O.prefill_chunked(*[xr[n] for n in names], x["scale"])
+    o_ref, s_ref = O.prefill_chunked(*[x[n] for n in names], x["scale"])
     torch.testing.assert_close(o.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
     assert float((s.cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
+
+
+def test_binding_prefill_four_equal_sequences_fused(device):
+    """Four 5 348-token sequences at qk16/v32 (128 chains): the lengths choose
+    the fused kernel, and the binding's results equal the package's fused
+    path bit for bit."""
+    ns = _binding()
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    lens = [5348] * 4
+    print("binding prefill 4 x 5348 qk16/v32", flush=True)
+    x = inp.prefill_inputs(lens, 16, 32, seed=603, with_state=True)
+    g = _to(x, device)
+    assert ns["prefill_slices"](x["cu_seqlens"], sum(lens), 32) == 0
+    names = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+    o, s = ns["prefill_run"](*[g[n] for n in names], None)
+    of, sf = pre.gdn_prefill(*[g[n] for n in names], None, path="fused")
+    torch.cuda.synchronize()
+    assert torch.equal(o, of) and torch.equal(s, sf)
+
+
+def test_binding_prefill_rejects_like_the_reference(device):
+    """AssertionError before any launch, as PRE:1635-1667: cu_seqlens[-1] != T,
+    and A_log not fp32."""
+    ns = _binding()
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs([100, 28], seed=604, with_state=True)
+    g = _to(x, device)
+    names = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+    bad = dict(g, cu_seqlens=torch.tensor([0, 100, 127], dtype=torch.int64, device=device))
+    with pytest.raises(AssertionError):
+        ns["prefill_run"](*[bad[n] for n in names], None)
+    bad = dict(g, A_log=g["A_log"].to(torch.bfloat16))
+    with pytest.raises(AssertionError):
+        ns["prefill_run"](*[bad[n] for n in names], None)

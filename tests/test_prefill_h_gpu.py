@@ -37,17 +37,22 @@ def _rel(a, b):
     return float((a - b).norm() / b.norm().clamp_min(1e-300))
 
 
+@pytest.mark.parametrize("path,slices", [("fused", 8), ("split", 8), ("split", 4)])
 @pytest.mark.parametrize("lens,HQ,HV,with_state,l2", [
     ([1, 63, 64, 65, 129], 4, 8, True, False), ([0, 300], 4, 8, False, False),
     ([130, 0, 70], 16, 32, True, False), ([200, 64], 4, 8, True, True)])
-def test_prefill_h_matches_oracle(device, lens, HQ, HV, with_state, l2):
+def test_prefill_h_matches_oracle(device, lens, HQ, HV, with_state, l2, path, slices):
+    """Both paths: the fused kernel's kH instantiation and the split path's
+    state slices (the output waves store the bf16 state image they read)."""
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
-    print(f"prefill h lens={lens} HQ={HQ} HV={HV} l2={l2}", flush=True)
+    print(f"prefill h lens={lens} HQ={HQ} HV={HV} l2={l2} path={path}{slices}", flush=True)
     x = inp.prefill_inputs(lens, HQ=HQ, HV=HV, seed=4100 + sum(lens), with_state=with_state)
     g = _to(x, device)
-    o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2)
-    o0, s0 = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2, path="fused")
+    o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2, path=path,
+                                slices=slices)
+    o0, s0 = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], qk_l2norm=l2, path=path,
+                             slices=slices)
     torch.cuda.synchronize()
     assert torch.equal(o, o0) and torch.equal(s, s0)
     offs = O.chunk_offsets(x["cu_seqlens"], 64)
@@ -68,7 +73,8 @@ def test_prefill_h_matches_oracle(device, lens, HQ, HV, with_state, l2):
                 assert rel <= H_REL_BAR, (n, i, rel)
 
 
-def test_prefill_h_capacity_guard_and_int32(device):
+@pytest.mark.parametrize("path", ["fused", "split"])
+def test_prefill_h_capacity_guard_and_int32(device, path):
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
     lens = [150, 90, 64]
@@ -77,9 +83,9 @@ def test_prefill_h_capacity_guard_and_int32(device):
     NT = pre.num_chunks(g["cu_seqlens"], sum(lens))
     assert NT == 3 + 2 + 1
     big = torch.full((NT + 2, 8, 128, 128), 7.0, dtype=torch.bfloat16, device=device)
-    o_full, s_full, h_full = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"])
+    o_full, s_full, h_full = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"], path=path)
     small = big[:NT - 2]                      # the last sequence's slots and one more are cut
-    o, s = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], h=small)
+    o, s = pre.gdn_prefill(*[g[n] for n in NAMES], g["scale"], h=small, path=path)
     torch.cuda.synchronize()
     assert torch.equal(o, o_full) and torch.equal(s, s_full)
     assert torch.equal(big[:NT - 2], h_full[:NT - 2])
@@ -136,3 +142,23 @@ def test_prefill_h_many_sequences(device):
             assert torch.equal(h_cpu[int(offs[n])], x["state"][n].to(torch.bfloat16)), n
     rel = _rel(h_cpu, h_ref)
     assert rel <= H_REL_BAR, rel
+
+
+def test_prefill_h_split_one_long_sequence(device):
+    """One 4096-token sequence at qk4/v8 (64 chunks, 8 chains): the length-based
+    choice takes the split path (8 state slices on 64 CUs); h matches the
+    fp64 oracle's per-chunk states and equals the fused kernel's h bit for
+    bit (the two paths form the same states)."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    lens = [4096]
+    print("prefill h 4096 tokens, split vs fused", flush=True)
+    x = inp.prefill_inputs(lens, seed=1002)
+    g = _to(x, device)
+    assert pre.choose_slices(x["cu_seqlens"], 4096, 8) == 8
+    o, s, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"])
+    of, sf, hf = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"], path="fused")
+    torch.cuda.synchronize()
+    assert torch.equal(s, sf) and torch.equal(h, hf)
+    h_ref = O.prefill_chunk_states(*[x[n] for n in NAMES])
+    assert _rel(h, h_ref) <= H_REL_BAR

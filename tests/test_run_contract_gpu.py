@@ -64,6 +64,40 @@ def test_prefill_run_rejects_bad_totals_dtypes_and_shapes(device):
         print("rejected:", name, flush=True)
 
 
+def test_prefill_run_rereads_rewritten_cu_seqlens(device):
+    """run reads cu_seqlens back once per tensor object and version: a repeated
+    call on the same tensor reuses the host copy, an in-place rewrite through
+    torch is read again (and fails the reference's cu_seqlens[-1] == T check
+    when it should), and a new tensor at a reused address is read again."""
+    pre = pkg_module("prefill")
+    x, g = _prefill_case(device, lens=(70, 30))
+    args = [g[n] for n in PNAMES]
+    cu = g["cu_seqlens"]
+    o1, s1 = pre.run(*args, x["scale"])
+    o2, s2 = pre.run(*args, x["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    cu.copy_(torch.tensor([0, 70, 99], dtype=cu.dtype, device=device))      # in place: T mismatch
+    with pytest.raises(AssertionError):
+        pre.run(*args, x["scale"])
+    cu.copy_(torch.tensor([0, 60, 100], dtype=cu.dtype, device=device))     # new split, T again
+    o3, s3 = pre.run(*args, x["scale"])
+    del args, cu
+    g["cu_seqlens"] = None
+    fresh = torch.tensor([0, 100], dtype=torch.int64, device=device)        # may reuse the address
+    one_state = g["state"][:1].contiguous()
+    o4, s4 = pre.run(g["q"], g["k"], g["v"], one_state, g["A_log"], g["a"], g["dt_bias"], g["b"],
+                     fresh, x["scale"])
+    torch.cuda.synchronize()
+    x60 = dict(x, cu_seqlens=torch.tensor([0, 60, 100], dtype=torch.int64))
+    o_ref, s_ref = O.prefill_chunked(*[x60[n] for n in PNAMES], x["scale"])
+    torch.testing.assert_close(o3.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    x1 = dict(x, cu_seqlens=torch.tensor([0, 100], dtype=torch.int64), state=x["state"][:1])
+    o_ref, s_ref = O.prefill_chunked(*[x1[n] for n in PNAMES], x["scale"])
+    torch.testing.assert_close(o4.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    assert float((s4.cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
+
+
 @pytest.mark.parametrize("cu_dtype", [torch.int64, torch.int32])
 def test_prefill_run_accepts_int64_and_int32(device, cu_dtype):
     pre = pkg_module("prefill")

@@ -54,6 +54,8 @@ SIGNATURES = {
                                    _P]),
     "gdn_prefill_h_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                _P, _P, _P, _I, _P, _S, _I, _P]),
+    "gdn_prefill_split_h_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
+                                     _P, _P, _P, _I, _I, _P, _S, _I, _P]),
     "gdn_prefill_bwd_workspace_bytes": (_S, [_I, _I, _I, _I]),
     "gdn_prefill_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _I, _P,
                              _P, _P, _P, _P, _P, _P, _P, _P, _S, _P]),

@@ -1225,17 +1225,44 @@ extern "C" int gdn_prefill_h_fwd(const uint16_t* q, const uint16_t* k, const uin
                                  int cu_is_int32, int N, int T, int HQ, int HV, float scale,
                                  uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
                                  void* workspace, size_t workspace_bytes, int flags, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
                                     N, T, HQ, HV);
   if (rc != GDN_OK) return rc;
   if (!h && h_chunks > 0) return GDN_ERR_NULL;
   if (h_chunks < 0 || (flags & ~GDN_FLAGS_ALL)) return GDN_ERR_SHAPE;
   if (N == 0) return GDN_OK;
+  // Few chains: the split path when the caller supplied its workspace, as gdn_prefill_ex_fwd.
+  const int slices = T > 0 ? gdn::prefill_split_auto_slices(N, HV) : 0;
+  if (slices > 0 && workspace != nullptr &&
+      workspace_bytes >= gdn::prefill_split_workspace_bytes(N, T, HQ, HV)) {
+    return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32,
+                                     N, T, HQ, HV, scale, out, final_state, slices, workspace, flags,
+                                     static_cast<hipStream_t>(stream), h, h_chunks);
+  }
   return prefill_dispatch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ,
                           HV, scale, out, final_state, h, h_chunks, flags,
                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gdn_prefill_split_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                       const float* state, const float* A_log, const uint16_t* a,
+                                       const float* dt_bias, const uint16_t* b,
+                                       const void* cu_seqlens, int cu_is_int32, int N, int T, int HQ,
+                                       int HV, float scale, uint16_t* out, float* final_state,
+                                       uint16_t* h, int h_chunks, int slices, void* workspace,
+                                       size_t workspace_bytes, int flags, void* stream) {
+  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
+                                    N, T, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (!h && h_chunks > 0) return GDN_ERR_NULL;
+  if (h_chunks < 0 || (flags & ~GDN_FLAGS_ALL) || !gdn::prefill_split_slices_valid(slices))
+    return GDN_ERR_SHAPE;
+  if (N == 0) return GDN_OK;
+  const size_t need = gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return GDN_ERR_WORKSPACE;
+  return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
+                                   T, HQ, HV, scale, out, final_state, slices, workspace, flags,
+                                   static_cast<hipStream_t>(stream), h, h_chunks);
 }
 
 extern "C" int gdn_prefill_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,

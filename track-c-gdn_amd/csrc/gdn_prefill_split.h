@@ -31,10 +31,13 @@ size_t prefill_scratch_bytes();
 void* prefill_scratch(hipError_t* err);
 
 // Enqueues both launches on st; workspace holds prefill_split_workspace_bytes.
+// With h non-NULL the slices also write the bf16 state entering every chunk
+// to h[chunk_offset(n) + i] for slots below h_chunks.
 int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                          const float* A_log, const uint16_t* a, const float* dt_bias,
                          const uint16_t* b, const void* cu_seqlens, int cu_is_int32, int N, int T,
                          int HQ, int HV, float scale, uint16_t* out, float* final_state,
-                         int slices, void* workspace, int flags, hipStream_t st);
+                         int slices, void* workspace, int flags, hipStream_t st,
+                         uint16_t* h = nullptr, int h_chunks = 0);
 
 }  // namespace gdn

@@ -506,11 +506,16 @@ struct SliceCfg {
   static_assert(kNB % kFrRing == 0, "ring slot from the buffer set");
 };
 
-template <typename CuT, bool kL2, int NRG>
+//
+// kH: the output waves also write the state entering every chunk, bf16, to
+// hout[chunk_offset(n) + ch][hv][v][k] (slots at or past h_chunks skipped):
+// the bf16 image of S they read for S Q^T is that state.
+template <typename CuT, bool kL2, int NRG, bool kH>
 __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ v, const float* __restrict__ h0,
     const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV,
-    uint16_t* __restrict__ out, float* __restrict__ ht, const char* __restrict__ ws, int nt_bound) {
+    uint16_t* __restrict__ out, float* __restrict__ ht, const char* __restrict__ ws, int nt_bound,
+    uint16_t* __restrict__ hout, int h_chunks) {
   using Cfg = SliceCfg<NRG>;
   constexpr int R = Cfg::R;
   constexpr int VS = Cfg::VS;
@@ -569,6 +574,8 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
     const int r = out_role ? wave - NRG : wave;     // row group
     const int v0 = vb + 16 * r;                 // rows v0 + c
     const int vl = 16 * r;                      // the same, relative to the slice
+    // kH: byte offset of this lane's 16 bytes in an h slot of the chain
+    const uint32_t h_lane = uint32_t((v0 + c) * D + ((g & 1) ? 4 * (g + 3) : 4 * g)) * 2u;
     // Sacc[kb][i] = S[v0 + c][16 kb + 4 g + i]: the S^T accumulator tiles.
     f32x4 Sacc[8];
     const float* h0row = h0 == nullptr ? nullptr
@@ -736,6 +743,20 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           for (int tb = 0; tb < 4; ++tb) {
             asm volatile("" : "+v"(qf[p & 1][tb]));
             OT[tb] = mfma16_bf(sbf, qf[p & 1][tb], OT[tb]);
+          }
+          if constexpr (kH) {
+            // Lane (g, c) holds row v0 + c, 4-column pieces g and g + 4 of
+            // column block p; v_permlane16_swap trades the odd 16-lane rows'
+            // first piece for the even rows' second, which leaves 16
+            // contiguous bytes per lane (pieces g, g + 1 for even g, g + 3,
+            // g + 4 for odd g): one 16-byte store covers 16 rows x 64 bytes.
+            if (coff + ch < h_chunks) {
+              char* hb = reinterpret_cast<char*>(hout) + (size_t(coff + ch) * HV + hv) * size_t(D * D * 2);
+              const u32x4_t w = __builtin_bit_cast(u32x4_t, sbf);
+              const auto lo = __builtin_amdgcn_permlane16_swap(w[0], w[2], false, false);
+              const auto hi = __builtin_amdgcn_permlane16_swap(w[1], w[3], false, false);
+              store_b128_saddr(hb, h_lane + uint32_t(64 * p), u32x4_t{lo[0], hi[0], lo[1], hi[1]});
+            }
           }
         }
 #pragma unroll
@@ -912,11 +933,23 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 
 int device_cu_count();
 
+template <typename CuT, bool kL2, int NRG>
+void launch_slices(dim3 grid, hipStream_t st, const uint16_t* q, const uint16_t* v, const float* state,
+                   const CuT* cu, int N, int T, int HQ, int HV, uint16_t* out, float* final_state,
+                   const char* ws, int nt_bound, uint16_t* h, int h_chunks) {
+  if (h != nullptr)
+    hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, NRG, true>), grid, dim3(SliceCfg<NRG>::kThreads), 0,
+                       st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound, h, h_chunks);
+  else
+    hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, NRG, false>), grid, dim3(SliceCfg<NRG>::kThreads), 0,
+                       st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound, nullptr, 0);
+}
+
 template <typename CuT, bool kL2>
 int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                    const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
                    const CuT* cu, int N, int T, int HQ, int HV, float scale, uint16_t* out,
-                   float* final_state, int slices, char* ws, hipStream_t st) {
+                   float* final_state, int slices, char* ws, uint16_t* h, int h_chunks, hipStream_t st) {
   const int nt_bound = T / C + N;
   if (nt_bound > 0) {
     // persistent workgroups, two per CU (75.5 KB of LDS each)
@@ -933,12 +966,12 @@ int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   const dim3 grid{8u * G * unsigned(slices) * ((units + 7u) / 8u), 1u, 1u};
   switch (slices) {
     case 8:
-      hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, 1>), grid, dim3(SliceCfg<1>::kThreads), 0,
-                         st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound);
+      launch_slices<CuT, kL2, 1>(grid, st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound,
+                                 h, h_chunks);
       break;
     case 4:
-      hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, 2>), grid, dim3(SliceCfg<2>::kThreads), 0,
-                         st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound);
+      launch_slices<CuT, kL2, 2>(grid, st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound,
+                                 h, h_chunks);
       break;
     default:
       return GDN_ERR_SHAPE;
@@ -1026,21 +1059,22 @@ int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          const float* A_log, const uint16_t* a, const float* dt_bias,
                          const uint16_t* b, const void* cu_seqlens, int cu_is_int32, int N, int T,
                          int HQ, int HV, float scale, uint16_t* out, float* final_state,
-                         int slices, void* workspace, int flags, hipStream_t st) {
+                         int slices, void* workspace, int flags, hipStream_t st, uint16_t* h,
+                         int h_chunks) {
   char* ws = static_cast<char*>(workspace);
   const bool l2 = (flags & GDN_QK_L2NORM) != 0;
   if (cu_is_int32) {
     const int32_t* cu = static_cast<const int32_t*>(cu_seqlens);
     return l2 ? launch_split_t<int32_t, true>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                              out, final_state, slices, ws, st)
+                                              out, final_state, slices, ws, h, h_chunks, st)
               : launch_split_t<int32_t, false>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                               out, final_state, slices, ws, st);
+                                               out, final_state, slices, ws, h, h_chunks, st);
   }
   const int64_t* cu = static_cast<const int64_t*>(cu_seqlens);
   return l2 ? launch_split_t<int64_t, true>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                            out, final_state, slices, ws, st)
+                                            out, final_state, slices, ws, h, h_chunks, st)
             : launch_split_t<int64_t, false>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                             out, final_state, slices, ws, st);
+                                             out, final_state, slices, ws, h, h_chunks, st);
 }
 
 }  // namespace gdn

@@ -23,6 +23,7 @@ stream.
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Optional
 
 import torch
@@ -43,6 +44,44 @@ def _resolve_scale(scale) -> float:
     return float(scale)
 
 
+# Host copies of cu_seqlens by tensor object: (weak reference, version, copy).
+_CU_HOST = {}
+# Path choices by (host copy, T, HV, device): (the host copy, slices per
+# chain, 0 = fused); holding the copy keeps its id from being reused.
+_CHOICE = {}
+# Split-path workspaces by (device, stream), reused by later calls on the
+# same stream (stream order keeps them from overlapping).
+_WORKSPACE = {}
+
+
+def host_cu_seqlens(cu_seqlens: torch.Tensor) -> torch.Tensor:
+    """``cu_seqlens`` in host memory: one device-to-host read per tensor object
+    and version, kept while the tensor lives.  Torch advances a tensor's
+    version on every in-place write made through torch, so a rewritten
+    ``cu_seqlens`` is read again; a write that bypasses torch (a raw kernel
+    on its storage) is not seen -- pass a new tensor then."""
+    ent = _CU_HOST.get(id(cu_seqlens))
+    if ent is not None and ent[0]() is cu_seqlens and ent[1] == cu_seqlens._version:
+        return ent[2]
+    host = cu_seqlens.detach().to("cpu").contiguous()
+    if len(_CU_HOST) >= 64:
+        for key in [key for key, e in _CU_HOST.items() if e[0]() is None]:
+            del _CU_HOST[key]
+        if len(_CU_HOST) >= 64:
+            _CU_HOST.clear()
+    _CU_HOST[id(cu_seqlens)] = (weakref.ref(cu_seqlens), cu_seqlens._version, host)
+    return host
+
+
+def _split_workspace(nbytes: int, device) -> torch.Tensor:
+    key = (device.index, _capi.stream_handle(device))
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = ws
+    return ws
+
+
 def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                     num_q_heads: int = NUM_Q_HEADS, num_v_heads: int = NUM_V_HEADS,
                     check_total: bool = True) -> Optional[torch.Tensor]:
@@ -50,7 +89,8 @@ def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
 
     ``check_total`` keeps the reference's ``cu_seqlens[-1] == T`` check
     (PRE:1665) and returns the host copy of ``cu_seqlens`` it reads for it
-    (one device-to-host copy); else None.
+    (one device-to-host copy per tensor and version, :func:`host_cu_seqlens`);
+    else None.
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda
     assert A_log.is_cuda and a.is_cuda and dt_bias.is_cuda and b.is_cuda and cu_seqlens.is_cuda
@@ -75,7 +115,7 @@ def validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
     if state is not None:
         assert state.shape == (cu_seqlens.numel() - 1, num_v_heads, HEAD_SIZE, HEAD_SIZE)
     if check_total:
-        cu_host = cu_seqlens.detach().to("cpu").contiguous()
+        cu_host = host_cu_seqlens(cu_seqlens)
         assert int(cu_host[-1]) == q.shape[0]
         return cu_host
     return None
@@ -190,11 +230,18 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
     assert final_state.dtype == torch.float32 and final_state.is_contiguous()
     assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
     assert path in ("auto", "fused", "split"), path
-    if path == "auto" and h is None and cu_host is not None:
-        chosen = choose_slices(cu_host, T, nv)
+    if path == "auto" and cu_host is not None:
+        key = (id(cu_host), T, nv, q.device.index)
+        ent = _CHOICE.get(key)
+        if ent is not None and ent[0] is cu_host:
+            chosen = ent[1]
+        else:
+            chosen = choose_slices(cu_host, T, nv) if N > 0 else 0
+            if len(_CHOICE) >= 256:
+                _CHOICE.clear()
+            _CHOICE[key] = (cu_host, chosen)
         path, slices = ("split", chosen) if chosen else ("fused", slices)
     if path == "split":
-        assert h is None, "the per-chunk states are written by the fused kernel only"
         ws_need = split_workspace_bytes(N, T, nq, nv)
     elif path == "auto" and h is None:
         ws_need = workspace_bytes(N, T, nq, nv)
@@ -202,9 +249,21 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
         ws_need = 0
         workspace = None
     if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
-        workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
+        workspace = _split_workspace(ws_need, q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     flags = _capi.GDN_QK_L2NORM if qk_l2norm else 0
+    if h is not None:
+        assert h.dtype == torch.bfloat16 and h.is_contiguous() and h.device == q.device
+        assert h.dim() == 4 and h.shape[1:] == (nv, HEAD_SIZE, HEAD_SIZE)
+    if path == "split" and h is not None:
+        rc = _capi.lib().gdn_prefill_split_h_fwd(
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
+            _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
+            1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
+            _capi.ptr(output), _capi.ptr(final_state), _capi.ptr(h), h.shape[0], int(slices),
+            _capi.ptr(workspace), ws_bytes, flags, _capi.stream_handle(q.device))
+        _capi.check(rc, "gdn_prefill_split_h_fwd")
+        return output, final_state
     if path == "split":
         rc = _capi.lib().gdn_prefill_split_fwd(
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
@@ -215,8 +274,6 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
         _capi.check(rc, "gdn_prefill_split_fwd")
         return output, final_state
     if h is not None:
-        assert h.dtype == torch.bfloat16 and h.is_contiguous() and h.device == q.device
-        assert h.dim() == 4 and h.shape[1:] == (nv, HEAD_SIZE, HEAD_SIZE)
         rc = _capi.lib().gdn_prefill_h_fwd(
             _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
             _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
@@ -237,23 +294,30 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
 
 @torch.no_grad()
 def gdn_prefill_h(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
-                  output=None, final_state=None, h=None, workspace=None, qk_l2norm: bool = False):
+                  output=None, final_state=None, h=None, workspace=None, qk_l2norm: bool = False,
+                  path: str = "auto", slices: int = 8):
     """:func:`gdn_prefill` that also returns ``h [NT, HV, 128, 128]`` bf16, the
     state entering every 64-token chunk: ``h[chunk_offset(n) + i]`` is the
     state of sequence ``n`` before its chunk ``i`` (the initial state for
     ``i = 0``), as ``chunk_gated_delta_rule_fwd_h`` stores it (PRE:1341-1398,
     1153-1160; round to nearest even).  Returns ``(output, final_state, h)``.
-    Reads ``cu_seqlens`` on the host to size ``h`` (as the reference's chunk
-    index preparation does, PRE:175-209).
+    Reads ``cu_seqlens`` on the host once, for the reference's
+    ``cu_seqlens[-1] == T`` check, to size ``h`` (as the reference's chunk
+    index preparation does, PRE:175-209) and for the path choice: ``path``
+    as for :func:`gdn_prefill` -- with few chains the split path writes ``h``
+    from its state slices (the reference writes it from its V-split grid,
+    PRE:1365-1393).
     """
     T = q.shape[0]
     nv = v.shape[1]
-    NT = num_chunks(cu_seqlens, T)
+    cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, q.shape[1], nv)
+    NT = num_chunks(cu_host, T)
     if h is None:
         h = torch.empty(NT, nv, HEAD_SIZE, HEAD_SIZE, dtype=torch.bfloat16, device=q.device)
     assert h.shape[0] >= NT, (h.shape, NT)
-    o, s = gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
-                       final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h)
+    o, s = _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
+                   final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h,
+                   path=path, slices=slices, cu_host=cu_host)
     return o, s, h
 
 
