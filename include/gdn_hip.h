@@ -46,7 +46,16 @@ extern "C" {
  *   reference expects normalised inputs from its caller and has no such
  *   option. */
 #define GDN_QK_L2NORM 1
-#define GDN_FLAGS_ALL 1
+/* GDN_NO_SEAMS (prefill entry points): with few chains the split path may
+ *   cut the longest sequences in two in time -- the tail runs from a zero
+ *   state beside a transition chain (v = 0 from the identity) and a seam pass
+ *   adds the head's state to the tail's outputs and final state -- so that
+ *   CUs left idle shorten the longest chain (no reference counterpart; the
+ *   reference runs every chain serially).  This bit runs every chain whole,
+ *   as the fused kernel does.  Decode entry points reject it. */
+#define GDN_NO_SEAMS 2
+#define GDN_FLAGS_ALL 3
+#define GDN_DECODE_FLAGS_ALL 1
 
 /* ABI version of the loaded library (GDN_ABI_VERSION). */
 int gdn_abi_version(void);

@@ -68,7 +68,7 @@ def test_argument_errors_return_before_launch():
     assert lib.gdn_prefill_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 7, 1.0, P, P, None, 0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 1, None, 0, 0, None) == capi.GDN_ERR_NULL
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, -1, None, 0, 0, None) == capi.GDN_ERR_SHAPE
-    assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, None, 0, 2, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, P, 1, None, 0, 4, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 6, 1.0, P, P, P, 1, None, 0, 0, None) == capi.GDN_ERR_SHAPE
     assert lib.gdn_prefill_chunk_count(None, 0, 1, 1) == -1
     assert lib.gdn_prefill_split_h_fwd(P, P, P, P, P, P, P, P, P, 0, 1, 1, 4, 8, 1.0, P, P, None, 1, 8, P, 1 << 30, 0, None) == capi.GDN_ERR_NULL

@@ -168,22 +168,30 @@ def test_prefill_long_sequence_split_is_bit_exact(device, path):
     """One 131 072-token sequence (2 048 chunks per chain): the run split at
     a chunk boundary, the second half started from the first half's final
     state, reproduces the single run bit for bit (same operations in the
-    same order; the fp32 state passes through memory unchanged)."""
+    same order; the fp32 state passes through memory unchanged) when every
+    chain runs whole (seams=False)."""
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
     T, H = 131072, 65536
     print(f"prefill long sequence T={T} path={path}", flush=True)
     x = inp.prefill_inputs([T], seed=4500, with_state=True)
     g = _to(x, device)
-    o, s = _run(pre, g, path=path)
+    o, s = _run(pre, g, path=path, seams=False)
     a = {k: (v[:H] if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == T else v) for k, v in g.items()}
     b = {k: (v[H:] if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] == T else v) for k, v in g.items()}
     a["cu_seqlens"] = torch.tensor([0, H], dtype=torch.int64, device=device)
     b["cu_seqlens"] = torch.tensor([0, T - H], dtype=torch.int64, device=device)
-    oa, sa = _run(pre, a, path=path)
+    oa, sa = _run(pre, a, path=path, seams=False)
     b["state"] = sa
-    ob, sb = _run(pre, b, path=path)
+    ob, sb = _run(pre, b, path=path, seams=False)
     torch.cuda.synchronize()
     assert torch.equal(torch.cat([oa, ob]), o)
     assert torch.equal(sb, s)
     assert bool(torch.isfinite(s).all()) and float(s.abs().max()) < 1e3
+    if path == "auto":
+        # the split path's seam (tail from a zero state beside the transition
+        # chain) agrees with the serial chain within the state and output bars
+        o2, s2 = _run(pre, g, path=path)
+        torch.cuda.synchronize()
+        assert float((s2 - s).norm() / s.norm()) <= 1e-3
+        torch.testing.assert_close(o2.float(), o.float(), atol=1e-2, rtol=1e-2)

@@ -19,6 +19,7 @@ GDN_ERR_NULL = -1001
 GDN_ERR_SHAPE = -1002
 GDN_ERR_WORKSPACE = -1003
 GDN_QK_L2NORM = 1
+GDN_NO_SEAMS = 2
 GDN_ACT_NONE = 0
 GDN_ACT_SILU = 1
 

@@ -382,7 +382,7 @@ extern "C" int gdn_decode_multi_fwd(const uint16_t* q, const uint16_t* k, const 
   const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
   if (rc != GDN_OK) return rc;
   if (T < 1) return GDN_ERR_SHAPE;
-  if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
+  if (flags & ~GDN_DECODE_FLAGS_ALL) return GDN_ERR_SHAPE;
   return launch_decode_multi(q, k, v, state, new_state, A_log, a, dt_bias, b, out, B, T, HQ, HV,
                              scale, flags, stream);
 }
@@ -404,7 +404,7 @@ extern "C" int gdn_decode_ex_fwd(const uint16_t* q, const uint16_t* k, const uin
                                  void* stream) {
   const int rc = check_decode_args(q, k, v, new_state, A_log, a, dt_bias, b, out, B, HQ, HV);
   if (rc != GDN_OK) return rc;
-  if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
+  if (flags & ~GDN_DECODE_FLAGS_ALL) return GDN_ERR_SHAPE;
   return launch_decode(q, k, v, state, new_state, A_log, a, dt_bias, b, out, nullptr, B, HQ, HV,
                        B, scale, flags, stream);
 }

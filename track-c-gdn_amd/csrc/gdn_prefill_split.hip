@@ -71,6 +71,116 @@ __host__ __device__ inline size_t order_offset(int n_slots, int HQ, int HV) {
   return size_t(n_slots) * (size_t(HV) * size_t(kBlob) + size_t(HQ) * size_t(kKcBytes));
 }
 
+// ---------------------------------------------------------------------------
+// Time splits ("seams") of long chains.  With workgroups to spare (few chains
+// on many CUs) a sequence of Lc chunks is cut at sp = ceil(Lc / 2): its head
+// [0, sp) runs as usual from the initial state; its tail [sp, Lc) runs at the
+// same time twice, from a zero state (giving the tail's outputs O0 and final
+// state S0) and as the transition chain: the same recurrence with v = 0 from
+// the identity, whose "state" X_c is the product of the tail's per-chunk
+// transitions M (S_{c+1} = S_c M_c + B_c, M independent of v) and whose
+// outputs OX_c = G_c X_c^T are the outputs' linear part.  With S_sp the head's
+// final state, the true tail outputs are O0_c + OX_c S_sp^T and the final
+// state S_sp X + S0; gdn_prefill_seam_kernel adds those terms.
+//
+// The plan is made on the device from the sequences ranked by length
+// (order[]): seams go to the j longest sequences, j <= the workgroups left
+// idle allow, choosing j by a chunk-period model (a split halves the longest
+// chain; the seam pass costs about kSeamCostChunks chunk periods).
+constexpr int kMaxSeams = 8;          // seams per launch
+constexpr int kSeamMaxChains = 64;    // (sequence, v-head) chains up to which seams are considered
+constexpr int kSeamMinChunks = 8;     // shortest chain split
+constexpr int kSeamCostChunks = 5;    // seam pass, in chunk periods of a slice
+
+__host__ __device__ inline int seam_split_chunk(int chunks) { return (chunks + 1) / 2; }
+
+// Seams the grid has room for (host and device): workgroups beyond the
+// N * HV * slices of the chains, two extra chains (tail, transition) per seam.
+__host__ __device__ inline int seam_room(int N, int HV, int slices, int cus) {
+  const long long chains = (long long)N * HV;
+  if (chains <= 0 || chains > kSeamMaxChains || cus <= 0) return 0;
+  const long long idle = (long long)cus - chains * slices;
+  if (idle <= 0) return 0;
+  long long k = idle / (2LL * HV * slices);
+  if (k > N) k = N;
+  if (k > kMaxSeams) k = kMaxSeams;
+  return int(k);
+}
+
+// Workspace of the seams, after the order[] ints: the seam plan (below), per
+// seam and v-head three fp32 [128][128] states (the head's final state, the
+// tail's zero-state final state, the transition X stored transposed), then
+// the transition outputs OX of every seam's tail tokens, bf16 [rows][HV][128].
+//
+// The plan, written by the slice launch for the seam pass: kSeamPlanStride
+// ints per seam slot j < the launch's room, sequence -1 in the slots past the
+// seam count.
+constexpr int kSeamPlanStride = 8;
+enum SeamPlanField { SP_SEQ, SP_BOS, SP_LEN, SP_SPLIT, SP_CHUNKS, SP_OX_ROW };
+constexpr size_t kSeamPlanBytes = 512;
+static_assert(size_t(kSeamPlanStride) * kMaxSeams * sizeof(int) <= kSeamPlanBytes, "seam plan");
+__host__ __device__ inline size_t seam_plan_offset(int n_slots, int N, int HQ, int HV) {
+  return order_offset(n_slots, HQ, HV) + (size_t(N) * sizeof(int) + 255) / 256 * 256;
+}
+__host__ __device__ inline size_t seam_offset(int n_slots, int N, int HQ, int HV) {
+  return seam_plan_offset(n_slots, N, HQ, HV) + kSeamPlanBytes;
+}
+constexpr size_t kSeamStateBytes = size_t(D) * D * 4;
+__host__ __device__ inline size_t seam_ox_offset(int n_slots, int N, int HQ, int HV) {
+  const int k = N < kMaxSeams ? N : kMaxSeams;
+  return seam_offset(n_slots, N, HQ, HV) + size_t(k) * HV * 3 * kSeamStateBytes;
+}
+__host__ __device__ inline size_t seam_bytes(int N, int T, int HV) {
+  if ((long long)N * HV > kSeamMaxChains) return 0;
+  const int k = N < kMaxSeams ? N : kMaxSeams;
+  return size_t(k) * HV * 3 * kSeamStateBytes + size_t(T / 2 + C * k) * HV * D * 2;
+}
+
+// The seams of a launch, identical in every workgroup and in the seam pass:
+// their count; the split chunk of seam j is seam_split_chunk of the chunk
+// count of sequence order[j].  Chunk counts are clamped as the chains clamp
+// them.  Wave-uniform.
+template <typename CuT>
+__device__ int seam_count(const CuT* cu, const int* order, int N, int T, int nt_bound, int room) {
+  if (room <= 0) return 0;
+  auto chunks_of = [&](int r) {
+    const int nn = order[r];
+    int bb, ll;
+    seq_bounds(cu, nn, T, bb, ll);
+    return (ll + C - 1) / C;
+  };
+  const int l0 = chunks_of(0);
+  int best = l0, best_k = 0;
+  for (int kk = 1; kk <= room; ++kk) {
+    if (chunks_of(kk - 1) < kSeamMinChunks) break;
+    const int rest = kk < N ? chunks_of(kk) : 0;
+    const int span = max(seam_split_chunk(l0), rest) + kSeamCostChunks;
+    if (span < best) {
+      best = span;
+      best_k = kk;
+    }
+  }
+  (void)nt_bound;
+  return best_k;
+}
+
+// OX rows of the seams before seam j (their tail tokens).  OX holds
+// seam_ox_rows(N, T) rows; writers drop rows past it (ranges that overlap
+// can ask for more).
+template <typename CuT>
+__device__ int seam_rows_before(const CuT* cu, const int* order, int T, int j) {
+  int row = 0;
+  for (int jj = 0; jj < j; ++jj) {
+    int bb, ll;
+    seq_bounds(cu, order[jj], T, bb, ll);
+    row += max(0, ll - C * seam_split_chunk((ll + C - 1) / C));
+  }
+  return row;
+}
+__host__ __device__ inline int seam_ox_rows(int N, int T) {
+  return T / 2 + C * (N < kMaxSeams ? N : kMaxSeams);
+}
+
 // HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): from
 // base + off (base uniform, off a 32-bit lane offset) to LDS byte address
 // lds + 16 l for lane l (lds uniform).  Issued from asm so that the compiler
@@ -514,8 +624,8 @@ template <typename CuT, bool kL2, int NRG, bool kH>
 __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ v, const float* __restrict__ h0,
     const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV,
-    uint16_t* __restrict__ out, float* __restrict__ ht, const char* __restrict__ ws, int nt_bound,
-    uint16_t* __restrict__ hout, int h_chunks) {
+    uint16_t* __restrict__ out, float* __restrict__ ht, char* __restrict__ ws, int nt_bound,
+    uint16_t* __restrict__ hout, int h_chunks, int seam_room_) {
   using Cfg = SliceCfg<NRG>;
   constexpr int R = Cfg::R;
   constexpr int VS = Cfg::VS;
@@ -538,22 +648,52 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   // unit position j of XCD x is sorted unit 8 j + x for even j and 8 j + 7 - x
   // for odd j, which evens out the work per XCD, and the workgroups that wait
   // for a CU land where the shortest of the first units ran.
+  //
+  // Workgroups past the chains' grid (ids from base_ids on) run the tails of
+  // the seams: for each seam unit (seam j, qk-head hq) 2 G S workgroups, the
+  // zero-state tail chains then the transition chains, ids 8 apart on one
+  // XCD; the seam units continue the XCD rotation after the last chain unit.
   const int G = HV / HQ;
-  const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
-  const int jx = id_row / (G * S);
-  const int su = 8 * jx + ((jx & 1) ? 7 - xcd : xcd);
-  if (su >= N * HQ) return;
-  const int within = id_row - jx * (G * S);
-  const int m = within / S, s = within - m * S;
-  const int n = reinterpret_cast<const int*>(ws + order_offset(nt_bound, HQ, HV))[su / HQ];
-  const int hq = su - (su / HQ) * HQ;
-  const int hv = hq * G + m;
-  const int vb = R * s;                         // first state row of the slice
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4, c = lane & 15;
+  const int* order = reinterpret_cast<const int*>(ws + order_offset(nt_bound, HQ, HV));
+  const int n_units = N * HQ;
+  const int base_ids = 8 * G * S * ((n_units + 7) / 8);
+  // 0: the whole chain; 1: a seam's head; 2: its tail from a zero state; 3: its transition chain
+  int role = 0, rank, m, s, hq;
+  const int n_seams = seam_count(cu_seqlens, order, N, T, nt_bound, seam_room_);
+  if (int(blockIdx.x) < base_ids) {
+    const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
+    const int jx = id_row / (G * S);
+    const int su = 8 * jx + ((jx & 1) ? 7 - xcd : xcd);
+    if (su >= n_units) return;
+    const int within = id_row - jx * (G * S);
+    m = within / S;
+    s = within - m * S;
+    rank = su / HQ;
+    hq = su - rank * HQ;
+    if (rank < n_seams) role = 1;
+  } else {
+    const int e = int(blockIdx.x) - base_ids;
+    const int xcd = e & 7, w = e >> 3;
+    const int ux = 8 * (w / (2 * G * S)) + xcd - (n_units & 7);
+    if (ux < 0 || ux >= n_seams * HQ) return;
+    const int within = w - (w / (2 * G * S)) * (2 * G * S);
+    role = 2 + within / (G * S);
+    m = (within % (G * S)) / S;
+    s = within % S;
+    rank = ux / HQ;
+    hq = ux - rank * HQ;
+  }
+  const int n = order[rank];
+  const int hv = hq * G + m;
+  const int vb = R * s;                         // first state row of the slice
+  int* plan = reinterpret_cast<int*>(ws + seam_plan_offset(nt_bound, N, HQ, HV));
+  if (blockIdx.x == 0 && tid == 0)
+    for (int jj = n_seams; jj < seam_room_; ++jj) plan[kSeamPlanStride * jj + SP_SEQ] = -1;
+
   int bos, len;
   seq_bounds(cu_seqlens, n, T, bos, len);
   const size_t qk_stride = size_t(HQ) * D;
@@ -564,9 +704,30 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   // well-formed cu_seqlens.  Ranges that overlap can count more chunks: the
   // chain then stops at the last slot the workspace holds (results
   // unspecified, every record and K image read in bounds).
-  const int n_chunks = min((len + C - 1) / C, max(0, nt_bound - coff));
+  const int n_all = min((len + C - 1) / C, max(0, nt_bound - coff));
+  // Chunks [ch0, ch0 + n_chunks) of the sequence: all of them, or a seam's
+  // head [0, sp) or tail [sp, n_all).
+  const int sp = seam_split_chunk(n_all);
+  const int ch0 = role >= 2 ? sp : 0;
+  const int n_chunks = role == 0 ? n_all : (role == 1 ? sp : n_all - sp);
   // workspace record of chunk ch of this chain
   auto record = [&](int ch) { return ws + (size_t(coff + ch) * HV + hv) * kBlob; };
+  // seam state j of kind (0 head final, 1 tail final, 2 transition X^T) of this v-head
+  auto seam_state = [&](int kind) {
+    return reinterpret_cast<float*>(ws + seam_offset(nt_bound, N, HQ, HV) +
+                                    ((size_t(rank) * HV + hv) * 3 + kind) * kSeamStateBytes);
+  };
+  // first OX row of seam `rank`: the tail tokens of the seams before it
+  auto seam_ox_row = [&]() { return seam_rows_before(cu_seqlens, order, T, rank); };
+  if (role == 1 && hq == 0 && m == 0 && s == 0 && tid == 0) {
+    int* e = plan + kSeamPlanStride * rank;
+    e[SP_SEQ] = n;
+    e[SP_BOS] = bos;
+    e[SP_LEN] = len;
+    e[SP_SPLIT] = sp;
+    e[SP_CHUNKS] = n_all;
+    e[SP_OX_ROW] = seam_ox_row();
+  }
 
   if (wave < 2 * NRG) {
     // ======================= state / output waves
@@ -577,13 +738,22 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
     // kH: byte offset of this lane's 16 bytes in an h slot of the chain
     const uint32_t h_lane = uint32_t((v0 + c) * D + ((g & 1) ? 4 * (g + 3) : 4 * g)) * 2u;
     // Sacc[kb][i] = S[v0 + c][16 kb + 4 g + i]: the S^T accumulator tiles.
+    // A seam's tail starts from zeros, its transition chain from the identity.
     f32x4 Sacc[8];
-    const float* h0row = h0 == nullptr ? nullptr
-                                       : h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
+    const float* h0row = (h0 == nullptr || role >= 2) ? nullptr
+                         : h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb)
       Sacc[kb] = (h0row && !out_role) ? *reinterpret_cast<const f32x4*>(h0row + 16 * kb + 4 * g)
                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    if (role == 3) {
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Sacc[kb][i] = (v0 + c == 16 * kb + 4 * g + i) ? 1.f : 0.f;
+    }
+    // the transition chain reads its v as zeros
+    const int vmask = role == 3 ? 0 : -1;
     // Fragments of the chunk's record this wave multiplies with (state: T_a,
     // T_b, -A_ba; output: P), loaded kAhead chunks ahead.
     constexpr int kAhead = Cfg::kAhead;
@@ -596,10 +766,10 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
       for (int f = 0; f < 6; ++f) dst[f] = *reinterpret_cast<const f16x8*>(rec + f * kFrag);
     };
     // (the chunk index is clamped: every chunk issues the same loads)
-    const int last_ch = n_chunks - 1;
+    const int last_ch = ch0 + n_chunks - 1;
     if (n_chunks > 0) {
 #pragma unroll
-      for (int a = 0; a < kAhead; ++a) load_frags(min(a, last_ch), fr[a]);
+      for (int a = 0; a < kAhead; ++a) load_frags(min(ch0 + a, last_ch), fr[a]);
     }
     // Per-lane element offsets of the two 4-column pieces of a Q fragment
     // (raw row 16 tb + c, columns 32 p + 4 g .. and 32 p + 16 + 4 g ..).
@@ -660,9 +830,10 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
     };
     // One chunk; b3c (0, 1, 2) is the buffer set as a compile-time constant,
     // so every LDS address is a loop-invariant lane offset plus an immediate.
-    auto chunk = [&](auto b3c, auto rolec, int ch) __attribute__((always_inline)) {
+    auto chunk = [&](auto b3c, auto rolec, int jj) __attribute__((always_inline)) {
       constexpr int b3 = decltype(b3c)::value;
       constexpr bool kOut = decltype(rolec)::value != 0;
+      const int ch = ch0 + jj;                  // the chunk; jj its place in this chain's run
       const int L = chunk_len(ch);
       const float* gd = reinterpret_cast<const float*>(gt[b3]);
       const _Float16* kc = Kc[b3];
@@ -680,7 +851,8 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           for (int tb = 0; tb < 4; ++tb) {
             const int t = 16 * tb + 4 * g + mm;
             const i16x4_t vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4_t*)&rv[b3][t * R + 8 * ((col >> 3) ^ (t & (VS - 1))) + (col & 7)]);
+                (__attribute__((address_space(3))) i16x4_t*)&rv[b3][t * R + 8 * ((col >> 3) ^ (t & (VS - 1))) + (col & 7)]) &
+                i16x4_t{short(vmask), short(vmask), short(vmask), short(vmask)};
             const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + 16 * tb + 4 * g]);
             const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * tb + 4 * g]);
 #pragma unroll
@@ -717,7 +889,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
         // the new state's bf16 image for the output wave, and K S^T of the next chunk
 #pragma unroll
         for (int p = 0; p < 4; ++p) sSb[r][p][lane] = pack2_bf(Sacc[2 * p], Sacc[2 * p + 1]);
-        if (ch + 1 < n_chunks) ks_of(Kc[(b3 + 1) % NB], KS);
+        if (jj + 1 < n_chunks) ks_of(Kc[(b3 + 1) % NB], KS);
       } else {
         // ---- O^T = S Q^T (transposed output tile: lane (g, c) of OT[tb] holds
         //      token 16 tb + c, state rows v0 + 4 g .. +3)
@@ -776,8 +948,16 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 #pragma unroll
           for (int f = 0; f < 6; ++f) OT[kPt[f]] = mfma16(vn[kPp[f]], pf[f], OT[kPt[f]]);
           // the chunk's L rows as one buffer: stores of rows past L are dropped
+          // (a transition chain's rows go to its seam's OX rows, cut at their end)
+          uint16_t* obase = out + size_t(bos + ch * C) * v_stride;
+          uint32_t orow_n = uint32_t(L);
+          if (role == 3) {
+            const int r0 = seam_ox_row() + (ch - ch0) * C;
+            obase = reinterpret_cast<uint16_t*>(ws + seam_ox_offset(nt_bound, N, HQ, HV)) + size_t(r0) * v_stride;
+            orow_n = uint32_t(max(0, min(L, seam_ox_rows(N, T) - r0)));
+          }
           const __amdgpu_buffer_rsrc_t orows =
-              uniform_buffer(out + size_t(bos + ch * C) * v_stride, uint32_t(L) * uint32_t(v_stride) * 2u);
+              uniform_buffer(obase, orow_n * uint32_t(v_stride) * 2u);
           const uint32_t ocol = uint32_t(hv * D + v0 + 4 * g) * 2u;
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
@@ -818,9 +998,18 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
       else run(IC<0>{});
     }
     if (!out_role) {
-      float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
+      if (role == 3) {                          // X stored transposed: X^T[k][v]
+        float* dst = seam_state(2);
 #pragma unroll
-      for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[size_t(16 * kb + 4 * g + i) * D + v0 + c] = Sacc[kb][i];
+      } else {
+        float* dst = (role == 0 ? ht + (size_t(n) * HV + hv) * size_t(D) * D : seam_state(role - 1)) +
+                     size_t(v0 + c) * D;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) *reinterpret_cast<f32x4*>(dst + 16 * kb + 4 * g) = Sacc[kb];
+      }
     }
   } else {
     // ======================= copy waves
@@ -856,9 +1045,10 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           v_off[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane % VS) ^ (row & (VS - 1))) * 16u;
         }
       }
-      auto issue_copies = [&](int ch) {
+      auto issue_copies = [&](int jj) {
+        const int ch = ch0 + jj;                // the chunk; jj its place in the run
         const int t0 = bos + ch * C, L = chunk_len(ch);
-        const int b3 = ch % NB;
+        const int b3 = jj % NB;
         if constexpr (CW == 0) {
           const uint32_t lq = lds_u32(rq[b3]);
           if (L == C) {
@@ -931,25 +1121,160 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Seam pass, after the slices: for seam j and v-head hv (blockIdx.y), pieces
+// 0 .. kSeamStatePieces - 1 (blockIdx.x) write a 16 x 64 block each of the
+// sequence's final state S_sp X + S0; piece p >= kSeamStatePieces adds
+// OX_c S_sp^T to the outputs of tail chunk c = sp + p - kSeamStatePieces (the
+// part of the tail outputs that depends on the state the head reached).  The
+// final state takes fp32-accurate products (each fp32 operand split into two
+// fp16 parts, three 16x16x16 MFMA products); the outputs bf16 products, as
+// the output path does.  Four waves; every wave issues all its loads (both
+// operands and, for outputs, the values it adds to) before its first MFMA,
+// so a piece costs one memory round trip and a few dozen MFMAs.
+constexpr int kSeamThreads = 256;
+constexpr int kSeamStatePieces = 2 * D / 16;
+
+__device__ __forceinline__ void split_f16(const f32x4& x, f16x4_t& hi, f16x4_t& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = (_Float16)x[i];
+    lo[i] = (_Float16)(x[i] - (float)hi[i]);
+  }
+}
+
+template <typename CuT>
+__global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
+    const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV, const char* __restrict__ ws,
+    int nt_bound, int seam_room_, uint16_t* __restrict__ out, float* __restrict__ ht) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int j = int(blockIdx.y) / HV, hv = int(blockIdx.y) - j * HV;
+  if (j >= seam_room_) return;
+  // the plan entry the slices wrote for seam slot j (sequence or -1, bounds,
+  // split, first OX row), one load
+  const int* plan = reinterpret_cast<const int*>(ws + seam_plan_offset(nt_bound, N, HQ, HV));
+  const int pe = plan[kSeamPlanStride * j + (lane & (kSeamPlanStride - 1))];   // lane f: field f
+  const int n = __builtin_amdgcn_readlane(pe, SP_SEQ);
+  if (n < 0) return;
+  const int bos = __builtin_amdgcn_readlane(pe, SP_BOS), len = __builtin_amdgcn_readlane(pe, SP_LEN);
+  const int sp = __builtin_amdgcn_readlane(pe, SP_SPLIT), n_all = __builtin_amdgcn_readlane(pe, SP_CHUNKS);
+  const int ox_row0 = __builtin_amdgcn_readlane(pe, SP_OX_ROW);
+  const int piece = int(blockIdx.x);
+  if (piece >= kSeamStatePieces + n_all - sp) return;
+  auto state = [&](int kind) {
+    return reinterpret_cast<const float*>(ws + seam_offset(nt_bound, N, HQ, HV) +
+                                          ((size_t(j) * HV + hv) * 3 + kind) * kSeamStateBytes);
+  };
+  const float* Ssp = state(0);
+  if (piece < kSeamStatePieces) {
+    // S_L[v][k] = sum_k' S_sp[v][k'] X[k'][k] + S0[v][k] for rows v of block
+    // tm = piece / 2; wave w: column block tn = 4 (piece % 2) + w
+    const int tm = piece >> 1, tn = 4 * (piece & 1) + wave;
+    const float* S0 = state(1);
+    const float* XT = state(2);
+    f32x4 sa[8], xb[8], acc;
+#pragma unroll
+    for (int tk = 0; tk < 8; ++tk) {
+      sa[tk] = *reinterpret_cast<const f32x4*>(&Ssp[size_t(16 * tm + c) * D + 16 * tk + 4 * g]);
+      xb[tk] = *reinterpret_cast<const f32x4*>(&XT[size_t(16 * tn + c) * D + 16 * tk + 4 * g]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = S0[size_t(16 * tm + 4 * g + i) * D + 16 * tn + c];
+#pragma unroll
+    for (int tk = 0; tk < 8; ++tk) {
+      f16x4_t ah, al, bh, bl;
+      split_f16(sa[tk], ah, al);
+      split_f16(xb[tk], bh, bl);
+      acc = mfma16k16(ah, bh, acc);
+      acc = mfma16k16(ah, bl, acc);
+      acc = mfma16k16(al, bh, acc);
+    }
+    float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[size_t(16 * tm + 4 * g + i) * D + 16 * tn + c] = acc[i];
+    return;
+  }
+  // Tail chunk ch: dO^T[v][t] = sum_k' S_sp[v][k'] OX[t][k'], added to
+  // out[t][hv][v]; wave w: row blocks tm = 2w, 2w + 1, token blocks tn 0..3
+  const int ch = sp + piece - kSeamStatePieces;
+  const int t0 = bos + ch * C, L = min(C, len - ch * C);
+  const int ox_rows = seam_ox_rows(N, T);
+  const int r0 = ox_row0 + (ch - sp) * C;
+  const size_t v_stride = size_t(HV) * D;
+  const uint16_t* OX = reinterpret_cast<const uint16_t*>(ws + seam_ox_offset(nt_bound, N, HQ, HV));
+  f32x4 sa[2][4][2];
+  uint4 ob[4][4];
+  uint2 ov[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int tk = 0; tk < 4; ++tk) {
+      const float* sr = &Ssp[size_t(16 * (2 * wave + u) + c) * D + 32 * tk + 8 * g];
+      sa[u][tk][0] = *reinterpret_cast<const f32x4*>(sr);
+      sa[u][tk][1] = *reinterpret_cast<const f32x4*>(sr + 4);
+    }
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) {
+    const int orow = min(r0 + 16 * tn + c, ox_rows - 1);   // rows past the region are never used
+#pragma unroll
+    for (int tk = 0; tk < 4; ++tk)
+      ob[tn][tk] = *reinterpret_cast<const uint4*>(&OX[size_t(orow) * v_stride + size_t(hv) * D + 32 * tk + 8 * g]);
+  }
+  auto valid = [&](int t) { return t < L && r0 + t < ox_rows; };
+  auto out_at = [&](int u, int tn) {
+    return reinterpret_cast<uint2*>(out + size_t(t0 + 16 * tn + c) * v_stride + size_t(hv) * D +
+                                    16 * (2 * wave + u) + 4 * g);
+  };
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) ov[u][tn] = valid(16 * tn + c) ? *out_at(u, tn) : uint2{0u, 0u};
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    bf16x8_t af[4];
+#pragma unroll
+    for (int tk = 0; tk < 4; ++tk) {
+      const f32x4 s0 = sa[u][tk][0], s1 = sa[u][tk][1];
+      af[tk] = bf16x8_t{(__bf16)s0[0], (__bf16)s0[1], (__bf16)s0[2], (__bf16)s0[3],
+                        (__bf16)s1[0], (__bf16)s1[1], (__bf16)s1[2], (__bf16)s1[3]};
+    }
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tk = 0; tk < 4; ++tk) acc = mfma16_bf(af[tk], __builtin_bit_cast(bf16x8_t, ob[tn][tk]), acc);
+      if (valid(16 * tn + c)) {
+        float f0, f1, f2, f3;
+        unpack_bf16x2(ov[u][tn].x, f0, f1);
+        unpack_bf16x2(ov[u][tn].y, f2, f3);
+        *out_at(u, tn) = uint2{cvt_pk_bf16(f0 + acc[0], f1 + acc[1]), cvt_pk_bf16(f2 + acc[2], f3 + acc[3])};
+      }
+    }
+  }
+}
+
 int device_cu_count();
 
 template <typename CuT, bool kL2, int NRG>
 void launch_slices(dim3 grid, hipStream_t st, const uint16_t* q, const uint16_t* v, const float* state,
                    const CuT* cu, int N, int T, int HQ, int HV, uint16_t* out, float* final_state,
-                   const char* ws, int nt_bound, uint16_t* h, int h_chunks) {
+                   char* ws, int nt_bound, uint16_t* h, int h_chunks, int room) {
   if (h != nullptr)
     hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, NRG, true>), grid, dim3(SliceCfg<NRG>::kThreads), 0,
-                       st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound, h, h_chunks);
+                       st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound, h, h_chunks, 0);
   else
     hipLaunchKernelGGL((gdn_prefill_slice_kernel<CuT, kL2, NRG, false>), grid, dim3(SliceCfg<NRG>::kThreads), 0,
-                       st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound, nullptr, 0);
+                       st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound, nullptr, 0, room);
 }
 
 template <typename CuT, bool kL2>
 int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                    const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
                    const CuT* cu, int N, int T, int HQ, int HV, float scale, uint16_t* out,
-                   float* final_state, int slices, char* ws, uint16_t* h, int h_chunks, hipStream_t st) {
+                   float* final_state, int slices, char* ws, uint16_t* h, int h_chunks, bool no_seams,
+                   hipStream_t st) {
   const int nt_bound = T / C + N;
   if (nt_bound > 0) {
     // persistent workgroups, two per CU (75.5 KB of LDS each)
@@ -963,18 +1288,33 @@ int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   }
   const unsigned units = unsigned(N) * unsigned(HQ);
   const unsigned G = unsigned(HV / HQ);
-  const dim3 grid{8u * G * unsigned(slices) * ((units + 7u) / 8u), 1u, 1u};
+  // Seams (time splits of the longest chains) use the CUs the slices leave
+  // idle; not with the per-chunk states (h), which the tails cannot give.
+  const int cus = device_cu_count();
+  const int room = (h == nullptr && !no_seams) ? seam_room(N, HV, slices, cus > 0 ? cus : 256) : 0;
+  const unsigned base = 8u * G * unsigned(slices) * ((units + 7u) / 8u);
+  const unsigned seam_units = unsigned(room) * unsigned(HQ) + (units & 7u);
+  const unsigned extra = room > 0 ? 8u * 2u * G * unsigned(slices) * ((seam_units + 7u) / 8u) : 0u;
+  const dim3 grid{base + extra, 1u, 1u};
   switch (slices) {
     case 8:
       launch_slices<CuT, kL2, 1>(grid, st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound,
-                                 h, h_chunks);
+                                 h, h_chunks, room);
       break;
     case 4:
       launch_slices<CuT, kL2, 2>(grid, st, q, v, state, cu, N, T, HQ, HV, out, final_state, ws, nt_bound,
-                                 h, h_chunks);
+                                 h, h_chunks, room);
       break;
     default:
       return GDN_ERR_SHAPE;
+  }
+  if (room > 0) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return -int(e);
+    // pieces: the final state's row blocks, then the longest possible tail
+    const dim3 sgrid{unsigned(kSeamStatePieces + (nt_bound + 1) / 2 + 1), unsigned(room * HV), 1u};
+    hipLaunchKernelGGL((gdn_prefill_seam_kernel<CuT>), sgrid, dim3(kSeamThreads), 0, st, cu, N, T, HQ, HV,
+                       ws, nt_bound, room, out, final_state);
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GDN_OK : -int(e);
@@ -1031,7 +1371,7 @@ namespace gdn {
 
 size_t prefill_split_workspace_bytes(int N, int T, int HQ, int HV) {
   if (N <= 0 || T < 0 || HQ <= 0 || HV <= 0) return 0;
-  return order_offset(T / C + N, HQ, HV) + (size_t(N) * sizeof(int) + 255) / 256 * 256;
+  return seam_offset(T / C + N, N, HQ, HV) + seam_bytes(N, T, HV);
 }
 
 int prefill_split_auto_slices(int N, int HV) {
@@ -1063,18 +1403,19 @@ int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          int h_chunks) {
   char* ws = static_cast<char*>(workspace);
   const bool l2 = (flags & GDN_QK_L2NORM) != 0;
+  const bool no_seams = (flags & GDN_NO_SEAMS) != 0;
   if (cu_is_int32) {
     const int32_t* cu = static_cast<const int32_t*>(cu_seqlens);
     return l2 ? launch_split_t<int32_t, true>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                              out, final_state, slices, ws, h, h_chunks, st)
+                                              out, final_state, slices, ws, h, h_chunks, no_seams, st)
               : launch_split_t<int32_t, false>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                               out, final_state, slices, ws, h, h_chunks, st);
+                                               out, final_state, slices, ws, h, h_chunks, no_seams, st);
   }
   const int64_t* cu = static_cast<const int64_t*>(cu_seqlens);
   return l2 ? launch_split_t<int64_t, true>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                            out, final_state, slices, ws, h, h_chunks, st)
+                                            out, final_state, slices, ws, h, h_chunks, no_seams, st)
             : launch_split_t<int64_t, false>(q, k, v, state, A_log, a, dt_bias, b, cu, N, T, HQ, HV, scale,
-                                             out, final_state, slices, ws, h, h_chunks, st);
+                                             out, final_state, slices, ws, h, h_chunks, no_seams, st);
 }
 
 }  // namespace gdn

@@ -167,7 +167,8 @@ def num_chunks(cu_seqlens: torch.Tensor, T: int) -> int:
 @torch.no_grad()
 def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
                 output=None, final_state=None, workspace=None, validate: bool = True,
-                qk_l2norm: bool = False, h=None, path: str = "auto", slices: int = 8):
+                qk_l2norm: bool = False, h=None, path: str = "auto", slices: int = 8,
+                seams: bool = True):
     """Chunked GDN prefill over packed varlen sequences, any ``HV % HQ == 0``.
 
     ``q, k [T, HQ, 128]``, ``v [T, HV, 128]``, ``a, b [T, HV]`` bf16;
@@ -189,7 +190,12 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     ``slices`` in (4, 8) state slices per chain.  Without ``qk_l2norm`` the
     two paths perform the state-path operations in the same order: their
     final states agree bit for bit but for rare last-place differences (one
-    or two sequences in thousands).
+    or two sequences in thousands).  ``seams=False`` keeps that equality
+    where the split path would otherwise cut its longest sequences in two in
+    time to use idle CUs (a zero-state tail and a transition chain beside the
+    head, joined by a seam pass; results then agree with the serial chain to
+    the rounding of the state path, and the per-chunk states ``h`` never use
+    seams).
 
     Input range: the state path multiplies fp16 operands, so k, v, the state
     and the intermediate X and Vn must stay below 65504 in magnitude (far
@@ -200,12 +206,13 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
                               v.shape[1], check_total=validate)
     return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
                    final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h,
-                   path=path, slices=slices, cu_host=cu_host)
+                   path=path, slices=slices, cu_host=cu_host, seams=seams)
 
 
 def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, output=None,
             final_state=None, workspace=None, qk_l2norm: bool = False, h=None,
-            path: str = "auto", slices: int = 8, cu_host: Optional[torch.Tensor] = None):
+            path: str = "auto", slices: int = 8, cu_host: Optional[torch.Tensor] = None,
+            seams: bool = True):
     """Allocation, layout and the C call behind :func:`gdn_prefill` (inputs
     already validated; ``cu_host``, when given, is the host copy of
     ``cu_seqlens`` the automatic path choice reads)."""
@@ -251,7 +258,7 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
     if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
         workspace = _split_workspace(ws_need, q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    flags = _capi.GDN_QK_L2NORM if qk_l2norm else 0
+    flags = (_capi.GDN_QK_L2NORM if qk_l2norm else 0) | (0 if seams else _capi.GDN_NO_SEAMS)
     if h is not None:
         assert h.dtype == torch.bfloat16 and h.is_contiguous() and h.device == q.device
         assert h.dim() == 4 and h.shape[1:] == (nv, HEAD_SIZE, HEAD_SIZE)
@@ -346,11 +353,11 @@ class PreparedPrefill:
     == T`` check, and the path choice of :func:`choose_slices`: ``path`` is
     ``"fused"``, ``"split4"`` or ``"split8"``); ``__call__`` only enqueues
     the launches on the stream that was current at construction.
-    ``qk_l2norm`` as for :func:`gdn_prefill`.
+    ``qk_l2norm`` and ``seams`` as for :func:`gdn_prefill`.
     """
 
     def __init__(self, q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
-                 final_state, *, qk_l2norm: bool = False):
+                 final_state, *, qk_l2norm: bool = False, seams: bool = True):
         T, nq, _ = q.shape
         nv = v.shape[1]
         cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv)
@@ -373,8 +380,8 @@ class PreparedPrefill:
             _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu_seqlens),
             1 if cu_seqlens.dtype == torch.int32 else 0, N, T, nq, nv,
             float(_resolve_scale(scale)), _capi.ptr(output), _capi.ptr(final_state))
-        tail = (_capi.ptr(self._ws), ws, _capi.GDN_QK_L2NORM if qk_l2norm else 0,
-                _capi.stream_handle(q.device))
+        flags = (_capi.GDN_QK_L2NORM if qk_l2norm else 0) | (0 if seams else _capi.GDN_NO_SEAMS)
+        tail = (_capi.ptr(self._ws), ws, flags, _capi.stream_handle(q.device))
         if self.slices:
             self._name = "gdn_prefill_split_fwd"
             self._args = head + (self.slices,) + tail
