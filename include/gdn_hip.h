@@ -46,14 +46,19 @@ extern "C" {
  *   reference expects normalised inputs from its caller and has no such
  *   option. */
 #define GDN_QK_L2NORM 1
-/* GDN_NO_SEAMS (prefill entry points): with few chains the split path may
- *   cut the longest sequences in two in time -- the tail runs from a zero
- *   state beside a transition chain (v = 0 from the identity) and a seam pass
- *   adds the head's state to the tail's outputs and final state -- so that
- *   CUs left idle shorten the longest chain (no reference counterpart; the
- *   reference runs every chain serially).  This bit runs every chain whole,
- *   as the fused kernel does.  Decode entry points reject it. */
+/* GDN_NO_SEAMS (prefill entry points): the split path (with few chains)
+ *   and the fused kernel under a plan (gdn_prefill_plan_fwd) may cut the
+ *   longest sequences in two in time -- the tail runs from a zero state
+ *   beside a transition chain (v = 0 from the identity) and a seam pass adds
+ *   the head's state to the tail's outputs and final state -- so that CUs
+ *   left idle shorten the longest chain (no reference counterpart; the
+ *   reference runs every chain serially).  Results then agree with the
+ *   serial chain to the rounding of the state path.  This bit runs every
+ *   chain whole.  Decode entry points reject it. */
 #define GDN_NO_SEAMS 2
+/* GDN_PLAN_FUSED (gdn_prefill_plan only): plan the fused kernel (with its
+ *   seams) whatever the lengths favour. */
+#define GDN_PLAN_FUSED 4
 #define GDN_FLAGS_ALL 3
 #define GDN_DECODE_FLAGS_ALL 1
 
@@ -198,6 +203,48 @@ int gdn_prefill_auto_slices(int N, int HV);
  */
 int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int N, int T, int HV,
                               int cus);
+
+/*
+ * Launch plan of a prefill call, made on the host from a HOST copy of
+ * cu_seqlens (N+1 entries; the reference's run() reads cu_seqlens back for
+ * its cu_seqlens[-1] == T check, PRE:1665, so its caller holds one): the
+ * path of gdn_prefill_choose_slices, and for the fused kernel the seams that
+ * its cost model finds to finish first -- with at most one chain per CU, the
+ * longest sequences cut at a common chunk M, their tails run (from a zero
+ * state and as the transition chain) by workgroups that take the CUs shorter
+ * chains free, then a seam pass (8 sequences of 2394-5348 tokens at 32
+ * v-heads: the 84-chunk chain becomes about 72 chunk periods).  `plan`
+ * receives GDN_PREFILL_PLAN_BYTES bytes (host memory, opaque, reusable for
+ * calls with the same cu_seqlens on the same device); *workspace_bytes (if
+ * not NULL) the device workspace gdn_prefill_plan_fwd needs (0: none).
+ * `cus` <= 0: the current device's CU count.  flags: GDN_NO_SEAMS plans no
+ * seams, GDN_PLAN_FUSED the fused kernel.  No reference counterpart.
+ */
+#define GDN_PREFILL_PLAN_BYTES 512
+int gdn_prefill_plan(const void* cu_seqlens_host, int cu_is_int32, int N, int T, int HQ, int HV,
+                     int cus, int flags, void* plan, size_t* workspace_bytes);
+
+/* Of a plan: the path (*slices: 4 / 8 split, 0 fused), the fused seams
+ * (*seams), their cut chunk (*split_chunk, 0 without seams) and the modelled
+ * fused finish in chunk periods (*periods, the seam pass excluded); any
+ * pointer may be NULL.  GDN_ERR_SHAPE if `plan` is not one. */
+int gdn_prefill_plan_info(const void* plan, int* slices, int* seams, int* split_chunk, int* periods);
+
+/*
+ * gdn_prefill_ex_fwd on the path and seams of `plan` (from gdn_prefill_plan
+ * with the same N, T, HQ, HV and the same cu_seqlens contents, else
+ * GDN_ERR_SHAPE or results that are not specified).  The workspace
+ * (device) holds the plan's workspace bytes: on the fused path the seam
+ * region (the seam plan, three fp32 [128][128] states per seam and v-head,
+ * the transition outputs of the tails), which nothing has to clear.  flags:
+ * GDN_QK_L2NORM, GDN_NO_SEAMS (the plan's fused seams are then not run).
+ */
+int gdn_prefill_plan_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const float* state, const float* A_log, const uint16_t* a,
+                         const float* dt_bias, const uint16_t* b, const void* cu_seqlens,
+                         int cu_is_int32, int N, int T, int HQ, int HV, float scale,
+                         uint16_t* out, float* final_state, const void* plan, void* workspace,
+                         size_t workspace_bytes, int flags, void* stream);
 
 /*
  * Workspace bytes of gdn_prefill_split_fwd: 14 080 bytes per (chunk, v-head)

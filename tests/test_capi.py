@@ -26,7 +26,8 @@ def test_header_declares_expected_entry_points():
         "gdn_prefill_split_workspace_bytes", "gdn_prefill_split_fwd", "gdn_prefill_auto_slices",
         "gdn_prefill_split_noalloc_max_bytes", "gdn_prefill_split_noalloc_fwd",
         "gdn_qkv_conv1d_fwd", "gdn_qkv_conv1d_update", "gdn_prefill_bwd_workspace_bytes",
-        "gdn_prefill_bwd", "gdn_gate_bwd", "gdn_prefill_choose_slices", "gdn_prefill_split_h_fwd"])
+        "gdn_prefill_bwd", "gdn_gate_bwd", "gdn_prefill_choose_slices", "gdn_prefill_split_h_fwd",
+        "gdn_prefill_plan", "gdn_prefill_plan_info", "gdn_prefill_plan_fwd"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -147,3 +148,93 @@ def test_choose_slices_edges():
     assert lib.gdn_prefill_choose_slices(cu.data_ptr(), 0, 0, 0, 0, 256) == -1
     # empty sequences only: no chunks; any answer is valid, none may fail
     assert _choose([0, 0, 0], 8) in (0, 4, 8)
+
+
+def _plan(lens, HQ, HV, cus=256, flags=0, dt=None):
+    """gdn_prefill_plan on these lengths: (rc, plan buffer, info dict)."""
+    import torch
+    capi = pkg_module("_capi")
+    lib = capi.lib()
+    cu = torch.tensor([0] + list(__import__("itertools").accumulate(lens)), dtype=dt or torch.int64)
+    buf = ctypes.create_string_buffer(capi.GDN_PREFILL_PLAN_BYTES)
+    ws = ctypes.c_size_t(0)
+    rc = lib.gdn_prefill_plan(cu.data_ptr(), int(cu.dtype == torch.int32), len(lens), int(cu[-1]),
+                              HQ, HV, cus, flags, buf, ctypes.byref(ws))
+    info = [ctypes.c_int(0) for _ in range(4)]
+    if rc == 0:
+        assert lib.gdn_prefill_plan_info(buf, *[ctypes.byref(i) for i in info]) == 0
+    keys = ("slices", "seams", "split_chunk", "periods")
+    return rc, buf, dict(zip(keys, (i.value for i in info)), workspace=ws.value)
+
+
+def test_plan_on_measured_batches():
+    """The host plan (path and fused seams) on the benchmark batches, 256 CUs.
+
+    Fused seams take only CUs idle at launch: 2 HV tail workgroups per seam
+    beside the chains.  The 16-sequence qk4/v8 batch (128 chains, chunk
+    counts up to 118): seven sequences cut at chunk 61, so the tails (from a
+    zero state and the transition chains) run on the 128 idle CUs, modelled
+    finish 61 chunk periods; measured on MI355X 251 us against the split
+    path's 279 us.  The 32k batch at qk16/v32 fills the GPU (256 chains): no
+    seams; tails there could only start where short chains end, and with
+    every CU busy the clock drops (measured: 330 us with seams against 285 us
+    serial).  The workspace is the seam region: 512 bytes of plan, three
+    64 KiB states per seam and v-head, the tails' OX rows."""
+    inp = pkg_module("inputs")
+    capi = pkg_module("_capi")
+    lens = inp.workload_lengths("prefill_varlen16_qk4_v8")
+    rc, _, p = _plan(lens, 4, 8)
+    assert rc == 0
+    assert (p["slices"], p["seams"], p["split_chunk"], p["periods"]) == (0, 7, 61, 61)
+    tails = sorted(lens, reverse=True)[:7]
+    ox_rows = sum(n - 64 * 61 for n in tails)
+    assert p["workspace"] == 512 + 7 * 8 * 3 * 65536 + ox_rows * 8 * 256
+    # int32 lengths plan the same
+    assert _plan(lens, 4, 8, dt=__import__("torch").int32)[2] == p
+    # no seams on request: the split path the lengths favour then (4 slices)
+    rc, _, p = _plan(lens, 4, 8, flags=capi.GDN_NO_SEAMS)
+    assert (p["slices"], p["seams"]) == (4, 0)
+    # the 32k batch: fused, no seams, the longest chain's 84 periods, no workspace
+    rc, _, p = _plan(inp.workload_lengths("prefill_varlen8_t32768_qk16_v32"), 16, 32)
+    assert (p["slices"], p["seams"], p["periods"], p["workspace"]) == (0, 0, 84, 0)
+    # one 4096-token sequence at qk4/v8: the split path (8 slices) and its workspace
+    rc, _, p = _plan([4096], 4, 8)
+    assert (p["slices"], p["seams"]) == (8, 0)
+    assert p["workspace"] == capi.lib().gdn_prefill_split_workspace_bytes(1, 4096, 4, 8)
+    # ... or, asked for the fused kernel, cut a little past half (the tail
+    # workgroups' start-up) on the idle CUs
+    rc, _, p = _plan([4096], 4, 8, flags=capi.GDN_PLAN_FUSED)
+    assert (p["slices"], p["seams"]) == (0, 1) and 32 < p["split_chunk"] < 40
+    # four equal chains per CU half: cutting two leaves two as long -- no seams
+    assert _plan([5348] * 4, 16, 32)[2]["seams"] == 0
+    # past one chain per CU, chains too short to cut, or no idle CU: no seams
+    assert _plan([100] * 64, 4, 8)[2]["seams"] == 0
+    assert _plan([300] * 20, 4, 8, flags=capi.GDN_PLAN_FUSED)[2]["seams"] == 0
+    assert _plan([4096] * 8, 16, 32)[2]["seams"] == 0
+
+
+def test_plan_argument_errors():
+    capi = pkg_module("_capi")
+    lib = capi.lib()
+    P = 0x1000  # never dereferenced: the checks fail first
+    buf = ctypes.create_string_buffer(capi.GDN_PREFILL_PLAN_BYTES)
+    assert lib.gdn_prefill_plan(None, 0, 1, 64, 4, 8, 256, 0, buf, None) == capi.GDN_ERR_NULL
+    rc, good, _ = _plan([700, 300], 4, 8)
+    assert rc == 0
+    cu = good  # any host memory: the shape checks fail first
+    assert lib.gdn_prefill_plan(cu, 0, 1, 64, 4, 6, 256, 0, buf, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_plan(cu, 0, 1, 64, 4, 8, 256, 8, buf, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_plan_info(None, None, None, None, None) == capi.GDN_ERR_NULL
+    assert lib.gdn_prefill_plan_info(ctypes.create_string_buffer(512), None, None, None, None) == capi.GDN_ERR_SHAPE
+    # plan_fwd: a missing plan, a plan of other sizes, unknown flags, a missing seam workspace
+    args = [P] * 9 + [0, 2, 1000, 4, 8, 1.0, P, P]
+    assert lib.gdn_prefill_plan_fwd(*args, None, None, 0, 0, None) == capi.GDN_ERR_NULL
+    args_t = [P] * 9 + [0, 2, 999, 4, 8, 1.0, P, P]
+    assert lib.gdn_prefill_plan_fwd(*args_t, good, None, 0, 0, None) == capi.GDN_ERR_SHAPE
+    args_h = [P] * 9 + [0, 2, 1000, 4, 16, 1.0, P, P]
+    assert lib.gdn_prefill_plan_fwd(*args_h, good, None, 0, 0, None) == capi.GDN_ERR_SHAPE
+    assert lib.gdn_prefill_plan_fwd(*args, good, None, 0, 8, None) == capi.GDN_ERR_SHAPE
+    rc, fused, p = _plan([700, 300], 4, 8, flags=capi.GDN_PLAN_FUSED)
+    assert rc == 0 and p["seams"] >= 1 and p["workspace"] > 0
+    assert lib.gdn_prefill_plan_fwd(*args, fused, None, 0, 0, None) == capi.GDN_ERR_WORKSPACE
+    assert lib.gdn_prefill_plan_fwd(*args, fused, P, p["workspace"] - 1, 0, None) == capi.GDN_ERR_WORKSPACE

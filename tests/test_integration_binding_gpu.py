@@ -58,7 +58,7 @@ def test_binding_prefill(device, lens, path):
     inp = pkg_module("inputs")
     x = inp.prefill_inputs(lens, seed=602, with_state=True)
     g = _to(x, device)
-    assert ns["prefill_slices"](x["cu_seqlens"], sum(lens), 8) == path
+    assert ns["prefill_plan"](x["cu_seqlens"], sum(lens), 4, 8)[2] == path
     qk = torch.cat([g["q"], g["k"]], dim=-1)                              # [T, 4, 256]
     q = qk[..., :128]
     assert not q.is_contiguous()
@@ -73,8 +73,9 @@ def test_binding_prefill(device, lens, path):
 
 def test_binding_prefill_four_equal_sequences_fused(device):
     """Four 5 348-token sequences at qk16/v32 (128 chains): the lengths choose
-    the fused kernel, and the binding's results equal the package's fused
-    path bit for bit."""
+    the fused kernel, without seams (cutting two of four equal chains leaves
+    two as long), and the binding's results equal the package's automatic
+    path bit for bit and the fp64 oracle within the prefill bars."""
     ns = _binding()
     pre = pkg_module("prefill")
     inp = pkg_module("inputs")
@@ -82,12 +83,41 @@ def test_binding_prefill_four_equal_sequences_fused(device):
     print("binding prefill 4 x 5348 qk16/v32", flush=True)
     x = inp.prefill_inputs(lens, 16, 32, seed=603, with_state=True)
     g = _to(x, device)
-    assert ns["prefill_slices"](x["cu_seqlens"], sum(lens), 32) == 0
+    _, ws, slices, seams = ns["prefill_plan"](x["cu_seqlens"], sum(lens), 16, 32)
+    assert (slices, seams, ws) == (0, 0, 0)
     names = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
     o, s = ns["prefill_run"](*[g[n] for n in names], None)
-    of, sf = pre.gdn_prefill(*[g[n] for n in names], None, path="fused")
+    of, sf = pre.gdn_prefill(*[g[n] for n in names], None)
     torch.cuda.synchronize()
     assert torch.equal(o, of) and torch.equal(s, sf)
+    o_ref, s_ref = O.prefill_chunked(*[x[n] for n in names], x["scale"])
+    torch.testing.assert_close(o.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    assert float((s.cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
+
+
+def test_binding_prefill_fused_with_seams(device):
+    """The 16-sequence qk4/v8 batch (128 chains, lengths 244-7 532, int32
+    cu_seqlens): the plan runs the fused kernel with seams on the 128 idle
+    CUs; the binding equals the package's automatic path bit for bit and
+    the fp64 oracle within the prefill bars."""
+    ns = _binding()
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    lens = inp.workload_lengths("prefill_varlen16_qk4_v8")
+    print("binding prefill varlen16 qk4/v8", flush=True)
+    x = inp.prefill_inputs(lens, 4, 8, seed=604, with_state=True, cu_dtype=torch.int32)
+    g = _to(x, device)
+    _, ws, slices, seams = ns["prefill_plan"](x["cu_seqlens"], sum(lens), 4, 8)
+    assert slices == 0 and seams > 0 and ws > 0
+    names = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+    o, s = ns["prefill_run"](*[g[n] for n in names], None)
+    of, sf = pre.gdn_prefill(*[g[n] for n in names], None)
+    torch.cuda.synchronize()
+    assert torch.equal(o, of) and torch.equal(s, sf)
+    x64 = dict(x, cu_seqlens=x["cu_seqlens"].long())
+    o_ref, s_ref = O.prefill_chunked(*[x64[n] for n in names], x["scale"])
+    torch.testing.assert_close(o.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    assert float((s.cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
 
 
 def test_binding_prefill_rejects_like_the_reference(device):

@@ -20,6 +20,8 @@ GDN_ERR_SHAPE = -1002
 GDN_ERR_WORKSPACE = -1003
 GDN_QK_L2NORM = 1
 GDN_NO_SEAMS = 2
+GDN_PLAN_FUSED = 4
+GDN_PREFILL_PLAN_BYTES = 512
 GDN_ACT_NONE = 0
 GDN_ACT_SILU = 1
 
@@ -49,6 +51,11 @@ SIGNATURES = {
                                            _F, _P, _P, _I, _I, _P]),
     "gdn_prefill_chunk_count": (ctypes.c_longlong, [_P, _I, _I, _I]),
     "gdn_prefill_choose_slices": (_I, [_P, _I, _I, _I, _I, _I]),
+    "gdn_prefill_plan": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, ctypes.POINTER(_S)]),
+    "gdn_prefill_plan_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
+                                   ctypes.POINTER(_I)]),
+    "gdn_prefill_plan_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
+                                  _P, _P, _P, _P, _S, _I, _P]),
     "gdn_qkv_conv1d_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _I, _I,
                                 _I, _P]),
     "gdn_qkv_conv1d_update": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _I,

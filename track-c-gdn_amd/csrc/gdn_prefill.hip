@@ -41,6 +41,7 @@
 #include "../../include/gdn_hip.h"
 
 #include <algorithm>
+#include <cstring>
 #include <functional>
 #include <queue>
 #include <vector>
@@ -103,6 +104,28 @@ constexpr int kTiles = kRowsPerWave / 16;        // 16-row column tiles per chai
 // (with t % 16 two rows share each pair).
 __device__ __forceinline__ int vsw(int t) { return ((t & 7) << 1) | ((t >> 3) & 1); }
 
+// The seams of a fused launch (time splits of the longest chains, run on the
+// CUs that shorter chains leave idle; the algebra is stated in
+// gdn_prefill_common.h), planned on the host from the sequence lengths and
+// passed by value.  Seam j cuts sequence seq[j] (of host bounds bos[j],
+// len[j]) at chunk sp[j]: its G v-heads' head chains run in the chains' grid
+// and stop at the cut; its tail chains (zero state, then transition) run in
+// extra workgroups from base_ids on.  OX rows of seam j start at ox_row[j].
+struct FusedSeams {
+  int count;                // 0 .. kMaxSeams
+  int base_ids;             // workgroup ids of the chains' grid
+  int seq[kMaxSeams];
+  int sp[kMaxSeams];
+  int bos[kMaxSeams];
+  int len[kMaxSeams];
+  int ox_row[kMaxSeams];
+  char* region;             // seam region of count slots
+};
+
+// One zero V row: the transition chains copy it in place of their V rows
+// (row offsets dropped), so their copies and waits are the chain's own.
+__device__ __align__(256) uint16_t g_zero_v_row[D];
+
 template <typename CuT, bool kL2, bool kH>
 __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -111,7 +134,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV,
     float scale, uint16_t* __restrict__ out, float* __restrict__ ht,
-    uint16_t* __restrict__ hout, int h_chunks) {
+    uint16_t* __restrict__ hout, int h_chunks, const FusedSeams seams) {
   __shared__ Smem sm;
   __shared__ SmemRaw raw;
   __shared__ __align__(16) uint16_t rawV[C * D];     // V chunk (bf16, swizzled), DMA target
@@ -126,14 +149,49 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   // dispatcher places on the same XCD (ids go round-robin over the 8 XCDs),
   // so the second read of a K/Q row can hit that XCD's L2.  Unit u = (n, hq)
   // and member m map to id 8 (G (u / 8) + m) + u % 8; ids past the last unit
-  // exit at once.
+  // exit at once.  Seams: the ids from seams.base_ids on take seam units
+  // (seam j, hq) the same way, 2 G members each (G zero-state tails, then G
+  // transition chains); the dispatcher starts them, seam by seam, as CUs free.
+  // role 0: a whole chain; 1: a seam's head; 2: its zero-state tail; 3: its
+  // transition chain.
   const int heads_per_qk = HV / HQ;
-  const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
-  const int unit = 8 * (id_row / heads_per_qk) + xcd;
-  if (unit >= N * HQ) return;
-  const int n = unit / HQ;
-  const int hq = unit - n * HQ;
-  const int hv = hq * heads_per_qk + (id_row - (id_row / heads_per_qk) * heads_per_qk);
+  int n, hq, hv, role = 0, sj = 0;
+  if (seams.count == 0 || int(blockIdx.x) < seams.base_ids) {
+    const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
+    const int unit = 8 * (id_row / heads_per_qk) + xcd;
+    if (unit >= N * HQ) return;
+    n = unit / HQ;
+    hq = unit - n * HQ;
+    hv = hq * heads_per_qk + (id_row - (id_row / heads_per_qk) * heads_per_qk);
+#pragma unroll
+    for (int j = 0; j < kMaxSeams; ++j)
+      if (j < seams.count && seams.seq[j] == n) {
+        role = 1;
+        sj = j;
+      }
+  } else {
+    const int e = int(blockIdx.x) - seams.base_ids;
+    const int xcd = e & 7, id_row = e >> 3;
+    const int su = 8 * (id_row / (2 * heads_per_qk)) + xcd;
+    if (su >= seams.count * HQ) return;
+    const int w = id_row - (id_row / (2 * heads_per_qk)) * (2 * heads_per_qk);
+    sj = su / HQ;
+    hq = su - sj * HQ;
+    role = 2 + w / heads_per_qk;
+    hv = hq * heads_per_qk + w % heads_per_qk;
+    n = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxSeams; ++j)
+      if (j == sj) n = seams.seq[j];
+  }
+  int sp_j = 0, ox_row_j = 0, tail_j = 0;   // this seam's cut, first OX row, tail tokens
+#pragma unroll
+  for (int j = 0; j < kMaxSeams; ++j)
+    if (role != 0 && j == sj) {
+      sp_j = seams.sp[j];
+      ox_row_j = seams.ox_row[j];
+      tail_j = seams.len[j] - C * seams.sp[j];
+    }
   int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: keep it scalar
   int lane = tid & 63;
@@ -150,6 +208,31 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 
   int bos, len;
   seq_bounds(cu_seqlens, n, T, bos, len);
+  // A seam's head and tails run as sequences of their own: chunks [0, sp) and
+  // [sp, ...), the tails' tokens clamped to the plan's (so a transition
+  // chain's OX rows stay inside the region).
+  if (role == 1) {
+    len = min(len, C * sp_j);
+  } else if (role >= 2) {
+    const int cut = min(len, C * sp_j);
+    bos += cut;
+    len = max(0, min(len - cut, tail_j));
+  }
+  if (blockIdx.x == 0 && tid == 0) {
+    // the plan of the seam pass
+    int* plan = reinterpret_cast<int*>(seams.region);
+#pragma unroll
+    for (int j = 0; j < kMaxSeams; ++j)
+      if (j < seams.count) {
+        int* e = plan + kSeamPlanStride * j;
+        e[SP_SEQ] = seams.seq[j];
+        e[SP_BOS] = seams.bos[j];
+        e[SP_LEN] = seams.len[j];
+        e[SP_SPLIT] = seams.sp[j];
+        e[SP_CHUNKS] = (seams.len[j] + C - 1) / C;
+        e[SP_OX_ROW] = seams.ox_row[j];
+      }
+  }
   // gate inputs of this head (uniform)
   const float a_log_exp = expf(A_log[hv]);
   const float dtb = dt_bias[hv];
@@ -198,7 +281,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   for (int j = 0; j < kMaxGroups; ++j) {
     const int row = group_row0(j) + (lane >> 4);
     dma_qk[j] = uint32_t(row) * uint32_t(qk_stride * 2) + uint32_t((lane & 15) ^ (row & 15)) * 16u;
-    dma_v[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane & 15) ^ vsw(row)) * 16u;
+    dma_v[j] = (role == 3 ? 0u : uint32_t(row) * uint32_t(v_stride * 2)) + uint32_t((lane & 15) ^ vsw(row)) * 16u;
   }
   auto copy_rows = [&](const uint16_t* src, size_t stride, size_t col0, const uint32_t* offs, int ch,
                        uint16_t* dst, bool is_v) {
@@ -224,7 +307,11 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   auto copy_k = [&](int ch) { copy_rows(k, qk_stride, size_t(hq) * D, dma_qk, ch, raw.k[ch & 1], false); };
   auto copy_q = [&](int ch) { copy_rows(q, qk_stride, size_t(hq) * D, dma_qk, ch, raw.q[ch & 1], false); };
   auto copy_kq = [&](int ch) { copy_k(ch); copy_q(ch); };
-  auto copy_v = [&](int ch) { copy_rows(v, v_stride, size_t(hv) * D, dma_v, ch, rawV, true); };
+  // the transition chain copies the zero row for every V row
+  const uint16_t* v_src = role == 3 ? g_zero_v_row : v;
+  const size_t v_src_stride = role == 3 ? 0 : v_stride;
+  const size_t v_src_col = role == 3 ? 0 : size_t(hv) * D;
+  auto copy_v = [&](int ch) { copy_rows(v_src, v_src_stride, v_src_col, dma_v, ch, rawV, true); };
   // L2-norm factors of the 4 n_groups rows this wave copied into buf, from the
   // diagonal of their Gram matrix: two 16-row tiles, each one bf16 MFMA chain
   // with the same registers as both operands (squares exact, fp32 sums).  Tile
@@ -516,6 +603,13 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
   };
   if (is_chain) {
     // ================= chain waves
+    // output rows: out[bos + t], or a transition chain's OX rows
+    uint16_t* out_rows = out;
+    int out_row0 = bos;
+    if (role == 3) {
+      out_rows = reinterpret_cast<uint16_t*>(seams.region + seam_ox_offset(seams.count, HV));
+      out_row0 = ox_row_j;
+    }
     // Column tile u (0, 1) of this wave holds state rows v = v0 + 16 u + c.
     // initial state: Sacc[u][kb][i] = S[v0 + 16 u + c][16 kb + 4 g + i]
     f32x4 Sacc[kTiles][8];
@@ -523,7 +617,15 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
     for (int u = 0; u < kTiles; ++u)
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb) Sacc[u][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (h0 != nullptr) {
+    if (role == 3) {              // the transition chain starts from the identity
+#pragma unroll
+      for (int u = 0; u < kTiles; ++u)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Sacc[u][kb][i] = (vrow + 16 * u == 16 * kb + 4 * g + i) ? 1.f : 0.f;
+    }
+    if (h0 != nullptr && role < 2) {
       const float* src = h0 + (size_t(n) * HV + hv) * size_t(D) * D + size_t(vrow) * D;
 #pragma unroll
       for (int u = 0; u < kTiles; ++u)
@@ -851,7 +953,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
           // 256-byte rows.
           constexpr int kOutRows = C / kChainWaves;
           const size_t row_bytes = v_stride * sizeof(uint16_t);
-          char* obase = reinterpret_cast<char*>(out + size_t(bos + ch * C) * v_stride + size_t(hv) * D);
+          char* obase = reinterpret_cast<char*>(out_rows + size_t(out_row0 + ch * C) * v_stride + size_t(hv) * D);
 #pragma unroll
           for (int q4 = 0; q4 < kOutRows / 4; ++q4) {
             const int row = kOutRows * (v0 / kRowsPerWave) + 4 * q4 + (lane >> 4);
@@ -899,12 +1001,25 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       }
     }
     asm volatile("" : "+v"(g), "+v"(c));
-    float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D + size_t(v0 + c) * D;
+    if (role == 3) {
+      // X stored transposed: X^T[k][v] = Sacc[u][kb][i] at k = 16 kb + 4 g + i, v = vrow + 16 u
+      float* dst = reinterpret_cast<float*>(seams.region + seam_state_offset(HV, sj, hv, 2));
 #pragma unroll
-    for (int u = 0; u < kTiles; ++u)
+      for (int u = 0; u < kTiles; ++u)
 #pragma unroll
-      for (int kb = 0; kb < 8; ++kb)
-        *reinterpret_cast<f32x4*>(dst + size_t(16 * u) * D + 16 * kb + 4 * g) = Sacc[u][kb];
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[size_t(16 * kb + 4 * g + i) * D + vrow + 16 * u] = Sacc[u][kb][i];
+    } else {
+      float* dst = (role == 0 ? ht + (size_t(n) * HV + hv) * size_t(D) * D
+                              : reinterpret_cast<float*>(seams.region + seam_state_offset(HV, sj, hv, role - 1))) +
+                   size_t(v0 + c) * D;
+#pragma unroll
+      for (int u = 0; u < kTiles; ++u)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+          *reinterpret_cast<f32x4*>(dst + size_t(16 * u) * D + 16 * kb + 4 * g) = Sacc[u][kb];
+    }
   } else {
     // ================= preparation waves
     // The preparation waves run single-wave dependency chains (Tm inverse and
@@ -1017,48 +1132,59 @@ int check_prefill_args(const void* q, const void* k, const void* v, const void* 
 }
 
 
+// The chain kernel over the chains' grid, plus the seams' workgroups and the
+// seam pass when `seams` holds any (never with h).
 template <bool kL2, bool kH>
 int launch_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                    const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
                    const void* cu_seqlens, int cu_is_int32, int N, int T, int HQ, int HV,
                    float scale, uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
-                   hipStream_t st) {
+                   FusedSeams seams, int seam_ox_rows, int seam_max_tail, hipStream_t st) {
   const unsigned units = unsigned(N) * unsigned(HQ);
-  const dim3 grid{8u * unsigned(HV / HQ) * ((units + 7u) / 8u), 1u, 1u};
+  const unsigned G = unsigned(HV / HQ);
+  const unsigned base = 8u * G * ((units + 7u) / 8u);
+  if (kH) seams.count = 0;
+  seams.base_ids = int(base);
+  const unsigned seam_units = unsigned(seams.count) * unsigned(HQ);
+  const unsigned extra = seams.count > 0 ? 8u * 2u * G * ((seam_units + 7u) / 8u) : 0u;
+  const dim3 grid{base + extra, 1u, 1u};
   const dim3 block(kThreads);
   if (cu_is_int32) {
     hipLaunchKernelGGL((gdn_prefill_chain_kernel<int32_t, kL2, kH>), grid, block, 0, st, q, k, v,
                        state, A_log, a, dt_bias, b, static_cast<const int32_t*>(cu_seqlens), N, T,
-                       HQ, HV, scale, out, final_state, h, h_chunks);
+                       HQ, HV, scale, out, final_state, h, h_chunks, seams);
   } else {
     hipLaunchKernelGGL((gdn_prefill_chain_kernel<int64_t, kL2, kH>), grid, block, 0, st, q, k, v,
                        state, A_log, a, dt_bias, b, static_cast<const int64_t*>(cu_seqlens), N, T,
-                       HQ, HV, scale, out, final_state, h, h_chunks);
+                       HQ, HV, scale, out, final_state, h, h_chunks, seams);
   }
   const hipError_t err = hipGetLastError();
-  return err == hipSuccess ? GDN_OK : -int(err);
+  if (err != hipSuccess) return -int(err);
+  return gdn::prefill_seam_pass(seams.region, HV, seams.count, seam_ox_rows, seams.count, seam_max_tail,
+                                out, final_state, st);
 }
 
 int prefill_dispatch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                      const float* A_log, const uint16_t* a, const float* dt_bias, const uint16_t* b,
                      const void* cu_seqlens, int cu_is_int32, int N, int T, int HQ, int HV,
                      float scale, uint16_t* out, float* final_state, uint16_t* h, int h_chunks,
-                     int flags, hipStream_t st) {
+                     int flags, hipStream_t st, const FusedSeams& seams = FusedSeams{},
+                     int seam_ox_rows = 0, int seam_max_tail = 0) {
   const bool l2 = (flags & GDN_QK_L2NORM) != 0;
   if (h != nullptr) {
     return l2 ? launch_prefill<true, true>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                                            cu_is_int32, N, T, HQ, HV, scale, out, final_state, h,
-                                           h_chunks, st)
+                                           h_chunks, FusedSeams{}, 0, 0, st)
               : launch_prefill<false, true>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                                             cu_is_int32, N, T, HQ, HV, scale, out, final_state, h,
-                                            h_chunks, st);
+                                            h_chunks, FusedSeams{}, 0, 0, st);
   }
   return l2 ? launch_prefill<true, false>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                                           cu_is_int32, N, T, HQ, HV, scale, out, final_state,
-                                          nullptr, 0, st)
+                                          nullptr, 0, seams, seam_ox_rows, seam_max_tail, st)
             : launch_prefill<false, false>(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                                            cu_is_int32, N, T, HQ, HV, scale, out, final_state,
-                                           nullptr, 0, st);
+                                           nullptr, 0, seams, seam_ox_rows, seam_max_tail, st);
 }
 
 }  // namespace
@@ -1156,6 +1282,7 @@ constexpr double kSlice8ChunkCycles = 2550.0;
 constexpr double kSlice4ChunkCycles = 3600.0;
 constexpr double kPrepUnitCycles256 = 25.0 * 256.0;
 constexpr double kStartupCycles = 24000.0;
+constexpr int kFusedSeamMinChunks = 8;    // shortest chain a fused seam cuts
 
 // Finish time of workgroups that each hold one CU for `chunks * period`
 // cycles, started in the given order as CUs free up, `per_seq` workgroups
@@ -1174,12 +1301,87 @@ double makespan(const std::vector<int>& chunks, int per_seq, double period, int 
   return end;
 }
 
-}  // namespace
+// The fused launch's seams for these lengths.  Seams take only the CUs idle
+// at launch (chains < CUs): each seam's 2 HV tail workgroups start at once,
+// beside the chains.  Cutting the k longest sequences (L: chunk counts,
+// longest first) at chunk M, the launch ends at
+//   max(M, L[k], L[0] - M + kSeamWgStartupPeriods)
+// chunk periods (a workgroup's start-up, about 12 us, counts for the tails
+// that start late in the serial case it replaces too little to matter), and
+// the seam pass costs kSeamPassFixedCycles plus kSeamPassTokenCycles per
+// (tail token, v-head) (OX rows written and read, the outputs read and
+// written again).  The plan takes the k and M of the earliest modelled end,
+// none when that is not earlier than the longest chain's.  `periods` is the
+// modelled finish in chunk periods, the seam pass excluded.
+constexpr double kSeamWgStartupPeriods = 3.5;
+constexpr double kSeamPassFixedCycles = 12000.0;
+constexpr double kSeamPassTokenCycles = 0.9;
 
-extern "C" int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int N, int T,
-                                         int HV, int cus) {
-  if (!cu_seqlens_host || N < 0 || T < 0 || HV <= 0) return -1;
-  if (cus <= 0) cus = gdn::device_cus();
+struct FusedPlan {
+  int count = 0;
+  int seq[kMaxSeams] = {}, sp[kMaxSeams] = {}, bos[kMaxSeams] = {}, len[kMaxSeams] = {};
+  int ox_row[kMaxSeams] = {};
+  int ox_rows = 0, max_tail = 0, periods = 0;
+};
+
+template <typename CuT>
+FusedPlan plan_fused_seams(const CuT* cu, int N, int T, int HV, int cus, bool allow) {
+  FusedPlan p;
+  std::vector<int> order(N), L(N), lens(N);
+  for (int m = 0; m < N; ++m) {
+    int bm, lm;
+    seq_bounds(cu, m, T, bm, lm);
+    lens[m] = lm;
+    L[m] = (lm + C - 1) / C;
+    order[m] = m;
+  }
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return L[x] > L[y]; });
+  p.periods = N > 0 ? L[order[0]] : 0;
+  const long long chains = (long long)N * HV;
+  if (!allow || N == 0 || cus <= 0 || chains >= cus) return p;
+  const int room = int(std::min<long long>({(cus - chains) / (2LL * HV), (long long)N, (long long)kMaxSeams}));
+  const int L0 = L[order[0]];
+  double best = double(L0) * kFusedChunkCycles;
+  int best_k = 0, best_M = 0, best_end = L0;
+  for (int k = 1; k <= room; ++k) {
+    const int Lk = k < N ? L[order[k]] : 0;
+    if (L[order[k - 1]] < kFusedSeamMinChunks) break;
+    for (int M = std::max(1, Lk); M < L[order[k - 1]]; ++M) {
+      long long tail_tokens = 0;
+      for (int j = 0; j < k; ++j) tail_tokens += lens[order[j]] - (long long)C * M;
+      const double end = std::max<double>({double(M), double(Lk), L0 - M + kSeamWgStartupPeriods});
+      const double cost = end * kFusedChunkCycles + kSeamPassFixedCycles +
+                          kSeamPassTokenCycles * double(tail_tokens) * HV;
+      if (cost < best) {
+        best = cost;
+        best_k = k;
+        best_M = M;
+        best_end = int(std::ceil(end));
+      }
+    }
+  }
+  if (best_k == 0) return p;
+  p.count = best_k;
+  p.periods = best_end;
+  for (int j = 0; j < best_k; ++j) {
+    const int n = order[j];
+    int bm, lm;
+    seq_bounds(cu, n, T, bm, lm);
+    p.seq[j] = n;
+    p.sp[j] = best_M;
+    p.bos[j] = bm;
+    p.len[j] = lm;
+    p.ox_row[j] = p.ox_rows;
+    p.ox_rows += lm - C * best_M;
+    p.max_tail = std::max(p.max_tail, L[n] - best_M);
+  }
+  return p;
+}
+
+// Slices of the split path (4 / 8) or 0 for the fused kernel, from the modelled
+// times of the three for these lengths; the fused kernel's with the seams of fp.
+template <typename CuT>
+int choose_path(const CuT* cu, int N, int T, int HV, int cus, const FusedPlan& fp) {
   const long long chains = (long long)N * HV;
   // Past one chain per CU the fused kernel fills the GPU and the split path
   // would need 4 or 8 times as many workgroups.
@@ -1188,14 +1390,15 @@ extern "C" int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_
   double units = 0.0;
   for (int m = 0; m < N; ++m) {
     int bm, lm;
-    if (cu_is_int32) seq_bounds(static_cast<const int32_t*>(cu_seqlens_host), m, T, bm, lm);
-    else seq_bounds(static_cast<const int64_t*>(cu_seqlens_host), m, T, bm, lm);
+    seq_bounds(cu, m, T, bm, lm);
     chunks[m] = (lm + C - 1) / C;
     units += double(chunks[m]) * HV;
   }
   // one fused workgroup per chain, all resident at once (chains <= CUs)
-  const double fused = kStartupCycles + *std::max_element(chunks.begin(), chunks.end()) *
-                                            kFusedChunkCycles;
+  long long tail_tokens = 0;
+  for (int j = 0; j < fp.count; ++j) tail_tokens += fp.len[j] - (long long)C * fp.sp[j];
+  const double fused = kStartupCycles + fp.periods * kFusedChunkCycles +
+                       (fp.count ? kSeamPassFixedCycles + kSeamPassTokenCycles * double(tail_tokens) * HV : 0.0);
   // the slice launch takes the sequences longest first
   std::sort(chunks.begin(), chunks.end(), std::greater<int>());
   const double prep = std::max(kStartupCycles, units * kPrepUnitCycles256 / cus);
@@ -1204,6 +1407,131 @@ extern "C" int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_
   if (split8 <= split4 && split8 < fused) return 8;
   if (split4 < fused) return 4;
   return 0;
+}
+
+// The plan behind gdn_prefill_plan / gdn_prefill_plan_fwd (host memory, opaque
+// to callers).
+constexpr uint32_t kPlanMagic = 0x50444e47u;   // "GNDP", layout 1
+struct PrefillPlan {
+  uint32_t magic;
+  int N, T, HQ, HV;
+  int slices;                 // 4 / 8: the split path; 0: the fused kernel
+  FusedPlan fused;            // the fused kernel's seams
+  unsigned long long workspace_bytes;
+};
+static_assert(sizeof(PrefillPlan) <= GDN_PREFILL_PLAN_BYTES, "plan size");
+
+template <typename CuT>
+void make_plan(const CuT* cu, int N, int T, int HQ, int HV, int cus, bool seams, bool fused_only,
+               PrefillPlan& p) {
+  p = PrefillPlan{};
+  p.magic = kPlanMagic;
+  p.N = N;
+  p.T = T;
+  p.HQ = HQ;
+  p.HV = HV;
+  p.fused = plan_fused_seams(cu, N, T, HV, cus, seams && T > 0);
+  p.slices = T > 0 && !fused_only ? choose_path(cu, N, T, HV, cus, p.fused) : 0;
+  if (p.slices) {
+    p.fused = FusedPlan{};
+    p.workspace_bytes = gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
+  } else {
+    p.workspace_bytes = p.fused.count ? seam_region_bytes(p.fused.count, HV, p.fused.ox_rows) : 0;
+  }
+}
+
+}  // namespace
+
+extern "C" int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int N, int T,
+                                         int HV, int cus) {
+  if (!cu_seqlens_host || N < 0 || T < 0 || HV <= 0) return -1;
+  if (cus <= 0) cus = gdn::device_cus();
+  if (N == 0 || cus <= 0 || (long long)N * HV > cus) return 0;
+  // the fused kernel as gdn_prefill_ex_fwd runs it without a workspace: no seams
+  if (cu_is_int32) {
+    const auto* cu = static_cast<const int32_t*>(cu_seqlens_host);
+    return choose_path(cu, N, T, HV, cus, plan_fused_seams(cu, N, T, HV, cus, false));
+  }
+  const auto* cu = static_cast<const int64_t*>(cu_seqlens_host);
+  return choose_path(cu, N, T, HV, cus, plan_fused_seams(cu, N, T, HV, cus, false));
+}
+
+extern "C" int gdn_prefill_plan(const void* cu_seqlens_host, int cu_is_int32, int N, int T, int HQ,
+                                int HV, int cus, int flags, void* plan, size_t* workspace_bytes) {
+  if (!cu_seqlens_host || !plan) return GDN_ERR_NULL;
+  if (N < 0 || T < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0 || (flags & ~(GDN_FLAGS_ALL | GDN_PLAN_FUSED)))
+    return GDN_ERR_SHAPE;
+  if (cus <= 0) cus = gdn::device_cus();
+  PrefillPlan p;
+  const bool seams = (flags & GDN_NO_SEAMS) == 0, fused = (flags & GDN_PLAN_FUSED) != 0;
+  if (cu_is_int32) make_plan(static_cast<const int32_t*>(cu_seqlens_host), N, T, HQ, HV, cus, seams, fused, p);
+  else make_plan(static_cast<const int64_t*>(cu_seqlens_host), N, T, HQ, HV, cus, seams, fused, p);
+  std::memcpy(plan, &p, sizeof(p));
+  if (workspace_bytes) *workspace_bytes = size_t(p.workspace_bytes);
+  return GDN_OK;
+}
+
+extern "C" int gdn_prefill_plan_info(const void* plan, int* slices, int* seams, int* split_chunk,
+                                     int* periods) {
+  if (!plan) return GDN_ERR_NULL;
+  PrefillPlan p;
+  std::memcpy(&p, plan, sizeof(p));
+  if (p.magic != kPlanMagic) return GDN_ERR_SHAPE;
+  if (slices) *slices = p.slices;
+  if (seams) *seams = p.fused.count;
+  if (split_chunk) *split_chunk = p.fused.count ? p.fused.sp[0] : 0;
+  if (periods) *periods = p.fused.periods;
+  return GDN_OK;
+}
+
+extern "C" int gdn_prefill_plan_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    const float* state, const float* A_log, const uint16_t* a,
+                                    const float* dt_bias, const uint16_t* b, const void* cu_seqlens,
+                                    int cu_is_int32, int N, int T, int HQ, int HV, float scale,
+                                    uint16_t* out, float* final_state, const void* plan,
+                                    void* workspace, size_t workspace_bytes, int flags, void* stream) {
+  const int rc = check_prefill_args(q, k, v, A_log, a, dt_bias, b, cu_seqlens, out, final_state,
+                                    N, T, HQ, HV);
+  if (rc != GDN_OK) return rc;
+  if (!plan) return GDN_ERR_NULL;
+  if (flags & ~GDN_FLAGS_ALL) return GDN_ERR_SHAPE;
+  PrefillPlan p;
+  std::memcpy(&p, plan, sizeof(p));
+  if (p.magic != kPlanMagic || p.N != N || p.T != T || p.HQ != HQ || p.HV != HV) return GDN_ERR_SHAPE;
+  if (p.fused.count < 0 || p.fused.count > kMaxSeams || (p.slices && !gdn::prefill_split_slices_valid(p.slices)))
+    return GDN_ERR_SHAPE;
+  if (N == 0) return GDN_OK;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p.slices) {
+    const size_t need = gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return GDN_ERR_WORKSPACE;
+    return gdn::prefill_split_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N,
+                                     T, HQ, HV, scale, out, final_state, p.slices, workspace, flags, st);
+  }
+  FusedSeams seams{};
+  if (p.fused.count > 0 && !(flags & GDN_NO_SEAMS)) {
+    const size_t need = seam_region_bytes(p.fused.count, HV, p.fused.ox_rows);
+    if (workspace == nullptr || workspace_bytes < need) return GDN_ERR_WORKSPACE;
+    // a plan made for other lengths could place tails past T
+    for (int j = 0; j < p.fused.count; ++j) {
+      const FusedPlan& f = p.fused;
+      if (f.seq[j] < 0 || f.seq[j] >= N || f.bos[j] < 0 || f.len[j] < 0 || (long long)f.bos[j] + f.len[j] > T ||
+          f.sp[j] < 1 || C * (long long)f.sp[j] >= f.len[j])
+        return GDN_ERR_SHAPE;
+    }
+    seams.count = p.fused.count;
+    for (int j = 0; j < seams.count; ++j) {
+      seams.seq[j] = p.fused.seq[j];
+      seams.sp[j] = p.fused.sp[j];
+      seams.bos[j] = p.fused.bos[j];
+      seams.len[j] = p.fused.len[j];
+      seams.ox_row[j] = p.fused.ox_row[j];
+    }
+    seams.region = static_cast<char*>(workspace);
+  }
+  return prefill_dispatch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_is_int32, N, T, HQ, HV,
+                          scale, out, final_state, nullptr, 0, flags, st, seams, p.fused.ox_rows,
+                          p.fused.max_tail);
 }
 
 extern "C" long long gdn_prefill_chunk_count(const void* cu_seqlens_host, int cu_is_int32, int N,

@@ -213,6 +213,39 @@ __host__ __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T,
   len = int(e0 - b0);
 }
 
+// ---------------------------------------------------------------------------
+// Seams: time splits of long chains, on either prefill path.  Sequence n of
+// Lc chunks cut at chunk sp runs its head [0, sp) from the initial state and,
+// at the same time, its tail [sp, Lc) twice: from a zero state (outputs O0,
+// final state S0) and as the transition chain (v = 0, initial state the
+// identity; its state X is the product of the tail's per-chunk transitions,
+// its outputs OX the outputs' part linear in the state entering the tail).
+// With S_sp the head's final state the tail outputs are O0 + OX S_sp^T and
+// the final state S_sp X + S0, which the seam pass forms.
+//
+// A seam region of the workspace holds the plan (kSeamPlanStride ints per
+// seam slot, fields SeamPlanField, sequence -1 in unused slots), then per
+// slot and v-head three fp32 [128][128] states (the head's final state, the
+// tail's zero-state final state, X stored transposed), then the OX rows of
+// the seams' tail tokens, bf16 [ox_rows][HV][128], seam j from row
+// SP_OX_ROW on.
+constexpr int kMaxSeams = 8;
+constexpr int kSeamPlanStride = 8;
+enum SeamPlanField { SP_SEQ, SP_BOS, SP_LEN, SP_SPLIT, SP_CHUNKS, SP_OX_ROW };
+constexpr size_t kSeamPlanBytes = 512;
+static_assert(size_t(kSeamPlanStride) * kMaxSeams * sizeof(int) <= kSeamPlanBytes, "seam plan");
+constexpr size_t kSeamStateBytes = size_t(D) * D * 4;
+// kind: 0 the head's final state, 1 the tail's zero-state final state, 2 X^T
+__host__ __device__ inline size_t seam_state_offset(int HV, int j, int hv, int kind) {
+  return kSeamPlanBytes + ((size_t(j) * HV + hv) * 3 + kind) * kSeamStateBytes;
+}
+__host__ __device__ inline size_t seam_ox_offset(int k_slots, int HV) {
+  return kSeamPlanBytes + size_t(k_slots) * HV * 3 * kSeamStateBytes;
+}
+__host__ __device__ inline size_t seam_region_bytes(int k_slots, int HV, int ox_rows) {
+  return seam_ox_offset(k_slots, HV) + size_t(ox_rows) * HV * D * 2;
+}
+
 // Lower 16x16 tiles of a 64x64 chunk matrix, row-major: tile -> (ti, tj).
 template <int TILE>
 struct Tile16 {

@@ -33,6 +33,13 @@ void* prefill_scratch(hipError_t* err);
 // Enqueues both launches on st; workspace holds prefill_split_workspace_bytes.
 // With h non-NULL the slices also write the bf16 state entering every chunk
 // to h[chunk_offset(n) + i] for slots below h_chunks.
+// Seam pass over a seam region (layout in gdn_prefill_common.h) of k_slots
+// slots and ox_rows OX rows: for the first `seams` slots, the final states
+// and the tail outputs' correction, max_tail_chunks bounding every seam's
+// tail chunks.  Enqueued on st.
+int prefill_seam_pass(char* region, int HV, int k_slots, int ox_rows, int seams, int max_tail_chunks,
+                      uint16_t* out, float* final_state, hipStream_t st);
+
 int prefill_split_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* state,
                          const float* A_log, const uint16_t* a, const float* dt_bias,
                          const uint16_t* b, const void* cu_seqlens, int cu_is_int32, int N, int T,

@@ -87,7 +87,6 @@ __host__ __device__ inline size_t order_offset(int n_slots, int HQ, int HV) {
 // (order[]): seams go to the j longest sequences, j <= the workgroups left
 // idle allow, choosing j by a chunk-period model (a split halves the longest
 // chain; the seam pass costs about kSeamCostChunks chunk periods).
-constexpr int kMaxSeams = 8;          // seams per launch
 constexpr int kSeamMaxChains = 64;    // (sequence, v-head) chains up to which seams are considered
 constexpr int kSeamMinChunks = 8;     // shortest chain split
 constexpr int kSeamCostChunks = 5;    // seam pass, in chunk periods of a slice
@@ -107,33 +106,17 @@ __host__ __device__ inline int seam_room(int N, int HV, int slices, int cus) {
   return int(k);
 }
 
-// Workspace of the seams, after the order[] ints: the seam plan (below), per
-// seam and v-head three fp32 [128][128] states (the head's final state, the
-// tail's zero-state final state, the transition X stored transposed), then
-// the transition outputs OX of every seam's tail tokens, bf16 [rows][HV][128].
-//
-// The plan, written by the slice launch for the seam pass: kSeamPlanStride
-// ints per seam slot j < the launch's room, sequence -1 in the slots past the
-// seam count.
-constexpr int kSeamPlanStride = 8;
-enum SeamPlanField { SP_SEQ, SP_BOS, SP_LEN, SP_SPLIT, SP_CHUNKS, SP_OX_ROW };
-constexpr size_t kSeamPlanBytes = 512;
-static_assert(size_t(kSeamPlanStride) * kMaxSeams * sizeof(int) <= kSeamPlanBytes, "seam plan");
+// The seam region of the split path follows the order[] ints; its slots:
+// min(N, kMaxSeams), its OX rows seam_ox_rows(N, T).  The slice launch writes
+// the plan (slots past the seam count get sequence -1).
 __host__ __device__ inline size_t seam_plan_offset(int n_slots, int N, int HQ, int HV) {
   return order_offset(n_slots, HQ, HV) + (size_t(N) * sizeof(int) + 255) / 256 * 256;
 }
-__host__ __device__ inline size_t seam_offset(int n_slots, int N, int HQ, int HV) {
-  return seam_plan_offset(n_slots, N, HQ, HV) + kSeamPlanBytes;
-}
-constexpr size_t kSeamStateBytes = size_t(D) * D * 4;
-__host__ __device__ inline size_t seam_ox_offset(int n_slots, int N, int HQ, int HV) {
-  const int k = N < kMaxSeams ? N : kMaxSeams;
-  return seam_offset(n_slots, N, HQ, HV) + size_t(k) * HV * 3 * kSeamStateBytes;
-}
+__host__ __device__ inline int seam_slots(int N) { return N < kMaxSeams ? N : kMaxSeams; }
+__host__ __device__ inline int seam_ox_rows(int N, int T) { return T / 2 + C * seam_slots(N); }
 __host__ __device__ inline size_t seam_bytes(int N, int T, int HV) {
-  if ((long long)N * HV > kSeamMaxChains) return 0;
-  const int k = N < kMaxSeams ? N : kMaxSeams;
-  return size_t(k) * HV * 3 * kSeamStateBytes + size_t(T / 2 + C * k) * HV * D * 2;
+  if ((long long)N * HV > kSeamMaxChains) return kSeamPlanBytes;
+  return seam_region_bytes(seam_slots(N), HV, seam_ox_rows(N, T));
 }
 
 // The seams of a launch, identical in every workgroup and in the seam pass:
@@ -176,9 +159,6 @@ __device__ int seam_rows_before(const CuT* cu, const int* order, int T, int j) {
     row += max(0, ll - C * seam_split_chunk((ll + C - 1) / C));
   }
   return row;
-}
-__host__ __device__ inline int seam_ox_rows(int N, int T) {
-  return T / 2 + C * (N < kMaxSeams ? N : kMaxSeams);
 }
 
 // HBM -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): from
@@ -690,7 +670,8 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   const int n = order[rank];
   const int hv = hq * G + m;
   const int vb = R * s;                         // first state row of the slice
-  int* plan = reinterpret_cast<int*>(ws + seam_plan_offset(nt_bound, N, HQ, HV));
+  char* seam_ws = ws + seam_plan_offset(nt_bound, N, HQ, HV);   // the seam region
+  int* plan = reinterpret_cast<int*>(seam_ws);
   if (blockIdx.x == 0 && tid == 0)
     for (int jj = n_seams; jj < seam_room_; ++jj) plan[kSeamPlanStride * jj + SP_SEQ] = -1;
 
@@ -714,8 +695,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   auto record = [&](int ch) { return ws + (size_t(coff + ch) * HV + hv) * kBlob; };
   // seam state j of kind (0 head final, 1 tail final, 2 transition X^T) of this v-head
   auto seam_state = [&](int kind) {
-    return reinterpret_cast<float*>(ws + seam_offset(nt_bound, N, HQ, HV) +
-                                    ((size_t(rank) * HV + hv) * 3 + kind) * kSeamStateBytes);
+    return reinterpret_cast<float*>(seam_ws + seam_state_offset(HV, rank, hv, kind));
   };
   // first OX row of seam `rank`: the tail tokens of the seams before it
   auto seam_ox_row = [&]() { return seam_rows_before(cu_seqlens, order, T, rank); };
@@ -953,7 +933,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           uint32_t orow_n = uint32_t(L);
           if (role == 3) {
             const int r0 = seam_ox_row() + (ch - ch0) * C;
-            obase = reinterpret_cast<uint16_t*>(ws + seam_ox_offset(nt_bound, N, HQ, HV)) + size_t(r0) * v_stride;
+            obase = reinterpret_cast<uint16_t*>(seam_ws + seam_ox_offset(seam_slots(N), HV)) + size_t(r0) * v_stride;
             orow_n = uint32_t(max(0, min(L, seam_ox_rows(N, T) - r0)));
           }
           const __amdgpu_buffer_rsrc_t orows =
@@ -1122,16 +1102,16 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 }
 
 // ---------------------------------------------------------------------------
-// Seam pass, after the slices: for seam j and v-head hv (blockIdx.y), pieces
-// 0 .. kSeamStatePieces - 1 (blockIdx.x) write a 16 x 64 block each of the
-// sequence's final state S_sp X + S0; piece p >= kSeamStatePieces adds
-// OX_c S_sp^T to the outputs of tail chunk c = sp + p - kSeamStatePieces (the
-// part of the tail outputs that depends on the state the head reached).  The
-// final state takes fp32-accurate products (each fp32 operand split into two
-// fp16 parts, three 16x16x16 MFMA products); the outputs bf16 products, as
-// the output path does.  Four waves; every wave issues all its loads (both
-// operands and, for outputs, the values it adds to) before its first MFMA,
-// so a piece costs one memory round trip and a few dozen MFMAs.
+// Seam pass, after the chains.  For seam j and v-head hv: pieces
+// 0 .. kSeamStatePieces - 1 write a 16 x 64 block each of the sequence's
+// final state S_sp X + S0; piece p >= kSeamStatePieces adds OX_c S_sp^T to the
+// outputs of tail chunk c = sp + p - kSeamStatePieces (the part of the tail
+// outputs that depends on the state the head reached).  The final state takes
+// fp32-accurate products (each fp32 operand split into two fp16 parts, three
+// 16x16x16 MFMA products); the outputs bf16 products, as the output path
+// does.  Four waves; every wave issues all its loads (both operands and, for
+// outputs, the values it adds to) before its first MFMA, so a piece costs one
+// memory round trip and a few dozen MFMAs.
 constexpr int kSeamThreads = 256;
 constexpr int kSeamStatePieces = 2 * D / 16;
 
@@ -1143,29 +1123,34 @@ __device__ __forceinline__ void split_f16(const f32x4& x, f16x4_t& hi, f16x4_t& 
   }
 }
 
-template <typename CuT>
+__host__ __device__ inline int seam_pieces(int max_tail_chunks) { return kSeamStatePieces + max_tail_chunks; }
+
 __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
-    const CuT* __restrict__ cu_seqlens, int N, int T, int HQ, int HV, const char* __restrict__ ws,
-    int nt_bound, int seam_room_, uint16_t* __restrict__ out, float* __restrict__ ht) {
+    const char* __restrict__ region, int HV, int k_slots, int ox_rows, int seams, int pieces,
+    uint16_t* __restrict__ out, float* __restrict__ ht) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int g = lane >> 4, c = lane & 15;
-  const int j = int(blockIdx.y) / HV, hv = int(blockIdx.y) - j * HV;
-  if (j >= seam_room_) return;
-  // the plan entry the slices wrote for seam slot j (sequence or -1, bounds,
-  // split, first OX row), one load
-  const int* plan = reinterpret_cast<const int*>(ws + seam_plan_offset(nt_bound, N, HQ, HV));
+  // Workgroup -> (seam j, v-head hv, piece): the pieces of one (j, hv) get ids
+  // 8 apart, which puts them on one XCD (ids go round-robin over the 8 XCDs),
+  // so its three states come from HBM into one L2 once.
+  const int xcd = int(blockIdx.x) & 7, id_row = int(blockIdx.x) >> 3;
+  const int jh = 8 * (id_row / pieces) + xcd;
+  const int piece = id_row - (id_row / pieces) * pieces;
+  const int j = jh / HV, hv = jh - j * HV;
+  if (j >= seams || j >= k_slots) return;
+  // the plan entry of seam slot j (sequence or -1, bounds, split, first OX
+  // row), one load
+  const int* plan = reinterpret_cast<const int*>(region);
   const int pe = plan[kSeamPlanStride * j + (lane & (kSeamPlanStride - 1))];   // lane f: field f
   const int n = __builtin_amdgcn_readlane(pe, SP_SEQ);
   if (n < 0) return;
   const int bos = __builtin_amdgcn_readlane(pe, SP_BOS), len = __builtin_amdgcn_readlane(pe, SP_LEN);
   const int sp = __builtin_amdgcn_readlane(pe, SP_SPLIT), n_all = __builtin_amdgcn_readlane(pe, SP_CHUNKS);
   const int ox_row0 = __builtin_amdgcn_readlane(pe, SP_OX_ROW);
-  const int piece = int(blockIdx.x);
   if (piece >= kSeamStatePieces + n_all - sp) return;
   auto state = [&](int kind) {
-    return reinterpret_cast<const float*>(ws + seam_offset(nt_bound, N, HQ, HV) +
-                                          ((size_t(j) * HV + hv) * 3 + kind) * kSeamStateBytes);
+    return reinterpret_cast<const float*>(region + seam_state_offset(HV, j, hv, kind));
   };
   const float* Ssp = state(0);
   if (piece < kSeamStatePieces) {
@@ -1200,10 +1185,9 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
   // out[t][hv][v]; wave w: row blocks tm = 2w, 2w + 1, token blocks tn 0..3
   const int ch = sp + piece - kSeamStatePieces;
   const int t0 = bos + ch * C, L = min(C, len - ch * C);
-  const int ox_rows = seam_ox_rows(N, T);
   const int r0 = ox_row0 + (ch - sp) * C;
   const size_t v_stride = size_t(HV) * D;
-  const uint16_t* OX = reinterpret_cast<const uint16_t*>(ws + seam_ox_offset(nt_bound, N, HQ, HV));
+  const uint16_t* OX = reinterpret_cast<const uint16_t*>(region + seam_ox_offset(k_slots, HV));
   f32x4 sa[2][4][2];
   uint4 ob[4][4];
   uint2 ov[2][4];
@@ -1254,6 +1238,26 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
     }
   }
 }
+
+}  // namespace
+
+namespace gdn {
+
+int prefill_seam_pass(char* region, int HV, int k_slots, int ox_rows, int seams, int max_tail_chunks,
+                      uint16_t* out, float* final_state, hipStream_t st) {
+  if (seams <= 0) return GDN_OK;
+  const unsigned pieces = unsigned(seam_pieces(max_tail_chunks));
+  const unsigned pairs = unsigned(seams) * unsigned(HV);
+  const dim3 grid{8u * pieces * ((pairs + 7u) / 8u), 1u, 1u};
+  hipLaunchKernelGGL(gdn_prefill_seam_kernel, grid, dim3(kSeamThreads), 0, st, region, HV, k_slots, ox_rows,
+                     seams, int(pieces), out, final_state);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GDN_OK : -int(e);
+}
+
+}  // namespace gdn
+
+namespace {
 
 int device_cu_count();
 
@@ -1311,10 +1315,10 @@ int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   if (room > 0) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return -int(e);
-    // pieces: the final state's row blocks, then the longest possible tail
-    const dim3 sgrid{unsigned(kSeamStatePieces + (nt_bound + 1) / 2 + 1), unsigned(room * HV), 1u};
-    hipLaunchKernelGGL((gdn_prefill_seam_kernel<CuT>), sgrid, dim3(kSeamThreads), 0, st, cu, N, T, HQ, HV,
-                       ws, nt_bound, room, out, final_state);
+    // pieces: the final state's blocks, then the longest possible tail
+    const int r = prefill_seam_pass(ws + seam_plan_offset(nt_bound, N, HQ, HV), HV, seam_slots(N),
+                                    seam_ox_rows(N, T), room, (nt_bound + 1) / 2 + 1, out, final_state, st);
+    if (r != GDN_OK) return r;
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GDN_OK : -int(e);
@@ -1371,7 +1375,7 @@ namespace gdn {
 
 size_t prefill_split_workspace_bytes(int N, int T, int HQ, int HV) {
   if (N <= 0 || T < 0 || HQ <= 0 || HV <= 0) return 0;
-  return seam_offset(T / C + N, N, HQ, HV) + seam_bytes(N, T, HV);
+  return seam_plan_offset(T / C + N, N, HQ, HV) + seam_bytes(N, T, HV);
 }
 
 int prefill_split_auto_slices(int N, int HV) {

@@ -22,6 +22,7 @@ stream.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import weakref
 from typing import Optional
@@ -49,6 +50,8 @@ _CU_HOST = {}
 # Path choices by (host copy, T, HV, device): (the host copy, slices per
 # chain, 0 = fused); holding the copy keeps its id from being reused.
 _CHOICE = {}
+# Launch plans by (host copy, T, HQ, HV, flags, device): (the host copy, plan).
+_PLANS = {}
 # Split-path workspaces by (device, stream), reused by later calls on the
 # same stream (stream order keeps them from overlapping).
 _WORKSPACE = {}
@@ -147,6 +150,53 @@ def choose_slices(cu_host: torch.Tensor, T: int, HV: int) -> int:
     return s
 
 
+class Plan:
+    """A prefill launch plan made on the host from the sequence lengths
+    (``gdn_prefill_plan``): the path (``slices`` 4 / 8: the split path, 0:
+    the fused kernel), the fused kernel's seams (``seams`` sequences cut at
+    chunk ``split_chunk``; ``periods``: the modelled finish in chunk periods)
+    and the device workspace :func:`gdn_prefill` needs with it."""
+
+    __slots__ = ("buf", "slices", "seams", "split_chunk", "periods", "workspace_bytes")
+
+    def __init__(self, cu_host: torch.Tensor, T: int, HQ: int, HV: int, *, seams: bool = True,
+                 fused: bool = False, cus: int = 0):
+        cu = cu_host.contiguous()
+        assert not cu.is_cuda and cu.dtype in (torch.int64, torch.int32) and cu.dim() == 1
+        lib = _capi.lib()
+        self.buf = ctypes.create_string_buffer(_capi.GDN_PREFILL_PLAN_BYTES)
+        ws = ctypes.c_size_t(0)
+        flags = (0 if seams else _capi.GDN_NO_SEAMS) | (_capi.GDN_PLAN_FUSED if fused else 0)
+        _capi.check(lib.gdn_prefill_plan(cu.data_ptr(), 1 if cu.dtype == torch.int32 else 0,
+                                         cu.numel() - 1, int(T), int(HQ), int(HV), int(cus), flags,
+                                         self.buf, ctypes.byref(ws)), "gdn_prefill_plan")
+        info = [ctypes.c_int(0) for _ in range(4)]
+        _capi.check(lib.gdn_prefill_plan_info(self.buf, *[ctypes.byref(i) for i in info]),
+                    "gdn_prefill_plan_info")
+        self.slices, self.seams, self.split_chunk, self.periods = (int(i.value) for i in info)
+        self.workspace_bytes = int(ws.value)
+
+    @property
+    def path(self) -> str:
+        if self.slices:
+            return f"split{self.slices}"
+        return f"fused+{self.seams}seams" if self.seams else "fused"
+
+
+def _plan_for(cu_host: torch.Tensor, T: int, HQ: int, HV: int, seams: bool, fused: bool,
+              device) -> Plan:
+    """The plan of these lengths, made once per host copy of ``cu_seqlens``."""
+    key = (id(cu_host), int(T), int(HQ), int(HV), bool(seams), bool(fused), device.index)
+    ent = _PLANS.get(key)
+    if ent is not None and ent[0] is cu_host:
+        return ent[1]
+    plan = Plan(cu_host, T, HQ, HV, seams=seams, fused=fused)
+    if len(_PLANS) >= 256:
+        _PLANS.clear()
+    _PLANS[key] = (cu_host, plan)
+    return plan
+
+
 def split_workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
     """Workspace of the split path (chunk preparation + state slices)."""
     return int(_capi.lib().gdn_prefill_split_workspace_bytes(N, T, HQ, HV))
@@ -184,17 +234,18 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
 
     ``path`` selects the kernels: ``"auto"`` (the split path -- a parallel
     chunk-preparation launch and ``HV * N * slices`` state slices -- or the
-    fused chain kernel, whichever :func:`choose_slices` expects to finish
-    first for these sequence lengths; with ``validate=False`` the lengths are
-    not read and the library decides from N and HV alone), ``"fused"`` (one workgroup per chain) or ``"split"`` with
-    ``slices`` in (4, 8) state slices per chain.  Without ``qk_l2norm`` the
-    two paths perform the state-path operations in the same order: their
-    final states agree bit for bit but for rare last-place differences (one
-    or two sequences in thousands).  ``seams=False`` keeps that equality
-    where the split path would otherwise cut its longest sequences in two in
-    time to use idle CUs (a zero-state tail and a transition chain beside the
-    head, joined by a seam pass; results then agree with the serial chain to
-    the rounding of the state path, and the per-chunk states ``h`` never use
+    fused chain kernel, whichever the library's :class:`Plan` of these
+    sequence lengths expects to finish first; with ``validate=False`` the
+    lengths are not read and the library decides from N and HV alone),
+    ``"fused"`` (one workgroup per chain) or ``"split"`` with ``slices`` in
+    (4, 8) state slices per chain.  Without ``qk_l2norm`` the two paths
+    perform the state-path operations in the same order: their final states
+    agree bit for bit but for rare last-place differences (one or two
+    sequences in thousands).  ``seams=False`` keeps that equality where
+    either path would otherwise cut its longest sequences in two in time to
+    use idle CUs (a zero-state tail and a transition chain beside the head,
+    joined by a seam pass; results then agree with the serial chain to the
+    rounding of the state path, and the per-chunk states ``h`` never use
     seams).
 
     Input range: the state path multiplies fp16 operands, so k, v, the state
@@ -237,6 +288,21 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
     assert final_state.dtype == torch.float32 and final_state.is_contiguous()
     assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
     assert path in ("auto", "fused", "split"), path
+    flags = (_capi.GDN_QK_L2NORM if qk_l2norm else 0) | (0 if seams else _capi.GDN_NO_SEAMS)
+    if path in ("auto", "fused") and cu_host is not None and h is None:
+        plan = _plan_for(cu_host, T, nq, nv, seams, path == "fused", q.device)
+        ws_need = plan.workspace_bytes
+        if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
+            workspace = _split_workspace(ws_need, q.device)
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        rc = _capi.lib().gdn_prefill_plan_fwd(
+            _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(state), _capi.ptr(A_log),
+            _capi.ptr(a), _capi.ptr(dt_bias), _capi.ptr(b), _capi.ptr(cu),
+            1 if cu.dtype == torch.int32 else 0, N, T, nq, nv, float(scale),
+            _capi.ptr(output), _capi.ptr(final_state), plan.buf, _capi.ptr(workspace), ws_bytes,
+            flags, _capi.stream_handle(q.device))
+        _capi.check(rc, "gdn_prefill_plan_fwd")
+        return output, final_state
     if path == "auto" and cu_host is not None:
         key = (id(cu_host), T, nv, q.device.index)
         ent = _CHOICE.get(key)
@@ -258,7 +324,6 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, out
     if ws_need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < ws_need):
         workspace = _split_workspace(ws_need, q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    flags = (_capi.GDN_QK_L2NORM if qk_l2norm else 0) | (0 if seams else _capi.GDN_NO_SEAMS)
     if h is not None:
         assert h.dtype == torch.bfloat16 and h.is_contiguous() and h.device == q.device
         assert h.dim() == 4 and h.shape[1:] == (nv, HEAD_SIZE, HEAD_SIZE)
@@ -350,14 +415,15 @@ class PreparedPrefill:
     """A prefill call on fixed buffers, validated once and launched by one C call.
 
     ``cu_seqlens`` is read back once here (the reference's ``cu_seqlens[-1]
-    == T`` check, and the path choice of :func:`choose_slices`: ``path`` is
-    ``"fused"``, ``"split4"`` or ``"split8"``); ``__call__`` only enqueues
-    the launches on the stream that was current at construction.
-    ``qk_l2norm`` and ``seams`` as for :func:`gdn_prefill`.
+    == T`` check, and the library's :class:`Plan` of the lengths: ``path``
+    is ``"split4"``, ``"split8"``, ``"fused"`` or ``"fused+<k>seams"``);
+    ``__call__`` only enqueues the launches on the stream that was current at
+    construction.  ``qk_l2norm`` and ``seams`` as for :func:`gdn_prefill`;
+    ``fused=True`` plans the fused kernel whatever the lengths favour.
     """
 
     def __init__(self, q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
-                 final_state, *, qk_l2norm: bool = False, seams: bool = True):
+                 final_state, *, qk_l2norm: bool = False, seams: bool = True, fused: bool = False):
         T, nq, _ = q.shape
         nv = v.shape[1]
         cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, nq, nv)
@@ -369,10 +435,11 @@ class PreparedPrefill:
         assert output.shape == (T, nv, HEAD_SIZE)
         assert final_state.dtype == torch.float32 and final_state.is_contiguous()
         assert final_state.shape == (N, nv, HEAD_SIZE, HEAD_SIZE)
-        # the path the sequence lengths favour: 8 / 4 state slices or fused
-        self.slices = choose_slices(cu_host, T, nv) if N > 0 else 0
-        self.path = f"split{self.slices}" if self.slices else "fused"
-        ws = split_workspace_bytes(N, T, nq, nv) if self.slices else 0
+        # the path and seams the sequence lengths favour
+        self.plan = Plan(cu_host, T, nq, nv, seams=seams, fused=fused)
+        self.slices = self.plan.slices
+        self.path = self.plan.path
+        ws = self.plan.workspace_bytes
         self._ws = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
         self._keep = (q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, final_state)
         head = (
@@ -381,13 +448,9 @@ class PreparedPrefill:
             1 if cu_seqlens.dtype == torch.int32 else 0, N, T, nq, nv,
             float(_resolve_scale(scale)), _capi.ptr(output), _capi.ptr(final_state))
         flags = (_capi.GDN_QK_L2NORM if qk_l2norm else 0) | (0 if seams else _capi.GDN_NO_SEAMS)
-        tail = (_capi.ptr(self._ws), ws, flags, _capi.stream_handle(q.device))
-        if self.slices:
-            self._name = "gdn_prefill_split_fwd"
-            self._args = head + (self.slices,) + tail
-        else:
-            self._name = "gdn_prefill_ex_fwd"
-            self._args = head + tail
+        self._name = "gdn_prefill_plan_fwd"
+        self._args = head + (self.plan.buf, _capi.ptr(self._ws), ws, flags,
+                             _capi.stream_handle(q.device))
         self._fn = getattr(_capi.lib(), self._name)
 
     def __call__(self) -> None:
