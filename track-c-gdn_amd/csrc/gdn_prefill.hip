@@ -1315,7 +1315,7 @@ double makespan(const std::vector<int>& chunks, int per_seq, double period, int 
 // modelled finish in chunk periods, the seam pass excluded.
 constexpr double kSeamWgStartupPeriods = 3.5;
 constexpr double kSeamPassFixedCycles = 12000.0;
-constexpr double kSeamPassTokenCycles = 0.9;
+constexpr double kSeamPassTokenCycles = 0.7;
 
 struct FusedPlan {
   int count = 0;

@@ -1105,15 +1105,19 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 // Seam pass, after the chains.  For seam j and v-head hv: pieces
 // 0 .. kSeamStatePieces - 1 write a 16 x 64 block each of the sequence's
 // final state S_sp X + S0; piece p >= kSeamStatePieces adds OX_c S_sp^T to the
-// outputs of tail chunk c = sp + p - kSeamStatePieces (the part of the tail
-// outputs that depends on the state the head reached).  The final state takes
-// fp32-accurate products (each fp32 operand split into two fp16 parts, three
-// 16x16x16 MFMA products); the outputs bf16 products, as the output path
-// does.  Four waves; every wave issues all its loads (both operands and, for
-// outputs, the values it adds to) before its first MFMA, so a piece costs one
-// memory round trip and a few dozen MFMAs.
+// outputs of kSeamGroupChunks tail chunks c from sp + kSeamGroupChunks
+// (p - kSeamStatePieces) on (the part of the tail outputs that depends on the
+// state the head reached).  The final state takes fp32-accurate products
+// (each fp32 operand split into two fp16 parts, three 16x16x16 MFMA
+// products); the outputs bf16 products, as the output path does.  Four waves.
+// A state piece issues all its loads before its first MFMA.  A tail piece
+// stages S_sp once, as bf16 MFMA A fragments in LDS; wave w then owns tokens
+// 16 w .. 16 w + 15 of each chunk across all 128 rows v (its OX rows read
+// once), and loads the next chunk's OX rows and outputs while it works on a
+// chunk.
 constexpr int kSeamThreads = 256;
 constexpr int kSeamStatePieces = 2 * D / 16;
+constexpr int kSeamGroupChunks = 2;
 
 __device__ __forceinline__ void split_f16(const f32x4& x, f16x4_t& hi, f16x4_t& lo) {
 #pragma unroll
@@ -1123,7 +1127,9 @@ __device__ __forceinline__ void split_f16(const f32x4& x, f16x4_t& hi, f16x4_t& 
   }
 }
 
-__host__ __device__ inline int seam_pieces(int max_tail_chunks) { return kSeamStatePieces + max_tail_chunks; }
+__host__ __device__ inline int seam_pieces(int max_tail_chunks) {
+  return kSeamStatePieces + (max_tail_chunks + kSeamGroupChunks - 1) / kSeamGroupChunks;
+}
 
 __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
     const char* __restrict__ region, int HV, int k_slots, int ox_rows, int seams, int pieces,
@@ -1148,7 +1154,7 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
   const int bos = __builtin_amdgcn_readlane(pe, SP_BOS), len = __builtin_amdgcn_readlane(pe, SP_LEN);
   const int sp = __builtin_amdgcn_readlane(pe, SP_SPLIT), n_all = __builtin_amdgcn_readlane(pe, SP_CHUNKS);
   const int ox_row0 = __builtin_amdgcn_readlane(pe, SP_OX_ROW);
-  if (piece >= kSeamStatePieces + n_all - sp) return;
+  if (piece >= kSeamStatePieces + (n_all - sp + kSeamGroupChunks - 1) / kSeamGroupChunks) return;
   auto state = [&](int kind) {
     return reinterpret_cast<const float*>(region + seam_state_offset(HV, j, hv, kind));
   };
@@ -1181,59 +1187,64 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
     for (int i = 0; i < 4; ++i) dst[size_t(16 * tm + 4 * g + i) * D + 16 * tn + c] = acc[i];
     return;
   }
-  // Tail chunk ch: dO^T[v][t] = sum_k' S_sp[v][k'] OX[t][k'], added to
-  // out[t][hv][v]; wave w: row blocks tm = 2w, 2w + 1, token blocks tn 0..3
-  const int ch = sp + piece - kSeamStatePieces;
-  const int t0 = bos + ch * C, L = min(C, len - ch * C);
-  const int r0 = ox_row0 + (ch - sp) * C;
+  // Tail chunks ch of this group: dO^T[v][t] = sum_k' S_sp[v][k'] OX[t][k'],
+  // added to out[t][hv][v].  S_sp as bf16 A fragments in LDS: fragment
+  // (tm, tk) (rows 16 tm .., k' 32 tk ..) at 1 KiB steps, lane (g, c) of it
+  // (row 16 tm + c, k' 32 tk + 8 g .. + 7) at 16 g + c 16-byte slots.
+  __shared__ __align__(16) bf16x8_t sA[8 * 4 * 64];
+  const int tid = threadIdx.x;
+  static_assert(8 * 4 * 64 % kSeamThreads == 0, "staging");
+#pragma unroll 4
+  for (int i = 0; i < 8 * 4 * 64 / kSeamThreads; ++i) {
+    const int idx = tid + kSeamThreads * i;       // (tm, tk, g, c), c fastest: < 2048
+    const int cc = idx & 15, gg = (idx >> 4) & 3, tk = (idx >> 6) & 3, tm = idx >> 8;
+    const float* sr = &Ssp[size_t(16 * tm + cc) * D + 32 * tk + 8 * gg];
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(sr);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(sr + 4);
+    sA[(tm * 4 + tk) * 64 + gg * 16 + cc] =
+        bf16x8_t{(__bf16)s0[0], (__bf16)s0[1], (__bf16)s0[2], (__bf16)s0[3],
+                 (__bf16)s1[0], (__bf16)s1[1], (__bf16)s1[2], (__bf16)s1[3]};
+  }
+  const int chb = sp + (piece - kSeamStatePieces) * kSeamGroupChunks;
+  const int che = min(n_all, chb + kSeamGroupChunks);
   const size_t v_stride = size_t(HV) * D;
   const uint16_t* OX = reinterpret_cast<const uint16_t*>(region + seam_ox_offset(k_slots, HV));
-  f32x4 sa[2][4][2];
-  uint4 ob[4][4];
-  uint2 ov[2][4];
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int tk = 0; tk < 4; ++tk) {
-      const float* sr = &Ssp[size_t(16 * (2 * wave + u) + c) * D + 32 * tk + 8 * g];
-      sa[u][tk][0] = *reinterpret_cast<const f32x4*>(sr);
-      sa[u][tk][1] = *reinterpret_cast<const f32x4*>(sr + 4);
-    }
-#pragma unroll
-  for (int tn = 0; tn < 4; ++tn) {
-    const int orow = min(r0 + 16 * tn + c, ox_rows - 1);   // rows past the region are never used
+  const int t = 16 * wave + c;                    // this lane's token of the chunk (B column)
+  // the token exists: inside the sequence and the OX region
+  auto valid = [&](int ch) { return t < min(C, len - ch * C) && ox_row0 + (ch - sp) * C + t < ox_rows; };
+  auto out_at = [&](int ch, int tm) {
+    return reinterpret_cast<uint2*>(out + size_t(bos + ch * C + t) * v_stride + size_t(hv) * D + 16 * tm + 4 * g);
+  };
+  uint4 ob[2][4];
+  uint2 ov[2][8];
+  auto load = [&](int ch, uint4 (&obb)[4], uint2 (&ovb)[8]) {
+    const int orow = min(ox_row0 + (ch - sp) * C + t, ox_rows - 1);   // rows past the region are never used
 #pragma unroll
     for (int tk = 0; tk < 4; ++tk)
-      ob[tn][tk] = *reinterpret_cast<const uint4*>(&OX[size_t(orow) * v_stride + size_t(hv) * D + 32 * tk + 8 * g]);
-  }
-  auto valid = [&](int t) { return t < L && r0 + t < ox_rows; };
-  auto out_at = [&](int u, int tn) {
-    return reinterpret_cast<uint2*>(out + size_t(t0 + 16 * tn + c) * v_stride + size_t(hv) * D +
-                                    16 * (2 * wave + u) + 4 * g);
+      obb[tk] = *reinterpret_cast<const uint4*>(&OX[size_t(orow) * v_stride + size_t(hv) * D + 32 * tk + 8 * g]);
+    const bool ok = valid(ch);
+#pragma unroll
+    for (int tm = 0; tm < 8; ++tm) ovb[tm] = ok ? *out_at(ch, tm) : uint2{0u, 0u};
   };
+  if (chb < che) load(chb, ob[0], ov[0]);
+  __syncthreads();
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+  for (int i = 0; i < kSeamGroupChunks; ++i) {
+    const int ch = chb + i;
+    if (ch >= che) break;
+    if (ch + 1 < che) load(ch + 1, ob[(i + 1) & 1], ov[(i + 1) & 1]);
+    const bool ok = valid(ch);
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) ov[u][tn] = valid(16 * tn + c) ? *out_at(u, tn) : uint2{0u, 0u};
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    bf16x8_t af[4];
-#pragma unroll
-    for (int tk = 0; tk < 4; ++tk) {
-      const f32x4 s0 = sa[u][tk][0], s1 = sa[u][tk][1];
-      af[tk] = bf16x8_t{(__bf16)s0[0], (__bf16)s0[1], (__bf16)s0[2], (__bf16)s0[3],
-                        (__bf16)s1[0], (__bf16)s1[1], (__bf16)s1[2], (__bf16)s1[3]};
-    }
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
+    for (int tm = 0; tm < 8; ++tm) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int tk = 0; tk < 4; ++tk) acc = mfma16_bf(af[tk], __builtin_bit_cast(bf16x8_t, ob[tn][tk]), acc);
-      if (valid(16 * tn + c)) {
+      for (int tk = 0; tk < 4; ++tk)
+        acc = mfma16_bf(sA[(tm * 4 + tk) * 64 + lane], __builtin_bit_cast(bf16x8_t, ob[i & 1][tk]), acc);
+      if (ok) {
         float f0, f1, f2, f3;
-        unpack_bf16x2(ov[u][tn].x, f0, f1);
-        unpack_bf16x2(ov[u][tn].y, f2, f3);
-        *out_at(u, tn) = uint2{cvt_pk_bf16(f0 + acc[0], f1 + acc[1]), cvt_pk_bf16(f2 + acc[2], f3 + acc[3])};
+        unpack_bf16x2(ov[i & 1][tm].x, f0, f1);
+        unpack_bf16x2(ov[i & 1][tm].y, f2, f3);
+        *out_at(ch, tm) = uint2{cvt_pk_bf16(f0 + acc[0], f1 + acc[1]), cvt_pk_bf16(f2 + acc[2], f3 + acc[3])};
       }
     }
   }
