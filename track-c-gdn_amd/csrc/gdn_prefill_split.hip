@@ -1103,8 +1103,8 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 
 // ---------------------------------------------------------------------------
 // Seam pass, after the chains.  For seam j and v-head hv: pieces
-// 0 .. kSeamStatePieces - 1 write a 16 x 64 block each of the sequence's
-// final state S_sp X + S0; piece p >= kSeamStatePieces adds OX_c S_sp^T to the
+// 0 .. kSeamStatePieces - 1 write 16 rows each of the sequence's final state
+// S_sp X + S0; piece p >= kSeamStatePieces adds OX_c S_sp^T to the
 // outputs of kSeamGroupChunks tail chunks c from sp + kSeamGroupChunks
 // (p - kSeamStatePieces) on (the part of the tail outputs that depends on the
 // state the head reached).  The final state takes fp32-accurate products
@@ -1116,7 +1116,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 // once), and loads the next chunk's OX rows and outputs while it works on a
 // chunk.
 constexpr int kSeamThreads = 256;
-constexpr int kSeamStatePieces = 2 * D / 16;
+constexpr int kSeamStatePieces = D / 16;
 constexpr int kSeamGroupChunks = 2;
 
 __device__ __forceinline__ void split_f16(const f32x4& x, f16x4_t& hi, f16x4_t& lo) {
@@ -1161,30 +1161,40 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
   const float* Ssp = state(0);
   if (piece < kSeamStatePieces) {
     // S_L[v][k] = sum_k' S_sp[v][k'] X[k'][k] + S0[v][k] for rows v of block
-    // tm = piece / 2; wave w: column block tn = 4 (piece % 2) + w
-    const int tm = piece >> 1, tn = 4 * (piece & 1) + wave;
+    // tm = piece; wave w: column blocks tn = 2 w, 2 w + 1
+    const int tm = piece;
     const float* S0 = state(1);
     const float* XT = state(2);
-    f32x4 sa[8], xb[8], acc;
+    f32x4 sa[8], xb[2][8], acc[2];
 #pragma unroll
     for (int tk = 0; tk < 8; ++tk) {
       sa[tk] = *reinterpret_cast<const f32x4*>(&Ssp[size_t(16 * tm + c) * D + 16 * tk + 4 * g]);
-      xb[tk] = *reinterpret_cast<const f32x4*>(&XT[size_t(16 * tn + c) * D + 16 * tk + 4 * g]);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        xb[u][tk] = *reinterpret_cast<const f32x4*>(&XT[size_t(16 * (2 * wave + u) + c) * D + 16 * tk + 4 * g]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = S0[size_t(16 * tm + 4 * g + i) * D + 16 * tn + c];
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[u][i] = S0[size_t(16 * tm + 4 * g + i) * D + 16 * (2 * wave + u) + c];
 #pragma unroll
     for (int tk = 0; tk < 8; ++tk) {
-      f16x4_t ah, al, bh, bl;
+      f16x4_t ah, al;
       split_f16(sa[tk], ah, al);
-      split_f16(xb[tk], bh, bl);
-      acc = mfma16k16(ah, bh, acc);
-      acc = mfma16k16(ah, bl, acc);
-      acc = mfma16k16(al, bh, acc);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        f16x4_t bh, bl;
+        split_f16(xb[u][tk], bh, bl);
+        acc[u] = mfma16k16(ah, bh, acc[u]);
+        acc[u] = mfma16k16(ah, bl, acc[u]);
+        acc[u] = mfma16k16(al, bh, acc[u]);
+      }
     }
     float* dst = ht + (size_t(n) * HV + hv) * size_t(D) * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[size_t(16 * tm + 4 * g + i) * D + 16 * tn + c] = acc[i];
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[size_t(16 * tm + 4 * g + i) * D + 16 * (2 * wave + u) + c] = acc[u][i];
     return;
   }
   // Tail chunks ch of this group: dO^T[v][t] = sum_k' S_sp[v][k'] OX[t][k'],
