@@ -66,13 +66,18 @@ def _to(x, dev):
     return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in x.items()}
 
 
-def _traffic(name: str):
+def _traffic(name: str, path: str = None):
+    """Bytes per launch from profiles/<name>_traffic.json; with ``path``, only
+    when the profile was measured on that path."""
     p = ROOT / "profiles" / f"{name}_traffic.json"
     if p.exists():
         try:
-            return json.loads(p.read_text()).get("bytes_per_launch")
+            d = json.loads(p.read_text())
         except Exception:
             return None
+        if path is not None and d.get("path") != path:
+            return None
+        return d.get("bytes_per_launch")
     return None
 
 
@@ -186,7 +191,7 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk
     return dict(total_ms=total_ms, kernel_ms=kern_ms, T=T, N=N, lens=lens, HQ=w["HQ"],
                 HV=w["HV"], flops=prefill_flops(T, w["HV"]),
                 flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True),
-                path=call.path)
+                path=call.path, kernels=call.plan.kernels)
 
 
 # Fused prefill over sequences of one length, qk16/v32: the chunk period at
@@ -639,8 +644,7 @@ def main():
                 r = bench_prefill(dev, args.prefill_steps, PREFILL_WARMUP, name=name)
                 kus = r["kernel_ms"] * 1e3
                 tfl = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
-                kernels = (["gdn_prefill_prep_kernel", "gdn_prefill_slice_kernel"]
-                           if r["path"].startswith("split") else ["gdn_prefill_chain_kernel"])
+                kernels = r["kernels"]
                 line[name] = {
                     "workload": name, "tokens": r["T"], "sequences": r["N"], "qk_heads": r["HQ"],
                     "v_heads": r["HV"], "path": r["path"], "kernel_us": round(kus, 2),
@@ -649,12 +653,12 @@ def main():
                                  "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4),
                                  "flops_per_launch": r["flops"], "kernels": kernels,
-                                 "time_basis": "both launches of one call" if len(kernels) > 1
+                                 "time_basis": "every launch of one call" if len(kernels) > 1
                                  else "one launch"}}
-                if r["path"].startswith("split"):
-                    tr = _traffic("gdn_prefill_split_" + name[len("prefill_"):])
-                    if tr is not None:
-                        line[name]["roofline"]["traffic"] = tr
+                tag = "split" if r["path"].startswith("split") else "fused"
+                tr = _traffic(f"gdn_prefill_{tag}_" + name[len("prefill_"):], path=r["path"])
+                if tr is not None:
+                    line[name]["roofline"]["traffic"] = tr
                 print(f"# {name} ({r['path']}): {kus:.1f} us, {tfl:.1f} TFLOP/s "
                       f"({tfl / MFMA_BF16_PEAK_TFLOPS * 100:.2f}% of bf16 MFMA peak)",
                       file=sys.stderr, flush=True)

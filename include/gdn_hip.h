@@ -224,10 +224,12 @@ int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int 
 int gdn_prefill_plan(const void* cu_seqlens_host, int cu_is_int32, int N, int T, int HQ, int HV,
                      int cus, int flags, void* plan, size_t* workspace_bytes);
 
-/* Of a plan: the path (*slices: 4 / 8 split, 0 fused), the fused seams
- * (*seams), their cut chunk (*split_chunk, 0 without seams) and the modelled
- * fused finish in chunk periods (*periods, the seam pass excluded); any
- * pointer may be NULL.  GDN_ERR_SHAPE if `plan` is not one. */
+/* Of a plan: the path (*slices: 4 / 8 split, 0 fused); *seams: the fused
+ * kernel's seams, or on the split path the seam slots its launch reserves
+ * (the seams themselves chosen on the device; any slot adds the seam pass);
+ * the fused seams' cut chunk (*split_chunk, 0 without seams) and the
+ * modelled fused finish in chunk periods (*periods, the seam pass excluded);
+ * any pointer may be NULL.  GDN_ERR_SHAPE if `plan` is not one. */
 int gdn_prefill_plan_info(const void* plan, int* slices, int* seams, int* split_chunk, int* periods);
 
 /*

@@ -197,9 +197,11 @@ def test_plan_on_measured_batches():
     # the 32k batch: fused, no seams, the longest chain's 84 periods, no workspace
     rc, _, p = _plan(inp.workload_lengths("prefill_varlen8_t32768_qk16_v32"), 16, 32)
     assert (p["slices"], p["seams"], p["periods"], p["workspace"]) == (0, 0, 84, 0)
-    # one 4096-token sequence at qk4/v8: the split path (8 slices) and its workspace
+    # one 4096-token sequence at qk4/v8: the split path (8 slices: 64 of 256
+    # CUs, room for one seam, 2 x 8 x 8 workgroups) and its workspace
     rc, _, p = _plan([4096], 4, 8)
-    assert (p["slices"], p["seams"]) == (8, 0)
+    assert (p["slices"], p["seams"]) == (8, 1)
+    assert _plan([4096], 4, 8, flags=capi.GDN_NO_SEAMS)[2]["seams"] == 0
     assert p["workspace"] == capi.lib().gdn_prefill_split_workspace_bytes(1, 4096, 4, 8)
     # ... or, asked for the fused kernel, cut a little past half (the tail
     # workgroups' start-up) on the idle CUs

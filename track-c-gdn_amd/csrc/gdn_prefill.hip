@@ -1416,6 +1416,7 @@ struct PrefillPlan {
   uint32_t magic;
   int N, T, HQ, HV;
   int slices;                 // 4 / 8: the split path; 0: the fused kernel
+  int split_seams;            // seam slots the split launch reserves
   FusedPlan fused;            // the fused kernel's seams
   unsigned long long workspace_bytes;
 };
@@ -1434,6 +1435,7 @@ void make_plan(const CuT* cu, int N, int T, int HQ, int HV, int cus, bool seams,
   p.slices = T > 0 && !fused_only ? choose_path(cu, N, T, HV, cus, p.fused) : 0;
   if (p.slices) {
     p.fused = FusedPlan{};
+    p.split_seams = seams ? gdn::prefill_split_seam_room(N, HV, p.slices, cus) : 0;
     p.workspace_bytes = gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
   } else {
     p.workspace_bytes = p.fused.count ? seam_region_bytes(p.fused.count, HV, p.fused.ox_rows) : 0;
@@ -1478,7 +1480,7 @@ extern "C" int gdn_prefill_plan_info(const void* plan, int* slices, int* seams, 
   std::memcpy(&p, plan, sizeof(p));
   if (p.magic != kPlanMagic) return GDN_ERR_SHAPE;
   if (slices) *slices = p.slices;
-  if (seams) *seams = p.fused.count;
+  if (seams) *seams = p.slices ? p.split_seams : p.fused.count;
   if (split_chunk) *split_chunk = p.fused.count ? p.fused.sp[0] : 0;
   if (periods) *periods = p.fused.periods;
   return GDN_OK;

@@ -33,6 +33,11 @@ void* prefill_scratch(hipError_t* err);
 // Enqueues both launches on st; workspace holds prefill_split_workspace_bytes.
 // With h non-NULL the slices also write the bf16 state entering every chunk
 // to h[chunk_offset(n) + i] for slots below h_chunks.
+// Seam slots the split launch reserves for N sequences of HV v-heads in
+// `slices` slices on `cus` CUs (the seams themselves are chosen on the
+// device; 0: no seam pass).
+int prefill_split_seam_room(int N, int HV, int slices, int cus);
+
 // Seam pass over a seam region (layout in gdn_prefill_common.h) of k_slots
 // slots and ox_rows OX rows: for the first `seams` slots, the final states
 // and the tail outputs' correction, max_tail_chunks bounding every seam's

@@ -1264,6 +1264,8 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
 
 namespace gdn {
 
+int prefill_split_seam_room(int N, int HV, int slices, int cus) { return seam_room(N, HV, slices, cus); }
+
 int prefill_seam_pass(char* region, int HV, int k_slots, int ox_rows, int seams, int max_tail_chunks,
                       uint16_t* out, float* final_state, hipStream_t st) {
   if (seams <= 0) return GDN_OK;

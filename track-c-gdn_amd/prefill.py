@@ -153,9 +153,11 @@ def choose_slices(cu_host: torch.Tensor, T: int, HV: int) -> int:
 class Plan:
     """A prefill launch plan made on the host from the sequence lengths
     (``gdn_prefill_plan``): the path (``slices`` 4 / 8: the split path, 0:
-    the fused kernel), the fused kernel's seams (``seams`` sequences cut at
-    chunk ``split_chunk``; ``periods``: the modelled finish in chunk periods)
-    and the device workspace :func:`gdn_prefill` needs with it."""
+    the fused kernel), the seams (the fused kernel's: ``seams`` sequences cut
+    at chunk ``split_chunk``, ``periods`` the modelled finish in chunk
+    periods; the split path's: ``seams`` slots its launch reserves, the cuts
+    chosen on the device), the kernels a call launches and the device
+    workspace :func:`gdn_prefill` needs with it."""
 
     __slots__ = ("buf", "slices", "seams", "split_chunk", "periods", "workspace_bytes")
 
@@ -181,6 +183,12 @@ class Plan:
         if self.slices:
             return f"split{self.slices}"
         return f"fused+{self.seams}seams" if self.seams else "fused"
+
+    @property
+    def kernels(self) -> list:
+        ks = (["gdn_prefill_prep_kernel", "gdn_prefill_slice_kernel"] if self.slices
+              else ["gdn_prefill_chain_kernel"])
+        return ks + (["gdn_prefill_seam_kernel"] if self.seams else [])
 
 
 def _plan_for(cu_host: torch.Tensor, T: int, HQ: int, HV: int, seams: bool, fused: bool,
