@@ -1113,8 +1113,9 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 // A state piece issues all its loads before its first MFMA.  A tail piece
 // stages S_sp once, as bf16 MFMA A fragments in LDS; wave w then owns tokens
 // 16 w .. 16 w + 15 of each chunk across all 128 rows v (its OX rows read
-// once), and loads the next chunk's OX rows and outputs while it works on a
-// chunk.
+// once), passes its corrections through LDS so that the outputs are read
+// and written as whole rows, and loads the next chunk's OX rows and outputs
+// while it works on a chunk.
 constexpr int kSeamThreads = 256;
 constexpr int kSeamStatePieces = D / 16;
 constexpr int kSeamGroupChunks = 2;
@@ -1219,22 +1220,32 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
   const int che = min(n_all, chb + kSeamGroupChunks);
   const size_t v_stride = size_t(HV) * D;
   const uint16_t* OX = reinterpret_cast<const uint16_t*>(region + seam_ox_offset(k_slots, HV));
+  // Each wave's corrections of a chunk, fp32 [token 16][v 128] (rows padded
+  // to 132 floats: the 16-byte writes of 16 rows hit distinct banks), so the
+  // outputs are read and written as whole rows: lane l takes row 4 j + l / 16,
+  // 8 values from 8 (l % 16), j = 0..3.
+  constexpr int kDLD = D + 4;
+  __shared__ __align__(16) float sD[4][16 * kDLD];
+  float* dW = sD[wave];
   const int t = 16 * wave + c;                    // this lane's token of the chunk (B column)
-  // the token exists: inside the sequence and the OX region
-  auto valid = [&](int ch) { return t < min(C, len - ch * C) && ox_row0 + (ch - sp) * C + t < ox_rows; };
-  auto out_at = [&](int ch, int tm) {
-    return reinterpret_cast<uint2*>(out + size_t(bos + ch * C + t) * v_stride + size_t(hv) * D + 16 * tm + 4 * g);
+  const int q8 = 8 * (lane & 15);                 // this lane's 8 columns in the row-major passes
+  // the chunk's token tt exists: inside the sequence and the OX region
+  auto valid = [&](int ch, int tt) {
+    return tt < min(C, len - ch * C) && ox_row0 + (ch - sp) * C + tt < ox_rows;
   };
-  uint4 ob[2][4];
-  uint2 ov[2][8];
-  auto load = [&](int ch, uint4 (&obb)[4], uint2 (&ovb)[8]) {
+  auto out_row = [&](int ch, int j) {
+    return reinterpret_cast<uint4*>(out + size_t(bos + ch * C + 16 * wave + 4 * j + (lane >> 4)) * v_stride +
+                                    size_t(hv) * D + q8);
+  };
+  uint4 ob[2][4], ov[2][4];
+  auto load = [&](int ch, uint4 (&obb)[4], uint4 (&ovb)[4]) {
     const int orow = min(ox_row0 + (ch - sp) * C + t, ox_rows - 1);   // rows past the region are never used
 #pragma unroll
     for (int tk = 0; tk < 4; ++tk)
       obb[tk] = *reinterpret_cast<const uint4*>(&OX[size_t(orow) * v_stride + size_t(hv) * D + 32 * tk + 8 * g]);
-    const bool ok = valid(ch);
 #pragma unroll
-    for (int tm = 0; tm < 8; ++tm) ovb[tm] = ok ? *out_at(ch, tm) : uint2{0u, 0u};
+    for (int j = 0; j < 4; ++j)
+      ovb[j] = valid(ch, 16 * wave + 4 * j + (lane >> 4)) ? *out_row(ch, j) : uint4{0u, 0u, 0u, 0u};
   };
   if (chb < che) load(chb, ob[0], ov[0]);
   __syncthreads();
@@ -1243,20 +1254,34 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
     const int ch = chb + i;
     if (ch >= che) break;
     if (ch + 1 < che) load(ch + 1, ob[(i + 1) & 1], ov[(i + 1) & 1]);
-    const bool ok = valid(ch);
 #pragma unroll
     for (int tm = 0; tm < 8; ++tm) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int tk = 0; tk < 4; ++tk)
         acc = mfma16_bf(sA[(tm * 4 + tk) * 64 + lane], __builtin_bit_cast(bf16x8_t, ob[i & 1][tk]), acc);
-      if (ok) {
-        float f0, f1, f2, f3;
-        unpack_bf16x2(ov[i & 1][tm].x, f0, f1);
-        unpack_bf16x2(ov[i & 1][tm].y, f2, f3);
-        *out_at(ch, tm) = uint2{cvt_pk_bf16(f0 + acc[0], f1 + acc[1]), cvt_pk_bf16(f2 + acc[2], f3 + acc[3])};
+      // acc[e]: v = 16 tm + 4 g + e, token c of this wave's 16
+      *reinterpret_cast<f32x4*>(&dW[c * kDLD + 16 * tm + 4 * g]) = acc;
+    }
+    // the wave reads back what its lanes wrote (LDS keeps one wave's order)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * j + (lane >> 4);
+      if (valid(ch, 16 * wave + r)) {
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&dW[r * kDLD + q8]);
+        const f32x4 d1 = *reinterpret_cast<const f32x4*>(&dW[r * kDLD + q8 + 4]);
+        const uint4 o = ov[i & 1][j];
+        float f[8];
+        unpack_bf16x2(o.x, f[0], f[1]);
+        unpack_bf16x2(o.y, f[2], f[3]);
+        unpack_bf16x2(o.z, f[4], f[5]);
+        unpack_bf16x2(o.w, f[6], f[7]);
+        *out_row(ch, j) = uint4{cvt_pk_bf16(f[0] + d0[0], f[1] + d0[1]), cvt_pk_bf16(f[2] + d0[2], f[3] + d0[3]),
+                                cvt_pk_bf16(f[4] + d1[0], f[5] + d1[1]), cvt_pk_bf16(f[6] + d1[2], f[7] + d1[3])};
       }
     }
+    asm volatile("" ::: "memory");
   }
 }
 
