@@ -596,6 +596,16 @@ struct SliceCfg {
   static_assert(kNB % kFrRing == 0, "ring slot from the buffer set");
 };
 
+// V slot swizzle of row t in a slice's LDS V rows (VS 16-byte slots per row):
+// slot s holds piece s ^ vslot(t).  t mod VS, and at 32 rows (VS = 4) also
+// 2 ((t / 4) mod 2): a transposing read cycle serves 8 rows with 4 lanes on
+// 32 contiguous bytes (two slots) of each, and the rows t, t + 4 then take
+// distinct slot pairs.
+template <int VS>
+__device__ __forceinline__ int vslot(int t) {
+  return VS == 4 ? ((t & 3) ^ (((t >> 2) & 1) << 1)) : (t & (VS - 1));
+}
+
 //
 // kH: the output waves also write the state entering every chunk, bf16, to
 // hout[chunk_offset(n) + ch][hv][v][k] (slots at or past h_chunks skipped):
@@ -831,7 +841,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
           for (int tb = 0; tb < 4; ++tb) {
             const int t = 16 * tb + 4 * g + mm;
             const i16x4_t vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4_t*)&rv[b3][t * R + 8 * ((col >> 3) ^ (t & (VS - 1))) + (col & 7)]) &
+                (__attribute__((address_space(3))) i16x4_t*)&rv[b3][t * R + 8 * ((col >> 3) ^ vslot<VS>(t)) + (col & 7)]) &
                 i16x4_t{short(vmask), short(vmask), short(vmask), short(vmask)};
             const f32x4 eg = *reinterpret_cast<const f32x4*>(&gd[G_EG + 16 * tb + 4 * g]);
             const f32x4 bt = *reinterpret_cast<const f32x4*>(&gd[G_BETA + 16 * tb + 4 * g]);
@@ -1022,7 +1032,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 #pragma unroll
         for (int j = 0; j < VS; ++j) {
           const int row = Cfg::VRows * j + lane / VS;
-          v_off[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane % VS) ^ (row & (VS - 1))) * 16u;
+          v_off[j] = uint32_t(row) * uint32_t(v_stride * 2) + uint32_t((lane % VS) ^ vslot<VS>(row)) * 16u;
         }
       }
       auto issue_copies = [&](int jj) {
@@ -1060,7 +1070,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
 #pragma unroll
             for (int j = 0; j < VS; ++j) {
               const int row = Cfg::VRows * j + lane / VS;
-              const int src_piece = (lane % VS) ^ (row & (VS - 1));
+              const int src_piece = (lane % VS) ^ vslot<VS>(row);
               lds_dma16(v + size_t(t0 + min(row, L - 1)) * v_stride + size_t(hv) * D + vb + 8 * src_piece,
                         &rv[b3][Cfg::VRows * j * R]);
             }
