@@ -240,3 +240,21 @@ def test_plan_argument_errors():
     assert rc == 0 and p["seams"] >= 1 and p["workspace"] > 0
     assert lib.gdn_prefill_plan_fwd(*args, fused, None, 0, 0, None) == capi.GDN_ERR_WORKSPACE
     assert lib.gdn_prefill_plan_fwd(*args, fused, P, p["workspace"] - 1, 0, None) == capi.GDN_ERR_WORKSPACE
+
+
+def test_check_final_range_names_new_nonfinite_states():
+    """The prefill's range check (host logic over device-reduced flags, here
+    on CPU tensors): sequences whose final state holds inf or NaN are named,
+    unless their initial state already did."""
+    import torch
+    pre = pkg_module("prefill")
+    fs = torch.zeros(4, 2, 128, 128)
+    pre.check_final_range(fs)                       # all finite: no error
+    fs[1, 0, 3, 4] = float("inf")
+    fs[3, 1, 0, 0] = float("nan")
+    with pytest.raises(pre.RangeOverflowError, match=r"\[1, 3\]"):
+        pre.check_final_range(fs)
+    s0 = torch.zeros(4, 2, 128, 128)
+    s0[3, 0, 0, 0] = float("-inf")                  # sequence 3 started non-finite
+    with pytest.raises(pre.RangeOverflowError, match=r"\[1\]"):
+        pre.check_final_range(fs, s0)

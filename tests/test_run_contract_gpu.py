@@ -168,6 +168,35 @@ def test_prefill_large_magnitude_inputs(device, path):
     assert float((s.cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
 
 
+@pytest.mark.parametrize("path", ["fused", "split"])
+def test_prefill_range_overflow_is_reported(device, path):
+    """v of the second sequence ~ N(0, 1e5^2) puts X past the fp16 operand
+    range: with check_range=True the call raises RangeOverflowError naming
+    that sequence only; the in-range sequence keeps its oracle result, and
+    the in-range inputs of the test above pass the check."""
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    x = inp.prefill_inputs([200, 77], seed=508, with_state=True)
+    gen = torch.Generator().manual_seed(509)
+    x["v"][200:] = (torch.randn(x["v"][200:].shape, generator=gen) * 1e5).to(torch.bfloat16)
+    g = _to(x, device)
+    with pytest.raises(pre.RangeOverflowError, match=r"\[1\]"):
+        pre.gdn_prefill(*[g[n] for n in PNAMES], g["scale"], path=path, check_range=True)
+    o, s = pre.gdn_prefill(*[g[n] for n in PNAMES], g["scale"], path=path)
+    torch.cuda.synchronize()
+    assert not bool(torch.isfinite(s[1]).all())
+    x0 = {n: (x[n][:200] if n in ("q", "k", "v", "a", "b") else x[n]) for n in PNAMES}
+    x0["state"] = x["state"][:1]
+    x0["cu_seqlens"] = torch.tensor([0, 200], dtype=torch.int64)
+    o_ref, s_ref = O.prefill_recurrent(*[x0[n] for n in PNAMES], x["scale"])
+    torch.testing.assert_close(o[:200].float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    assert float((s[:1].cpu().double() - s_ref).norm() / s_ref.norm()) <= 1e-3
+    # in range: the check passes
+    y = inp.prefill_inputs([200, 77], seed=504, with_state=True)
+    gy = _to(y, device)
+    pre.gdn_prefill(*[gy[n] for n in PNAMES], gy["scale"], path=path, check_range=True)
+
+
 def test_decode_large_magnitude_inputs(device):
     dec = pkg_module("decode")
     inp = pkg_module("inputs")

@@ -226,7 +226,7 @@ def num_chunks(cu_seqlens: torch.Tensor, T: int) -> int:
 def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
                 output=None, final_state=None, workspace=None, validate: bool = True,
                 qk_l2norm: bool = False, h=None, path: str = "auto", slices: int = 8,
-                seams: bool = True):
+                seams: bool = True, check_range: bool = False):
     """Chunked GDN prefill over packed varlen sequences, any ``HV % HQ == 0``.
 
     ``q, k [T, HQ, 128]``, ``v [T, HV, 128]``, ``a, b [T, HV]`` bf16;
@@ -259,13 +259,39 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *,
     Input range: the state path multiplies fp16 operands, so k, v, the state
     and the intermediate X and Vn must stay below 65504 in magnitude (far
     above normalised q / k and states of ordinary size; the reference's bf16
-    intermediates reach 3e38).
+    intermediates reach 3e38).  A value past that range becomes infinite and
+    the state, once infinite or NaN, stays so to the final state:
+    ``check_range=True`` checks the final states on the device after the
+    launch (one reduction and one synchronisation) and raises
+    :class:`RangeOverflowError` naming the sequences whose final state is not
+    finite.
     """
     cu_host = validate_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, q.shape[1],
                               v.shape[1], check_total=validate)
-    return _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
+    o, s = _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=output,
                    final_state=final_state, workspace=workspace, qk_l2norm=qk_l2norm, h=h,
                    path=path, slices=slices, cu_host=cu_host, seams=seams)
+    if check_range:
+        check_final_range(s, state)
+    return o, s
+
+
+class RangeOverflowError(FloatingPointError):
+    """A prefill's state path left the fp16 range: some final state is not finite."""
+
+
+def check_final_range(final_state: torch.Tensor, state: Optional[torch.Tensor] = None) -> None:
+    """Raise :class:`RangeOverflowError` when a final state holds an infinite
+    or NaN value that its initial state did not (one device reduction per
+    tensor and one synchronisation)."""
+    bad = ~torch.isfinite(final_state).flatten(1).all(dim=1)
+    if state is not None:
+        bad &= torch.isfinite(state).flatten(1).all(dim=1)
+    idx = bad.nonzero().flatten().tolist()
+    if idx:
+        raise RangeOverflowError(
+            f"prefill state left the fp16 operand range (|x| > 65504) in sequence(s) {idx[:16]}"
+            + (" ..." if len(idx) > 16 else "") + "; scale k / v or the initial state down")
 
 
 def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, *, output=None,
