@@ -146,6 +146,33 @@ def test_decode_pool_matches_gather_step_scatter(device):
     assert torch.count_nonzero(out[3]) == 0
 
 
+def test_decode_pool_check_slots(device):
+    """check_slots=True: repeated in-pool slots raise ValueError before any
+    launch (the pool is unchanged); repeated out-of-pool slots (no state
+    access) and distinct slots pass, and the step matches the unchecked one."""
+    dec = pkg_module("decode")
+    inp = pkg_module("inputs")
+    B, P = 6, 16
+    x = inp.decode_inputs(B, seed=15)
+    g = _to(x, device)
+    pool = (torch.randn(P, 8, 128, 128, generator=torch.Generator().manual_seed(7)) * 0.02).to(device)
+    args = lambda slots: (g["q"], g["k"], g["v"], pool, slots, g["A_log"], g["a"], g["dt_bias"],
+                          g["b"], g["scale"])
+    bad = torch.tensor([3, 9, 3, 12, 9, 0], dtype=torch.int32, device=device)
+    before = pool.clone()
+    with pytest.raises(ValueError, match=r"\[3, 9\]"):
+        dec.decode_pool_(*args(bad), check_slots=True)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, before)
+    ok = torch.tensor([3, -1, 5, -1, P, 0], dtype=torch.int32, device=device)
+    o1 = dec.decode_pool_(*args(ok), check_slots=True)
+    p1 = pool.clone()
+    pool.copy_(before)
+    o2 = dec.decode_pool_(*args(ok))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(p1, pool)
+
+
 def test_decode_pool_full_size_b1024_qk16_v32(device):
     """Decode at batch 1024 against a [1024, 32, 128, 128] fp32 pool (2 GiB),
     slots a random permutation: equal bit for bit to gather -> dense decode ->

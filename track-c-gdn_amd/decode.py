@@ -192,12 +192,17 @@ def gdn_decode_multi(q, k, v, state, A_log, a, dt_bias, b, scale=None, *, output
 
 @torch.no_grad()
 def decode_pool_(q, k, v, state_pool, slot_ids, A_log, a, dt_bias, b, scale=None, *,
-                 output=None):
+                 output=None, check_slots: bool = False):
     """One decode step against ``state_pool[slot_ids[n]]``, updated in place.
 
-    ``state_pool [P, HV, 128, 128]`` fp32, ``slot_ids [B]`` int32 (distinct).
-    A slot outside ``[0, P)`` leaves the pool untouched and gives a zero
-    output row.  Returns ``output [B, 1, HV, 128]`` bf16.
+    ``state_pool [P, HV, 128, 128]`` fp32, ``slot_ids [B]`` int32 (distinct:
+    two sequences naming one slot would update it concurrently, with a
+    result that is not specified).  A slot outside ``[0, P)`` leaves the pool
+    untouched and gives a zero output row.  ``check_slots=True`` checks the
+    slots on the device before the launch (a sort and one synchronisation)
+    and raises ``ValueError`` naming repeated slots inside the pool (slots
+    outside it touch no state and may repeat), launching nothing.
+    Returns ``output [B, 1, HV, 128]`` bf16.
     """
     B, nq, nv = _check_common(q, k, v, A_log, a, dt_bias, b)
     scale = _resolve_scale(scale, q.shape[-1])
@@ -205,6 +210,13 @@ def decode_pool_(q, k, v, state_pool, slot_ids, A_log, a, dt_bias, b, scale=None
     assert state_pool.dim() == 4 and state_pool.shape[1:] == (nv, D, D)
     assert slot_ids.is_cuda and slot_ids.dtype == torch.int32 and slot_ids.numel() == B
     slot_ids = slot_ids.contiguous()
+    if check_slots and B > 1:
+        srt = torch.sort(slot_ids.flatten()).values
+        rep = (srt[1:] == srt[:-1]) & (srt[1:] >= 0) & (srt[1:] < state_pool.shape[0])
+        dup = srt[1:][rep].unique()
+        if dup.numel():
+            raise ValueError(f"slot_ids repeat slot(s) {dup[:16].tolist()}: each sequence "
+                             "needs its own slot")
     if output is None:
         output = torch.empty(B, 1, nv, D, dtype=q.dtype, device=q.device)
     A_log, dt_bias = _gates(A_log, dt_bias)
