@@ -56,6 +56,8 @@ CASES = [
     ([2500, 2300, 640, 1000, 130, 0, 900], 4, 8, True, False, False),   # two seams, an empty sequence
     ([1900, 450, 1700], 16, 32, True, False, False),            # qk16 / v32
     ([2222, 600], 4, 8, True, False, True),                     # L2-norm option
+    ([3000, 200, 1300], 1, 4, True, False, False),              # one qk-head, 4 v-heads
+    ([2700, 90, 2000, 640], 2, 8, False, True, False),          # two qk-heads, seam units across XCDs
 ]
 
 
