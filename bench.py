@@ -673,8 +673,7 @@ def main():
                 "workload": name, "tokens": r["T"], "sequences": r["N"], "qk_heads": r["HQ"],
                 "v_heads": r["HV"], "kernel_us": round(kus, 2),
                 "tokens_per_s": round(r["T"] / (r["kernel_ms"] * 1e-3), 1),
-                "kernels": ["gdn_bwd_prep_kernel", "gdn_bwd_chain_kernel", "gdn_bwd_grad_kernel",
-                            "gdn_bwd_head_sum_kernel"],
+                "kernels": ["gdn_bwd_prep_kernel", "gdn_bwd_chain_kernel", "gdn_bwd_grad_kernel"],
                 "roofline": {"bound": "mfma", "achieved": round(tfl, 2),
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4),

@@ -24,8 +24,8 @@
 //     quarter of its state rows when the chains are few: walks the chunks
 //     from last to first with dS^T in MFMA accumulators, storing dSn of
 //     every chunk (bf16) and the gradient of the initial state.
-//  3. gdn_bwd_grad_kernel, one workgroup per (chunk, v-head): with S and dSn
-//     known, every gradient of the chunk:
+//  3. gdn_bwd_grad_kernel, one workgroup per (chunk, qk-head), its v-heads
+//     in turn: with S and dSn known, every gradient of the chunk:
 //        dVn = P^T dO + Dc K dSn^T,  dX = Tm^T dVn,  dV = beta dX,
 //        dP = dO Vn^T,  dTm = dVn X^T,  dA = -Tm^T dTm Tm^T (strictly lower),
 //        dQ = scale E dO S + dPm K,
@@ -36,8 +36,8 @@
 //                (+ sum_i Dc rowsum(Vn K dSn^T) + e^{gam_L} <dSn, S> at gam_L),
 //        dg = reverse cumsum of dgam within the chunk,
 //     with dPm = scale e^{gam_i-gam_j} dP (j <= i), dAb = beta_i e^{gam_i-gam_j} dA.
-//     dq / dk of the v-heads that share a qk-head are summed by a last
-//     elementwise kernel.
+//     dq / dk of the v-heads that share a qk-head are summed in registers,
+//     in v-head order, and stored once.
 //
 // All products run on MFMA 16x16x32 bf16 with fp32 accumulation; the matrix
 // operands live in LDS as bf16 rows of the form [m][r] and are read either
@@ -595,8 +595,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
     float scale, const uint16_t* __restrict__ d_out, const uint16_t* __restrict__ h, int h_chunks,
     const uint16_t* __restrict__ dh, float* __restrict__ dq, float* __restrict__ dk,
     float* __restrict__ dv, float* __restrict__ dg, float* __restrict__ dbeta) {
-  __shared__ __align__(16) uint16_t sK[kCB];
-  __shared__ __align__(16) uint16_t sQ[kCB];
+  __shared__ __align__(16) uint16_t sK_rows[kCB];
+  __shared__ __align__(16) uint16_t sQ_rows[kCB];
   __shared__ __align__(16) uint16_t sdO[kCB];
   __shared__ __align__(16) uint16_t sVn[kCB];
   __shared__ __align__(16) uint16_t sX[kCB];      // V; X; then -beta E dX
@@ -610,10 +610,13 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   uint16_t* sdV = sS;
   float* sAr = reinterpret_cast<float*>(sS + kCB);
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g4 = lane >> 4, c16 = lane & 15;
-  const int slot = blockIdx.x, hv = blockIdx.y;
+  int g4 = lane >> 4, c16 = lane & 15;
+  // One (chunk, qk-head) per workgroup: its G v-heads in turn, dq and dk
+  // summed over them in registers (v-head order) and stored once.
+  const int slot = blockIdx.x, hq = blockIdx.y;
+  const int G = HV / HQ;
   if (slot >= h_chunks) return;
   int n, ci;
   locate_chunk(cu, N, T, slot, lane, n, ci);
@@ -622,22 +625,39 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   seq_bounds(cu, n, T, bos, slen);
   const int t0 = bos + C * ci;
   const int len = min(C, slen - C * ci);
-  const int hq = hv / (HV / HQ);
+  uint4 wk[2], wq[2];
+  rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+  rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+  rows_store(sK_rows, wk, tid);
+  rows_store(sQ_rows, wq, tid);
+  const int tb = wave & 3, d0 = 4 * (wave >> 2);
+  const int ib = wave >> 1, j0 = 2 * (wave & 1);
+  f32x4 dq_acc[4], dk_acc[4];     // this wave's dq / dk tiles, summed over the v-heads
+
+  for (int m = 0; m < G; ++m) {
+  // K and Q rows stay in LDS across the v-heads; an offset the compiler
+  // cannot see through (zero) keeps their reads inside the iteration, where
+  // the registers are, instead of hoisted out of the loop.
+  int lds0 = 0;
+  asm volatile("" : "+s"(lds0));
+  uint16_t* sK = sK_rows + lds0;
+  uint16_t* sQ = sQ_rows + lds0;
+  // likewise the lane indices: their address arithmetic is formed where it is used
+  asm volatile("" : "+v"(tid), "+v"(lane), "+v"(g4), "+v"(c16));
+  const int hv = hq * G + m;
   const size_t rec = (size_t(slot) * HV + hv) * D * D;
   const uint16_t* Sg = h + rec;
   const uint16_t* dSg = dh + rec;
 
   GateIn gi{};
   if (wave == 0) gi = gate_inputs(A_log, a, dt_bias, b, HV, hv, t0, len, lane);
-  uint4 wk[2], wq[2], wo[2], wv[2];
-  rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
-  rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
+  uint4 wo[2], wv[2];
   rows_fetch(wo, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
   rows_fetch(wv, v + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
+  // the previous v-head's last reads of these buffers are behind the barrier
+  // that ends its iteration
   for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
   for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
-  rows_store(sK, wk, tid);
-  rows_store(sQ, wq, tid);
   rows_store(sdO, wo, tid);
   rows_store(sX, wv, tid);
   if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
@@ -646,8 +666,6 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
   ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
   lds_barrier();
 
-  const int tb = wave & 3, d0 = 4 * (wave >> 2);
-  const int ib = wave >> 1, j0 = 2 * (wave & 1);
   f32x4 eks[4], xr[4], kds[4];
   // the inverse's fp32 blocks over sVn, its staging over sY (both unused until later)
   if (wave == 0) unit_lower_inverse(sAr, gb, reinterpret_cast<float*>(sVn), reinterpret_cast<float*>(sY), sTm, lane);
@@ -840,11 +858,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
 #pragma unroll
     for (int s = 0; s < C / 32; ++s)
       y = mfma16_bf(op_mr(sTm, LDC, 16 * tb, 32 * s, lane), op_rm(sK, LDK, 16 * kb, 32 * s, lane), y);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * tb + 4 * g4 + i;
-      if (row < len) dq[(size_t(t0 + row) * HV + hv) * D + 16 * kb + c16] = y[i];
-    }
+    if (m == 0) dq_acc[u] = y;
+    else dq_acc[u] += y;
     f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < D / 32; ++s)
@@ -891,11 +906,11 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
 #pragma unroll
     for (int s = 0; s < D / 32; ++s)
       x = mfma16_bf(op_mr(sVn, LDK, 16 * tb, 32 * s, lane), op_rm(sS, LDK, 16 * kb, 32 * s, lane), x);
+    f32x4 z;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * tb + 4 * g4 + i;
-      if (row < len) dk[(size_t(t0 + row) * HV + hv) * D + 16 * kb + c16] = fmaf(gb[GB_DC + row], x[i], dkp[u][i]);
-    }
+    for (int i = 0; i < 4; ++i) z[i] = fmaf(gb[GB_DC + 16 * tb + 4 * g4 + i], x[i], dkp[u][i]);
+    if (m == 0) dk_acc[u] = z;
+    else dk_acc[u] += z;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -930,21 +945,20 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_grad_kernel(
       dbeta[size_t(t0 + t) * HV + hv] = dbt;
     }
   }
-}
+  lds_barrier();    // the next v-head rewrites every buffer but sK, sQ
+  }
 
-// dq / dk of the v-heads sharing a qk-head: out[t][hq] = sum_m ws[t][hq G + m].
-// Grid (ceil(HQ * 32 / 256), T): thread x of row t takes float4 x of out[t].
-__global__ __launch_bounds__(256) void gdn_bwd_head_sum_kernel(const float* __restrict__ ws,
-                                                               float* __restrict__ out, int T, int HQ,
-                                                               int G) {
-  const int x = blockIdx.x * 256 + threadIdx.x;
-  if (x >= HQ * (D / 4)) return;
-  const int hq = x / (D / 4), d4 = x - hq * (D / 4);
-  const size_t t = blockIdx.y;
-  const f32x4* src = reinterpret_cast<const f32x4*>(ws) + (t * HQ + hq) * G * (D / 4) + d4;
-  f32x4 acc = src[0];
-  for (int m = 1; m < G; ++m) acc += src[m * (D / 4)];
-  reinterpret_cast<f32x4*>(out)[t * HQ * (D / 4) + x] = acc;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * tb + 4 * g4 + i;
+      if (row < len) {
+        const size_t at = (size_t(t0 + row) * HQ + hq) * D + 16 * (d0 + u) + c16;
+        dq[at] = dq_acc[u][i];
+        dk[at] = dk_acc[u][i];
+      }
+    }
 }
 
 // Gradients of the gating, per v-head (one workgroup each):
@@ -1002,9 +1016,6 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
   char* mrec = ws;
   char* rrec = mrec + slots * HV * kMBytes;
   uint16_t* dhr = reinterpret_cast<uint16_t*>(rrec + slots * HV * kRBytes);
-  float* dq_ws = reinterpret_cast<float*>(reinterpret_cast<char*>(dhr) + slots * HV * kHBytes);
-  float* dk_ws = dq_ws + size_t(T) * HV * D;
-  const int G = HV / HQ;
   const dim3 cgrid{unsigned(slots), unsigned(HV), 1u};
   hipLaunchKernelGGL((gdn_bwd_prep_kernel<CuT>), cgrid, dim3(kGradThreads), 0, st, q, k, A_log, a,
                      dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h_chunks, mrec, rrec);
@@ -1019,14 +1030,10 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
     hipLaunchKernelGGL((gdn_bwd_chain_kernel<CuT, 8>), dim3(chain_ids), dim3(512), 0, st, cu, N, T, HV,
                        h_chunks, mrec, rrec, d_ht, dhr, dh0);
   if (T > 0) {
-    hipLaunchKernelGGL((gdn_bwd_grad_kernel<CuT>), cgrid, dim3(kGradThreads), 0, st, q, k, v, A_log, a,
-                       dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h, h_chunks, dhr,
-                       G > 1 ? dq_ws : dq, G > 1 ? dk_ws : dk, dv, dg, dbeta);
-    if (G > 1) {
-      const dim3 sgrid{unsigned((HQ * (D / 4) + 255) / 256), unsigned(T), 1u};
-      hipLaunchKernelGGL(gdn_bwd_head_sum_kernel, sgrid, dim3(256), 0, st, dq_ws, dq, T, HQ, G);
-      hipLaunchKernelGGL(gdn_bwd_head_sum_kernel, sgrid, dim3(256), 0, st, dk_ws, dk, T, HQ, G);
-    }
+    // one workgroup per (chunk, qk-head), its v-heads in turn
+    const dim3 qgrid{unsigned(slots), unsigned(HQ), 1u};
+    hipLaunchKernelGGL((gdn_bwd_grad_kernel<CuT>), qgrid, dim3(kGradThreads), 0, st, q, k, v, A_log, a,
+                       dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h, h_chunks, dhr, dq, dk, dv, dg, dbeta);
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GDN_OK : -int(e);
@@ -1037,9 +1044,7 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
 extern "C" size_t gdn_prefill_bwd_workspace_bytes(int N, int T, int HQ, int HV) {
   if (N < 0 || T < 0 || HQ <= 0 || HV <= 0 || HV % HQ != 0) return 0;
   const size_t slots = size_t(T) / C + size_t(N);
-  size_t bytes = slots * size_t(HV) * (kMBytes + kRBytes + kHBytes);
-  if (HV != HQ) bytes += 2 * size_t(T) * HV * D * sizeof(float);
-  return bytes;
+  return slots * size_t(HV) * (kMBytes + kRBytes + kHBytes);
 }
 
 extern "C" int gdn_prefill_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
