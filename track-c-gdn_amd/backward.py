@@ -36,8 +36,7 @@ HEAD_SIZE = 128
 def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
     """Device workspace of :func:`gdn_prefill_backward`: per chunk slot and
     v-head the chunk's state-gradient transition (32 KiB bf16 + 64 KiB fp32)
-    and the gradient of the state leaving it (32 KiB bf16), plus per-v-head
-    dq / dk when v-heads share qk-heads."""
+    and the gradient of the state leaving it (32 KiB bf16)."""
     return int(_capi.lib().gdn_prefill_bwd_workspace_bytes(N, T, HQ, HV))
 
 
