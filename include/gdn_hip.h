@@ -364,8 +364,7 @@ int gdn_prefill_split_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t
  *
  * Device workspace bytes of gdn_prefill_bwd: per (64-token chunk slot,
  * v-head) 128 KiB (the chunk's state-gradient transition and the gradient of
- * the state leaving it), plus 2 T HV 512 B when HV > HQ.  0 for invalid
- * sizes.
+ * the state leaving it).  0 for invalid sizes.
  */
 size_t gdn_prefill_bwd_workspace_bytes(int N, int T, int HQ, int HV);
 
