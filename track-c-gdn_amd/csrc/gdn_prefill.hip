@@ -1286,18 +1286,26 @@ constexpr int kFusedSeamMinChunks = 8;    // shortest chain a fused seam cuts
 
 // Finish time of workgroups that each hold one CU for `chunks * period`
 // cycles, started in the given order as CUs free up, `per_seq` workgroups
-// per sequence.
+// per sequence.  The workgroups of one sequence last equally long, so the
+// CUs are tracked as groups that free at the same time (sorted by time).
 double makespan(const std::vector<int>& chunks, int per_seq, double period, int cus) {
-  std::priority_queue<double, std::vector<double>, std::greater<double>> cu_free;
-  for (int i = 0; i < cus; ++i) cu_free.push(0.0);
+  std::vector<std::pair<double, long long>> free_at{{0.0, (long long)cus}};
   double end = 0.0;
-  for (int n : chunks)
-    for (int j = 0; j < per_seq; ++j) {
-      const double t = cu_free.top() + n * period;
-      cu_free.pop();
-      cu_free.push(t);
+  for (int n : chunks) {
+    const double d = n * period;
+    long long need = per_seq;
+    while (need > 0 && !free_at.empty()) {
+      const double t = free_at.front().first + d;
+      const long long c = std::min(free_at.front().second, need);
+      free_at.front().second -= c;
+      if (free_at.front().second == 0) free_at.erase(free_at.begin());
+      need -= c;
       end = std::max(end, t);
+      auto it = std::lower_bound(free_at.begin(), free_at.end(), std::make_pair(t, 0LL));
+      if (it != free_at.end() && it->first == t) it->second += c;
+      else free_at.insert(it, {t, c});
     }
+  }
   return end;
 }
 
@@ -1335,10 +1343,13 @@ FusedPlan plan_fused_seams(const CuT* cu, int N, int T, int HV, int cus, bool al
     L[m] = (lm + C - 1) / C;
     order[m] = m;
   }
-  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return L[x] > L[y]; });
-  p.periods = N > 0 ? L[order[0]] : 0;
   const long long chains = (long long)N * HV;
-  if (!allow || N == 0 || cus <= 0 || chains >= cus) return p;
+  if (!allow || N == 0 || cus <= 0 || chains >= cus) {
+    p.periods = N > 0 ? *std::max_element(L.begin(), L.end()) : 0;
+    return p;
+  }
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return L[x] > L[y]; });
+  p.periods = L[order[0]];
   const int room = int(std::min<long long>({(cus - chains) / (2LL * HV), (long long)N, (long long)kMaxSeams}));
   const int L0 = L[order[0]];
   double best = double(L0) * kFusedChunkCycles;
