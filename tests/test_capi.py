@@ -258,3 +258,40 @@ def test_check_final_range_names_new_nonfinite_states():
     s0[3, 0, 0, 0] = float("-inf")                  # sequence 3 started non-finite
     with pytest.raises(pre.RangeOverflowError, match=r"\[1\]"):
         pre.check_final_range(fs, s0)
+
+
+def test_plan_fwd_checks_the_plan_against_itself():
+    """A plan whose seam entries disagree with the region it sizes (OX rows
+    out of order, a sequence cut twice, a short row count) is refused before
+    any launch.  Offsets are those of the library's plan layout: seam count
+    at byte 28, then 8-int arrays seq, sp, bos, len, ox_row from byte 32,
+    ox_rows at 192 (layout 1)."""
+    import struct
+    capi = pkg_module("_capi")
+    lib = capi.lib()
+    P = 0x1000  # never dereferenced: the checks fail first
+    lens = [2500, 2300, 640, 1000]
+    rc, plan, p = _plan(lens, 4, 8, flags=capi.GDN_PLAN_FUSED)
+    assert rc == 0 and p["seams"] == 2
+    T = sum(lens)
+    args = [P] * 9 + [0, len(lens), T, 4, 8, 1.0, P, P]
+    raw = bytearray(plan.raw)
+    count, = struct.unpack_from("<i", raw, 28)
+    assert count == 2
+    seq = struct.unpack_from("<8i", raw, 32)
+    ox_row = struct.unpack_from("<8i", raw, 160)
+    assert sorted(seq[:2]) == [0, 1] and ox_row[0] == 0 and ox_row[1] > 0
+
+    def call(buf):
+        b = ctypes.create_string_buffer(bytes(buf), capi.GDN_PREFILL_PLAN_BYTES)
+        return lib.gdn_prefill_plan_fwd(*args, b, P, 1 << 40, 0, None)
+
+    bad = bytearray(raw)
+    struct.pack_into("<i", bad, 160 + 4, ox_row[1] + 64)          # seam 1's OX rows moved
+    assert call(bad) == capi.GDN_ERR_SHAPE
+    bad = bytearray(raw)
+    struct.pack_into("<i", bad, 32 + 4, seq[0])                   # one sequence cut twice
+    assert call(bad) == capi.GDN_ERR_SHAPE
+    bad = bytearray(raw)
+    struct.pack_into("<i", bad, 192, struct.unpack_from("<i", raw, 192)[0] - 1)   # region one row short
+    assert call(bad) == capi.GDN_ERR_SHAPE

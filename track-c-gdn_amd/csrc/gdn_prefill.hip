@@ -1525,13 +1525,23 @@ extern "C" int gdn_prefill_plan_fwd(const uint16_t* q, const uint16_t* k, const 
   if (p.fused.count > 0 && !(flags & GDN_NO_SEAMS)) {
     const size_t need = seam_region_bytes(p.fused.count, HV, p.fused.ox_rows);
     if (workspace == nullptr || workspace_bytes < need) return GDN_ERR_WORKSPACE;
-    // a plan made for other lengths could place tails past T
-    for (int j = 0; j < p.fused.count; ++j) {
-      const FusedPlan& f = p.fused;
+    // A plan is checked against itself before it sizes any write: every
+    // tail inside [0, T), the OX rows of seam j at the running sum of the
+    // tails before it and the region sized for all of them, the seam pass's
+    // pieces covering the longest tail, no sequence cut twice.
+    const FusedPlan& f = p.fused;
+    long long rows = 0;
+    int max_tail = 0;
+    for (int j = 0; j < f.count; ++j) {
       if (f.seq[j] < 0 || f.seq[j] >= N || f.bos[j] < 0 || f.len[j] < 0 || (long long)f.bos[j] + f.len[j] > T ||
-          f.sp[j] < 1 || C * (long long)f.sp[j] >= f.len[j])
+          f.sp[j] < 1 || C * (long long)f.sp[j] >= f.len[j] || f.ox_row[j] != rows)
         return GDN_ERR_SHAPE;
+      for (int i = 0; i < j; ++i)
+        if (f.seq[i] == f.seq[j]) return GDN_ERR_SHAPE;
+      rows += f.len[j] - (long long)C * f.sp[j];
+      max_tail = std::max(max_tail, (f.len[j] + C - 1) / C - f.sp[j]);
     }
+    if (rows != f.ox_rows || max_tail != f.max_tail) return GDN_ERR_SHAPE;
     seams.count = p.fused.count;
     for (int j = 0; j < seams.count; ++j) {
       seams.seq[j] = p.fused.seq[j];
