@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kThreadsPerHead, 8) void gdn_decode_multi_kernel(
       *reinterpret_cast<f32x4*>(&tk[t][which][8 * chunk]) = f32x4{x[0], x[1], x[2], x[3]};
       *reinterpret_cast<f32x4*>(&tk[t][which][8 * chunk + 4]) = f32x4{x[4], x[5], x[6], x[7]};
     }
-    if (threadIdx.x < nt) {      // gates (reference DEC:59-65)
+    if (int(threadIdx.x) < nt) {      // gates (reference DEC:59-65)
       const int t = threadIdx.x;
       const size_t tok = size_t(n) * T + t0 + t;
       tab[t][0] = expf(-a_log_exp * softplus_thresh20(bf16_bits_to_f32(a[tok * HV + hv]) + dtb));

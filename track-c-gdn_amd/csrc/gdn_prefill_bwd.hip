@@ -99,13 +99,6 @@ __device__ __forceinline__ void st_tile(uint16_t* base, int ld, int r0, int c0, 
   for (int i = 0; i < 4; ++i) p[i * ld] = f32_to_bf16_bits(x[i]);
 }
 
-__device__ __forceinline__ void st_tile_t(uint16_t* base, int ld, int r0, int c0, const f32x4& x, int lane) {
-  uint2 w;
-  w.x = pack_bf16x2(x[0], x[1]);
-  w.y = pack_bf16x2(x[2], x[3]);
-  *reinterpret_cast<uint2*>(base + (c0 + (lane & 15)) * ld + r0 + 4 * (lane >> 4)) = w;
-}
-
 // Sum over the 4 lane groups (same lane % 16) of a wave.
 __device__ __forceinline__ float group4_sum(float x) {
   x += __shfl_xor(x, 16);

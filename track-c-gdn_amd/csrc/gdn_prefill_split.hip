@@ -50,7 +50,6 @@ constexpr int BL_G = 12 * kFrag;       // gate data, GSZ floats (layout of the G
 constexpr int BL_N = BL_G + 4 * GSZ;   // GDN_QK_L2NORM: row factors of K (64 floats), then of Q
 constexpr int kBlob = BL_N + 4 * 2 * C;
 static_assert(kBlob % 256 == 0, "records stay 256-byte aligned");
-constexpr int kBlobCopies = (kBlob + kFrag - 1) / kFrag;   // 1 KB copy instructions per record
 // fp16 K rows of one (chunk, qk-head) as the chain reads them in LDS: [t][p32(k)]
 // with KCLD-element rows (the padding is never read), rows past the chunk end 0.
 constexpr int kKcBytes = C * KCLD * 2;
@@ -287,7 +286,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prefill_prep_kernel(
   fetch(cur);
   for (;;) {
   const int slot = cur.slot, hv = cur.hv;
-  const int t0 = cur.t0, L = cur.L;
+  const int L = cur.L;
   const int hq = hv / heads_per_qk;
   char* rec = blob + (size_t(slot) * HV + hv) * kBlob;
 
