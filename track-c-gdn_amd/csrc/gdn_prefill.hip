@@ -633,27 +633,18 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         for (int kb = 0; kb < 8; ++kb)
           Sacc[u][kb] = *reinterpret_cast<const f32x4*>(src + size_t(16 * u) * D + 16 * kb + 4 * g);
     }
-    // kH: the bf16 fragments sb[u] of column block p of the state entering chunk
-    // ch go to its h slot.  Lane (g, c) holds row v0 + 16 u + c, 4-column
-    // pieces g and g + 4 of the block (columns 32 p + 4 g .., 32 p + 16 + 4 g ..).
-    // v_permlane16_swap trades the odd 16-lane rows' first piece for the even
-    // rows' second piece, which leaves every lane two adjacent pieces: pieces
-    // g, g + 1 (g even) or g + 3, g + 4 (g odd), 16 contiguous bytes, so one
-    // 16-byte store per lane writes the block's 64 bytes of each of 16 rows.
-    const uint32_t h_lane = uint32_t(vrow * D + ((g & 1) ? 4 * (g + 3) : 4 * g)) * 2u;
-    auto store_h = [&](int ch, int p, const bf16x8_t (&sb)[kTiles]) {
+    // kH: the bf16 fragments of column blocks 2 pp and 2 pp + 1 (s0, s1) of
+    // the state entering chunk ch go to its h slot as whole 128-byte lines
+    // (store_state_lines; lane (g, c) of tile u holds row v0 + 16 u + c).
+    const uint32_t h_lane = state_lines_lane(g, c);
+    auto store_h = [&](int ch, int pp, const bf16x8_t (&s0)[kTiles], const bf16x8_t (&s1)[kTiles]) {
       if constexpr (kH) {
         const int slot = h_base + ch;
         if (slot < h_chunks) {
-          char* base = reinterpret_cast<char*>(hout) + (size_t(slot) * HV + hv) * size_t(D * D * 2);
+          char* base = reinterpret_cast<char*>(hout) + (size_t(slot) * HV + hv) * size_t(D * D * 2) +
+                       size_t(v0) * (D * 2) + 128 * pp;
 #pragma unroll
-          for (int u = 0; u < kTiles; ++u) {
-            const u32x4_t w = __builtin_bit_cast(u32x4_t, sb[u]);
-            const auto lo = __builtin_amdgcn_permlane16_swap(w[0], w[2], false, false);
-            const auto hi = __builtin_amdgcn_permlane16_swap(w[1], w[3], false, false);
-            store_b128_saddr(base + u * (16 * D * 2), h_lane + uint32_t(64 * p),
-                             u32x4_t{lo[0], hi[0], lo[1], hi[1]});
-          }
+          for (int u = 0; u < kTiles; ++u) store_state_lines(base + u * (16 * D * 2), h_lane, c, s0[u], s1[u]);
         }
       }
     };
@@ -863,6 +854,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
       {
         // Column blocks 0, 1 of S Q^T here, blocks 2, 3 in P3a (their Q fragments
         // read here, before other chain waves stage outputs in the raw Q buffer)
+        bf16x8_t sbh[kTiles];     // kH: block 0's fragments, stored with block 1's
 #pragma unroll
         for (int p = 0; p < 2; ++p) {     // the 8 products of block p, then the reads of block p + 2
           bf16x8_t sb[kTiles];
@@ -874,7 +866,12 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
             for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16_bf(sb[u], qf[p & 1][tb], OT[u][tb]);
           }
-          store_h(ch, p, sb);
+          if (p == 0) {
+#pragma unroll
+            for (int u = 0; u < kTiles; ++u) sbh[u] = sb[u];
+          } else {
+            store_h(ch, 0, sbh, sb);
+          }
           load_qf(p + 2, qf[p & 1]);
         }
         asm volatile("" ::: "memory");
@@ -893,6 +890,7 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         if (half == 0) {
+          bf16x8_t sbh[kTiles];   // kH: block 2's fragments, stored with block 3's
 #pragma unroll
           for (int p = 2; p < 4; ++p) {   // the rest of S Q^T (S before this chunk's update)
             bf16x8_t sb[kTiles];
@@ -904,7 +902,12 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
 #pragma unroll
               for (int u = 0; u < kTiles; ++u) OT[u][tb] = mfma16_bf(sb[u], qf[p & 1][tb], OT[u][tb]);
             }
-            store_h(ch, p, sb);
+            if (p == 2) {
+#pragma unroll
+              for (int u = 0; u < kTiles; ++u) sbh[u] = sb[u];
+            } else {
+              store_h(ch, 1, sbh, sb);
+            }
           }
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {

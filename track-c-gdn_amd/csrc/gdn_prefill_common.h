@@ -203,6 +203,47 @@ __device__ __forceinline__ void buffer_store_b64(__amdgpu_buffer_rsrc_t r, uint3
   __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, r, int(off), 0, 0);
 }
 
+// The bf16 image of a 16-row tile of the state to a row-major [16][128]
+// bf16 destination (an h slot), column blocks 2 pp and 2 pp + 1 (s0, s1)
+// at a time, as whole 128-byte lines.  Lane (g, c) holds row c of the tile,
+// 4-column pieces g and g + 4 of each block (the S^T accumulator layout
+// packed to bf16).  v_permlane16_swap trades the odd 16-lane rows' first
+// piece for the even rows' second, which leaves every lane two adjacent
+// pieces of each block (16 contiguous bytes: x of block 2 pp, y of block
+// 2 pp + 1): pieces g, g + 1 (g even) or g + 3, g + 4 (g odd).  A DPP
+// rotation by 8 within each 16-lane row gives lane c the x and y of lane
+// c ^ 8, so the first store writes rows c % 8 (x on lanes c < 8, the y of
+// row c - 8 on the others) and the second rows c % 8 + 8: 8 whole lines
+// each, where one store per block would write 16 half lines.  (Used by the
+// fused chain kernel, where all 256 CUs write h at once.)
+// `tile` points at the tile's row 0, column 64 pp; lane_off is
+// state_lines_lane(g, c).
+__device__ __forceinline__ uint32_t state_lines_lane(int g, int c) {
+  return uint32_t((c & 7) * 128 + ((g & 1) ? 4 * (g + 3) : 4 * g)) * 2u + ((c & 8) ? 64u : 0u);
+}
+__device__ __forceinline__ void store_state_lines(char* tile, uint32_t lane_off, int c, bf16x8_t s0,
+                                                  bf16x8_t s1) {
+  const u32x4_t w0 = __builtin_bit_cast(u32x4_t, s0);
+  const u32x4_t w1 = __builtin_bit_cast(u32x4_t, s1);
+  const auto a0 = __builtin_amdgcn_permlane16_swap(w0[0], w0[2], false, false);
+  const auto a1 = __builtin_amdgcn_permlane16_swap(w0[1], w0[3], false, false);
+  const auto b0 = __builtin_amdgcn_permlane16_swap(w1[0], w1[2], false, false);
+  const auto b1 = __builtin_amdgcn_permlane16_swap(w1[1], w1[3], false, false);
+  const uint32_t x[4] = {a0[0], a1[0], a0[1], a1[1]};
+  const uint32_t y[4] = {b0[0], b1[0], b0[1], b1[1]};
+  const bool low = (c & 8) == 0;
+  u32x4_t d1, d2;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t rx = __builtin_amdgcn_update_dpp(0u, x[e], 0x128, 0xf, 0xf, false);   // row_ror:8
+    const uint32_t ry = __builtin_amdgcn_update_dpp(0u, y[e], 0x128, 0xf, 0xf, false);
+    d1[e] = low ? x[e] : ry;
+    d2[e] = low ? rx : y[e];
+  }
+  store_b128_saddr(tile, lane_off, d1);
+  store_b128_saddr(tile, lane_off + 8u * 128u * 2u, d2);
+}
+
 // Tokens [bos, bos + len) of sequence n, clamped into [0, T].
 template <typename CuT>
 __host__ __device__ __forceinline__ void seq_bounds(const CuT* cu, int n, int T, int& bos, int& len) {

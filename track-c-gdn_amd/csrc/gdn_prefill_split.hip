@@ -911,6 +911,9 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
             // first piece for the even rows' second, which leaves 16
             // contiguous bytes per lane (pieces g, g + 1 for even g, g + 3,
             // g + 4 for odd g): one 16-byte store covers 16 rows x 64 bytes.
+            // (Whole lines two blocks at a time, store_state_lines, are
+            // slower here: the extra lane exchange sits on this wave's path,
+            // and at few chains the half lines cost little in HBM.)
             if (coff + ch < h_chunks) {
               char* hb = reinterpret_cast<char*>(hout) + (size_t(coff + ch) * HV + hv) * size_t(D * D * 2);
               const u32x4_t w = __builtin_bit_cast(u32x4_t, sbf);
