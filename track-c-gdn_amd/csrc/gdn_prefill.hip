@@ -953,15 +953,21 @@ __global__ __launch_bounds__(kThreads, 1) void gdn_prefill_chain_kernel(
         if (half == 1) {
           // Rows kOutRows w .. kOutRows (w + 1) - 1 of the staged output tile
           // (w = this chain wave), 4 rows per instruction, to HBM as whole
-          // 256-byte rows.
+          // 256-byte rows.  All reads first, then the stores: one LDS round
+          // trip instead of one per store.
           constexpr int kOutRows = C / kChainWaves;
           const size_t row_bytes = v_stride * sizeof(uint16_t);
           char* obase = reinterpret_cast<char*>(out_rows + size_t(out_row0 + ch * C) * v_stride + size_t(hv) * D);
+          u32x4_t od[kOutRows / 4];
 #pragma unroll
           for (int q4 = 0; q4 < kOutRows / 4; ++q4) {
             const int row = kOutRows * (v0 / kRowsPerWave) + 4 * q4 + (lane >> 4);
-            const u32x4_t d = *reinterpret_cast<const u32x4_t*>(&raw.q[kb_buf][raw_off(row, 8 * c)]);
-            if (L == C || row < L) store_b128_saddr(obase, uint32_t(row) * uint32_t(row_bytes) + uint32_t(16 * c), d);
+            od[q4] = *reinterpret_cast<const u32x4_t*>(&raw.q[kb_buf][raw_off(row, 8 * c)]);
+          }
+#pragma unroll
+          for (int q4 = 0; q4 < kOutRows / 4; ++q4) {
+            const int row = kOutRows * (v0 / kRowsPerWave) + 4 * q4 + (lane >> 4);
+            if (L == C || row < L) store_b128_saddr(obase, uint32_t(row) * uint32_t(row_bytes) + uint32_t(16 * c), od[q4]);
           }
         }
         // K^T fragments of the next k-block pair are read before the products of
