@@ -258,7 +258,7 @@ BWD_MFMA_PER_CHUNK_HEAD = 656 + 256 + 1360
 
 def bench_backward(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     """Backward of the prefill (gdn_prefill_bwd: transition, reverse chain,
-    per-chunk gradients, head sums) from the forward's h, one C call per step."""
+    per-chunk gradients) from the forward's h, one C call per step."""
     w = ginp.WORKLOADS[name]
     lens = ginp.workload_lengths(name)
     x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"])

@@ -363,7 +363,7 @@ int gdn_prefill_split_h_fwd(const uint16_t* q, const uint16_t* k, const uint16_t
  * produces, kernel.py:1153-1160, here gdn_prefill_h_fwd).
  *
  * Device workspace bytes of gdn_prefill_bwd: per (64-token chunk slot,
- * v-head) 128 KiB (the chunk's state-gradient transition and the gradient of
+ * v-head) 96 KiB (the chunk's state-gradient transition and the gradient of
  * the state leaving it).  0 for invalid sizes.
  */
 size_t gdn_prefill_bwd_workspace_bytes(int N, int T, int HQ, int HV);

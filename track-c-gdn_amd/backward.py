@@ -35,7 +35,7 @@ HEAD_SIZE = 128
 
 def workspace_bytes(N: int, T: int, HQ: int, HV: int) -> int:
     """Device workspace of :func:`gdn_prefill_backward`: per chunk slot and
-    v-head the chunk's state-gradient transition (32 KiB bf16 + 64 KiB fp32)
+    v-head the chunk's state-gradient transition (M and R, 32 KiB bf16 each)
     and the gradient of the state leaving it (32 KiB bf16)."""
     return int(_capi.lib().gdn_prefill_bwd_workspace_bytes(N, T, HQ, HV))
 

@@ -65,7 +65,7 @@ constexpr int LDA = C + 4;           // [64][64] fp32 rows (272 B)
 constexpr int kCB = C * LDK;         // elements of a [64][128] buffer
 constexpr int kTB = C * LDC;         // elements of a [64][64] buffer
 constexpr size_t kMBytes = size_t(D) * D * 2;   // M record (bf16 fragments)
-constexpr size_t kRBytes = size_t(D) * D * 4;   // R record (fp32 accumulators)
+constexpr size_t kRBytes = size_t(D) * D * 2;   // R record (bf16, accumulator layout)
 constexpr size_t kHBytes = size_t(D) * D * 2;   // dSn record (bf16 [v][k])
 constexpr int kGradThreads = 512;
 
@@ -300,9 +300,10 @@ __device__ __forceinline__ void ar_p_tiles(const uint16_t* sK, const uint16_t* s
 // lane l the 8 bf16 of M^T[16 kt + l % 16][j] at j = 32 s + 16 (e / 4) +
 // 4 (l / 16) + e % 4, e = 0..7: the A operand of the chain kernel's product
 // dS^T M-side, whose B operand is two stacked accumulator tiles of dS^T.
-// R record: R^T tiles (kt, vt), vt-major, lane l's 4 floats at 16 l: rows
-// 16 kt + 4 (l / 16) + i, column 16 vt + l % 16 -- the chain kernel's
-// accumulator layout.
+// R record: R^T tiles (kt, vt), vt-major, lane l's 4 values (bf16, 8 bytes)
+// at 8 l: rows 16 kt + 4 (l / 16) + i, column 16 vt + l % 16 -- the chain
+// kernel's accumulator layout.  bf16 like M and like the dSn operand the
+// chain multiplies by M: R enters dS = dSn M + R with the same rounding.
 template <typename CuT>
 __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const float* __restrict__ A_log,
@@ -444,7 +445,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
         acc = mfma16_bf(op_rm(sEQ, LDK, 16 * kt, 32 * s, lane), op_rm(sdO, LDK, 16 * vt, 32 * s, lane), acc);
         acc = mfma16_bf(op_rm(sBEK, LDK, 16 * kt, 32 * s, lane), op_rm(sG1, LDK, 16 * vt, 32 * s, lane), acc);
       }
-      *reinterpret_cast<f32x4*>(rr + ((vt * 8 + kt) * 64 + lane) * 16) = acc;
+      *reinterpret_cast<uint2*>(rr + ((vt * 8 + kt) * 64 + lane) * 8) =
+          uint2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
     }
   }
 }
@@ -502,15 +504,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
     for (int x = 0; x < kMCopies; ++x)
       lds_dma16_saddr(ms, uint32_t((x * kThreads + tid) * 16), &sM[buf][(x * kThreads + wave * 64) * 8]);
   };
-  auto fetch_r = [&](int ch, f32x4 (&r)[8]) {
+  auto fetch_r = [&](int ch, uint2 (&r)[8]) {
     const char* rs = rrec + rec_of(ch) * kRBytes;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
-      r[kt] = *reinterpret_cast<const f32x4*>(rs + ((vb * 8 + kt) * 64 + lane) * 16);
+      r[kt] = *reinterpret_cast<const uint2*>(rs + ((vb * 8 + kt) * 64 + lane) * 8);
   };
   // one chunk: dSn out, dS = dSn M + R (cur = R of chunk ch), and the copies
   // for chunk ch - 2 (R into nxt2, M into LDS buffer (it + 2) % 3)
-  auto step = [&](int ch, int it, f32x4 (&cur)[8], f32x4 (&nxt2)[8]) {
+  auto step = [&](int ch, int it, uint2 (&cur)[8], uint2 (&nxt2)[8]) {
     const int buf = it % 3;
     if (ch > 1) {
       copy_m(ch - 2, (it + 2) % 3);
@@ -529,7 +531,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
     for (int s = 0; s < 4; ++s) bop[s] = pack2_bf(acc[2 * s], acc[2 * s + 1]);
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
-      acc[kt] = cur[kt];
+      acc[kt] = f32x4{__uint_as_float(cur[kt].x << 16), __uint_as_float(cur[kt].x & 0xffff0000u),
+                      __uint_as_float(cur[kt].y << 16), __uint_as_float(cur[kt].y & 0xffff0000u)};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         acc[kt] = mfma16_bf(ld16_bf(&sM[buf][((kt * 4 + s) * 64 + lane) * 8]), bop[s], acc[kt]);
@@ -541,7 +544,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gdn_bwd_chain_kernel(
     else wait_vm<8>();
     lds_barrier();
   };
-  f32x4 r0[8], r1[8], r2[8];
+  uint2 r0[8], r1[8], r2[8];
   if (last >= 0) {
     copy_m(last, 0);
     fetch_r(last, r0);
