@@ -123,7 +123,7 @@ __host__ __device__ inline size_t seam_bytes(int N, int T, int HV) {
 // count of sequence order[j].  Chunk counts are clamped as the chains clamp
 // them.  Wave-uniform.
 template <typename CuT>
-__device__ int seam_count(const CuT* cu, const int* order, int N, int T, int nt_bound, int room) {
+__device__ int seam_count(const CuT* cu, const int* order, int N, int T, int room) {
   if (room <= 0) return 0;
   auto chunks_of = [&](int r) {
     const int nn = order[r];
@@ -142,7 +142,6 @@ __device__ int seam_count(const CuT* cu, const int* order, int N, int T, int nt_
       best_k = kk;
     }
   }
-  (void)nt_bound;
   return best_k;
 }
 
@@ -652,7 +651,7 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   const int base_ids = 8 * G * S * ((n_units + 7) / 8);
   // 0: the whole chain; 1: a seam's head; 2: its tail from a zero state; 3: its transition chain
   int role = 0, rank, m, s, hq;
-  const int n_seams = seam_count(cu_seqlens, order, N, T, nt_bound, seam_room_);
+  const int n_seams = seam_count(cu_seqlens, order, N, T, seam_room_);
   if (int(blockIdx.x) < base_ids) {
     const int xcd = blockIdx.x & 7, id_row = blockIdx.x >> 3;
     const int jx = id_row / (G * S);
