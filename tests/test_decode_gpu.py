@@ -93,7 +93,7 @@ def test_decode_dps_inplace_and_noncontiguous_state(device):
     _check(o3, s3, o_ref, s_ref)
 
 
-@pytest.mark.parametrize("HQ,HV", [(16, 32), (4, 4), (2, 8), (1, 8), (2, 32)])
+@pytest.mark.parametrize("HQ,HV", [(16, 32), (4, 4), (2, 8), (1, 8), (2, 32), (1, 1), (3, 6)])
 def test_decode_head_layouts(device, HQ, HV):
     dec = pkg_module("decode")
     inp = pkg_module("inputs")
