@@ -1,0 +1,89 @@
+"""Seeded random batches through every prefill path against the fp64 oracle.
+
+Each case draws a batch (1-24 sequences, lengths 0-4000 including empty
+ones and exact multiples of 64, head layout, initial states or none, int32 or
+int64 cu_seqlens) and runs it through the library's own path choice
+(``path="auto"``: the plan picks the split path or the fused kernel and, with
+CUs idle at launch, seams), the fused kernel (seams where the plan finds
+them), the fused kernel with every chain whole, and the split path at 4 and
+8 slices.  On a 256-CU GPU the 24 batches plan the split path at 4 or 8
+slices for ``"auto"`` and, for the fused kernel, 1-4 seams in 19 of them.
+Bars as the other prefill tests: output (bf16) within atol = rtol
+= 1e-2; final state relative error (Frobenius, per sequence and overall)
+<= 1e-3.
+"""
+
+import random
+
+import pytest
+import torch
+
+from conftest import pkg_module
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+STATE_REL_BAR = 1e-3
+NAMES = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+HEADS = [(4, 8), (16, 32), (1, 4), (2, 2)]
+
+
+def _case(seed):
+    r = random.Random(seed)
+    n = r.choice([1, 1, 2, 3, 5, 8, 16, 24])
+    lens = []
+    for _ in range(n):
+        kind = r.random()
+        if kind < 0.1:
+            lens.append(0)
+        elif kind < 0.3:
+            lens.append(64 * r.randint(1, 10))
+        elif kind < 0.5:
+            lens.append(r.randint(1500, 4000))   # long enough for the plans to cut
+        else:
+            lens.append(r.randint(1, 900))
+    while sum(lens) > 9000:          # keeps the oracle to a few seconds
+        lens.pop()
+    if not lens:
+        lens = [r.randint(1, 300)]
+    HQ, HV = r.choice(HEADS)
+    if HV * len(lens) > 256:
+        HQ, HV = 4, 8
+    return lens, HQ, HV, r.random() < 0.7, r.random() < 0.5
+
+
+def _check(o, s, o_ref, s_ref):
+    torch.testing.assert_close(o.float().cpu().double(), o_ref, atol=1e-2, rtol=1e-2)
+    s = s.cpu().double()
+    rel = float((s - s_ref).norm() / s_ref.norm().clamp_min(1e-300))
+    assert rel <= STATE_REL_BAR, rel
+    for n in range(s.shape[0]):
+        nr = float(s_ref[n].norm())
+        if nr > 0:
+            assert float((s[n] - s_ref[n]).norm()) / nr <= STATE_REL_BAR, n
+        else:
+            assert float(s[n].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("seed", list(range(24)))
+def test_random_batches_every_path(device, seed):
+    pre = pkg_module("prefill")
+    inp = pkg_module("inputs")
+    lens, HQ, HV, with_state, cu32 = _case(5000 + seed)
+    print(f"random prefill seed={seed} N={len(lens)} T={sum(lens)} HQ={HQ} HV={HV} "
+          f"state={with_state} cu32={cu32}", flush=True)
+    x = inp.prefill_inputs(lens, HQ, HV, seed=7000 + seed, with_state=with_state,
+                           cu_dtype=torch.int32 if cu32 else torch.int64)
+    g = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in x.items()}
+    x64 = dict(x, cu_seqlens=x["cu_seqlens"].long())
+    o_ref, s_ref = O.prefill_chunked(*[x64[n] for n in NAMES], x["scale"])
+    args = [g[n] for n in NAMES]
+    runs = [("auto", {}), ("fused", {"path": "fused"}), ("fused whole", {"path": "fused", "seams": False}),
+            ("split4", {"path": "split", "slices": 4}), ("split8", {"path": "split", "slices": 8})]
+    for name, kw in runs:
+        o, s = pre.gdn_prefill(*args, g["scale"], **kw)
+        torch.cuda.synchronize()
+        try:
+            _check(o, s, o_ref, s_ref)
+        except AssertionError as e:
+            raise AssertionError(f"path {name}: {e}") from None
