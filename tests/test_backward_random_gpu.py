@@ -1,0 +1,87 @@
+"""Seeded random batches through the prefill backward against the fp64 oracle.
+
+Each case draws 1-6 sequences (lengths 0-1100, empty ones and exact
+multiples of 64 included), a head layout, initial states or none, a
+final-state gradient or none, and int32 or int64 cu_seqlens, then runs the
+forward with h (``gdn_prefill_h``), the backward (``gdn_prefill_backward``,
+whose reverse chain splits over state rows when the chains are few) and the
+gate backward, each gradient checked against ``oracle.prefill_backward`` /
+``oracle.gate_backward`` with the bars of the other backward tests:
+relative Frobenius error <= 1e-2 and largest elementwise error <= 3e-2
+max|r|.
+"""
+
+import random
+
+import pytest
+import torch
+
+from conftest import pkg_module
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+REL_BAR = 1e-2
+MAX_BAR = 3e-2
+HEADS = [(4, 8), (2, 2), (1, 4), (16, 32)]
+
+
+def _case(seed):
+    r = random.Random(seed)
+    n = r.randint(1, 6)
+    lens = []
+    for _ in range(n):
+        kind = r.random()
+        if kind < 0.15:
+            lens.append(0)
+        elif kind < 0.35:
+            lens.append(64 * r.randint(1, 12))
+        else:
+            lens.append(r.randint(1, 1100))
+    if sum(lens) == 0:
+        lens[0] = r.randint(1, 200)
+    HQ, HV = r.choice(HEADS)
+    while sum(lens) * HV > 40000 and len(lens) > 1:   # keeps the oracle to a few seconds
+        lens.pop()
+    if sum(lens) * HV > 40000:
+        HQ, HV = 2, 2
+    return lens, HQ, HV, r.random() < 0.7, r.random() < 0.6, r.random() < 0.5
+
+
+def _check(x, r, name):
+    x = x.detach().double().cpu()
+    rel = float((x - r).norm() / r.norm().clamp_min(1e-300))
+    mx = float((x - r).abs().max())
+    assert rel <= REL_BAR, (name, rel)
+    assert mx <= MAX_BAR * float(r.abs().max()), (name, mx, float(r.abs().max()))
+
+
+@pytest.mark.parametrize("seed", list(range(12)))
+def test_random_backward(device, seed):
+    pre = pkg_module("prefill")
+    bwd = pkg_module("backward")
+    inp = pkg_module("inputs")
+    lens, HQ, HV, with_state, dfin, cu32 = _case(9000 + seed)
+    print(f"random backward seed={seed} lens={lens} HQ={HQ} HV={HV} state={with_state} "
+          f"dfin={dfin} cu32={cu32}", flush=True)
+    x = inp.prefill_inputs(lens, HQ, HV, seed=9500 + seed, with_state=with_state,
+                           cu_dtype=torch.int32 if cu32 else torch.int64)
+    T, N = sum(lens), len(lens)
+    gen = torch.Generator().manual_seed(9600 + seed)
+    d_out = torch.randn(T, HV, 128, generator=gen).to(torch.bfloat16)
+    d_fin = torch.randn(N, HV, 128, 128, generator=gen) * 0.1 if dfin else None
+    g = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in x.items()}
+    _, _, h = pre.gdn_prefill_h(*[g[n] for n in NAMES], g["scale"])
+    r = bwd.gdn_prefill_backward(g["q"], g["k"], g["v"], g["A_log"], g["a"], g["dt_bias"], g["b"],
+                                 g["cu_seqlens"], g["scale"], h, d_out.to(device),
+                                 None if d_fin is None else d_fin.to(device))
+    gg = bwd.gdn_gate_backward(g["A_log"], g["a"], g["dt_bias"], g["b"], r["dg"], r["dbeta"])
+    torch.cuda.synchronize()
+    x64 = dict(x, cu_seqlens=x["cu_seqlens"].long())
+    ref = O.prefill_backward(*[x64[n] for n in NAMES], x["scale"], d_out, d_fin)
+    for name in ("dq", "dk", "dv", "dg", "dbeta", "dh0"):
+        _check(r[name], ref[name], name)
+    gref = O.gate_backward(x["A_log"], x["a"], x["dt_bias"], x["b"], ref["dg"], ref["dbeta"])
+    for name in ("da", "db", "dA_log", "ddt_bias"):
+        _check(gg[name], gref[name], name)
