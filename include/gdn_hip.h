@@ -193,8 +193,9 @@ int gdn_prefill_auto_slices(int N, int HV);
  * gdn_prefill_ex_fwd without a workspace), whichever a cost model of the
  * launches (cycles per chunk of each kernel measured on MI355X, the split
  * path's preparation per (chunk, v-head), the slice workgroups scheduled
- * longest sequence first on `cus` CUs, one per CU) finishes first.  Only
- * batches of at most one chain per CU are considered for the split path.
+ * longest sequence first on `cus` CUs, one per CU; seams on neither path,
+ * the qk-heads being unknown here) finishes first.  Only batches of at most
+ * one chain per CU are considered for the split path.
  * `cus` <= 0: the current device's CU count.  -1 on a NULL pointer or
  * negative N / T or HV <= 0.  gdn_prefill_auto_slices decides from N and HV
  * alone and may pick the split path where the fused kernel is faster (four
@@ -208,8 +209,10 @@ int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_int32, int 
  * Launch plan of a prefill call, made on the host from a HOST copy of
  * cu_seqlens (N+1 entries; the reference's run() reads cu_seqlens back for
  * its cu_seqlens[-1] == T check, PRE:1665, so its caller holds one): the
- * path of gdn_prefill_choose_slices, and for the fused kernel the seams that
- * its cost model finds to finish first -- with at most one chain per CU, the
+ * path of gdn_prefill_choose_slices's model with each path's seams (the
+ * split path's as its launch chooses them, XCD by XCD), and for the fused
+ * kernel the seams that its cost model finds to finish first -- with at
+ * most one chain per CU, the
  * longest sequences cut at a common chunk M, their tails run (from a zero
  * state and as the transition chain) by workgroups that take the CUs shorter
  * chains free, then a seam pass (8 sequences of 2394-5348 tokens at 32

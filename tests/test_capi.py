@@ -209,6 +209,27 @@ def test_plan_on_measured_batches():
     assert (p["slices"], p["seams"]) == (0, 1) and 32 < p["split_chunk"] < 40
     # four equal chains per CU half: cutting two leaves two as long -- no seams
     assert _plan([5348] * 4, 16, 32)[2]["seams"] == 0
+    # Split seams are counted XCD by XCD (a seam's tails and transition
+    # chains are two groups of G * slices workgroups on the XCDs the chains
+    # leave free).  Batches timed on MI355X with every path in rotation:
+    # chunk counts 113, 44 at qk4/v8 -- 8 slices with one seam 96.8 us
+    # (16 chain + 16 seam workgroups on each XCD), 4 slices 107.4 us;
+    rc, _, p = _plan([113 * 64, 44 * 64], 4, 8)
+    assert (p["slices"], p["seams"]) == (8, 1)
+    # 56, 22, 8, 4 at qk4/v8 -- at 8 slices the chains fill every XCD, at 4
+    # two seams fit: 4 slices 61.9 us, 8 slices 74.6 us; without seams the
+    # model takes 8 slices
+    rc, _, p = _plan([56 * 64, 22 * 64, 8 * 64, 4 * 64], 4, 8)
+    assert (p["slices"], p["seams"]) == (4, 2)
+    assert _plan([56 * 64, 22 * 64, 8 * 64, 4 * 64], 4, 8, flags=capi.GDN_NO_SEAMS)[2]["slices"] == 8
+    # six chains at qk4/v8 at 4 slices: 24 workgroups on each XCD, one seam
+    # (8 more each) fits -- 4 slices 191.4 us, 8 slices 208.8 us
+    rc, _, p = _plan([117 * 64, 100 * 64, 84 * 64, 82 * 64, 59 * 64, 36 * 64], 4, 8)
+    assert (p["slices"], p["seams"]) == (4, 1)
+    # 118, 84 at qk16/v32: the fused kernel with two seams 231.3 us, the
+    # split path (no room for a seam at 4 or 8 slices) 258.6 / 341.8 us
+    rc, _, p = _plan([118 * 64, 84 * 64], 16, 32)
+    assert (p["slices"], p["seams"], p["split_chunk"]) == (0, 2, 61)
     # past one chain per CU, chains too short to cut, or no idle CU: no seams
     assert _plan([100] * 64, 4, 8)[2]["seams"] == 0
     assert _plan([300] * 20, 4, 8, flags=capi.GDN_PLAN_FUSED)[2]["seams"] == 0

@@ -6,8 +6,9 @@ int64 cu_seqlens) and runs it through the library's own path choice
 (``path="auto"``: the plan picks the split path or the fused kernel and, with
 CUs idle at launch, seams), the fused kernel (seams where the plan finds
 them), the fused kernel with every chain whole, and the split path at 4 and
-8 slices.  On a 256-CU GPU the 24 batches plan the split path at 4 or 8
-slices for ``"auto"`` and, for the fused kernel, 1-4 seams in 19 of them.
+8 slices.  On a 256-CU GPU the 24 batches plan, for ``"auto"``, the split
+path at 8 slices in 18 (seam slots in 14), at 4 in 3 and the fused kernel in
+3 (one with seams); the fused kernel alone cuts 1-4 seams in 19 of them.
 Bars as the other prefill tests: output (bf16) within atol = rtol
 = 1e-2; final state relative error (Frobenius, per sequence and overall)
 <= 1e-3.

@@ -1280,17 +1280,20 @@ extern "C" int gdn_prefill_split_noalloc_fwd(const uint16_t* q, const uint16_t* 
 
 namespace {
 
-// Cost model of gdn_prefill_choose_slices, in GPU cycles measured on MI355X
-// (qk16/v32 and qk4/v8 batches): per chunk of a chain, the fused kernel 7 600,
-// the slice kernel 2 550 with 16 state rows (8 slices) and 3 600 with 32 rows
-// (4 slices, the GPU filled); the split path's preparation launch 25 cycles per
-// (chunk, v-head) on 256 CUs (scaled by 256 / CUs); either path's start-up
-// about 24 000 cycles.
+// Cost model of the path choice, in cycles of the fused kernel's clock
+// (about 2.6 GHz with at most a quarter of the CUs busy), fitted to MI355X
+// timings of qk16/v32 and qk4/v8 batches (40 batches of 1-8 sequences, every
+// path timed in rotation; the model's median error 5%): per chunk of a chain,
+// the fused kernel 7 600 and the slice kernel 2 330 with 16 state rows
+// (8 slices), 2 690 with 32 (4 slices); the split path's preparation launch
+// 49 cycles per (chunk, v-head) on 256 CUs (scaled by 256 / CUs); start-up
+// 24 000 cycles for the fused launch, 27 700 for the split path's two.
 constexpr double kFusedChunkCycles = 7600.0;
-constexpr double kSlice8ChunkCycles = 2550.0;
-constexpr double kSlice4ChunkCycles = 3600.0;
-constexpr double kPrepUnitCycles256 = 25.0 * 256.0;
+constexpr double kSlice8ChunkCycles = 2330.0;
+constexpr double kSlice4ChunkCycles = 2690.0;
+constexpr double kPrepUnitCycles256 = 49.0 * 256.0;
 constexpr double kStartupCycles = 24000.0;
+constexpr double kSplitStartupCycles = 27700.0;
 constexpr int kFusedSeamMinChunks = 8;    // shortest chain a fused seam cuts
 
 // Finish time of workgroups that each hold one CU for `chunks * period`
@@ -1399,9 +1402,11 @@ FusedPlan plan_fused_seams(const CuT* cu, int N, int T, int HV, int cus, bool al
 }
 
 // Slices of the split path (4 / 8) or 0 for the fused kernel, from the modelled
-// times of the three for these lengths; the fused kernel's with the seams of fp.
+// times of the three for these lengths; the fused kernel's with the seams of
+// fp, the split path's with the seams its launch chooses on the device
+// (HQ > 0; HQ = 0: none).
 template <typename CuT>
-int choose_path(const CuT* cu, int N, int T, int HV, int cus, const FusedPlan& fp) {
+int choose_path(const CuT* cu, int N, int T, int HQ, int HV, int cus, const FusedPlan& fp) {
   const long long chains = (long long)N * HV;
   // Past one chain per CU the fused kernel fills the GPU and the split path
   // would need 4 or 8 times as many workgroups.
@@ -1421,9 +1426,16 @@ int choose_path(const CuT* cu, int N, int T, int HV, int cus, const FusedPlan& f
                        (fp.count ? kSeamPassFixedCycles + kSeamPassTokenCycles * double(tail_tokens) * HV : 0.0);
   // the slice launch takes the sequences longest first
   std::sort(chunks.begin(), chunks.end(), std::greater<int>());
-  const double prep = std::max(kStartupCycles, units * kPrepUnitCycles256 / cus);
-  const double split8 = prep + makespan(chunks, HV * 8, kSlice8ChunkCycles, cus);
-  const double split4 = prep + makespan(chunks, HV * 4, kSlice4ChunkCycles, cus);
+  const double prep = kSplitStartupCycles + units * kPrepUnitCycles256 / cus;
+  auto split = [&](int slices, double period) {
+    const int room = HQ > 0 ? gdn::prefill_split_seam_room(N, HQ, HV, slices, cus) : 0;
+    int seams = 0;
+    const int span = gdn::prefill_split_seam_span(chunks.data(), N, room, &seams);
+    // with seams every workgroup is resident: the span is the finish
+    return prep + (seams > 0 ? span * period : makespan(chunks, HV * slices, period, cus));
+  };
+  const double split8 = split(8, kSlice8ChunkCycles);
+  const double split4 = split(4, kSlice4ChunkCycles);
   if (split8 <= split4 && split8 < fused) return 8;
   if (split4 < fused) return 4;
   return 0;
@@ -1452,10 +1464,10 @@ void make_plan(const CuT* cu, int N, int T, int HQ, int HV, int cus, bool seams,
   p.HQ = HQ;
   p.HV = HV;
   p.fused = plan_fused_seams(cu, N, T, HV, cus, seams && T > 0);
-  p.slices = T > 0 && !fused_only ? choose_path(cu, N, T, HV, cus, p.fused) : 0;
+  p.slices = T > 0 && !fused_only ? choose_path(cu, N, T, seams ? HQ : 0, HV, cus, p.fused) : 0;
   if (p.slices) {
     p.fused = FusedPlan{};
-    p.split_seams = seams ? gdn::prefill_split_seam_room(N, HV, p.slices, cus) : 0;
+    p.split_seams = seams ? gdn::prefill_split_seam_room(N, HQ, HV, p.slices, cus) : 0;
     p.workspace_bytes = gdn::prefill_split_workspace_bytes(N, T, HQ, HV);
   } else {
     p.workspace_bytes = p.fused.count ? seam_region_bytes(p.fused.count, HV, p.fused.ox_rows) : 0;
@@ -1472,10 +1484,10 @@ extern "C" int gdn_prefill_choose_slices(const void* cu_seqlens_host, int cu_is_
   // the fused kernel as gdn_prefill_ex_fwd runs it without a workspace: no seams
   if (cu_is_int32) {
     const auto* cu = static_cast<const int32_t*>(cu_seqlens_host);
-    return choose_path(cu, N, T, HV, cus, plan_fused_seams(cu, N, T, HV, cus, false));
+    return choose_path(cu, N, T, 0, HV, cus, plan_fused_seams(cu, N, T, HV, cus, false));
   }
   const auto* cu = static_cast<const int64_t*>(cu_seqlens_host);
-  return choose_path(cu, N, T, HV, cus, plan_fused_seams(cu, N, T, HV, cus, false));
+  return choose_path(cu, N, T, 0, HV, cus, plan_fused_seams(cu, N, T, HV, cus, false));
 }
 
 extern "C" int gdn_prefill_plan(const void* cu_seqlens_host, int cu_is_int32, int N, int T, int HQ,

@@ -33,10 +33,16 @@ void* prefill_scratch(hipError_t* err);
 // Enqueues both launches on st; workspace holds prefill_split_workspace_bytes.
 // With h non-NULL the slices also write the bf16 state entering every chunk
 // to h[chunk_offset(n) + i] for slots below h_chunks.
-// Seam slots the split launch reserves for N sequences of HV v-heads in
-// `slices` slices on `cus` CUs (the seams themselves are chosen on the
-// device; 0: no seam pass).
-int prefill_split_seam_room(int N, int HV, int slices, int cus);
+// Seam slots the split launch reserves for N sequences of HQ qk-heads and HV
+// v-heads in `slices` slices on `cus` CUs (the seams themselves are chosen on
+// the device; 0: no seam pass).
+int prefill_split_seam_room(int N, int HQ, int HV, int slices, int cus);
+
+// The seams the split launch chooses within `room` slots for sequences of
+// these chunk counts (longest first, N of them): their count in *seams (may
+// be NULL) and the modelled finish in chunk periods of a slice (the seam
+// pass included; the longest chain's chunks without seams).
+int prefill_split_seam_span(const int* chunks_desc, int N, int room, int* seams);
 
 // Seam pass over a seam region (layout in gdn_prefill_common.h) of k_slots
 // slots and ox_rows OX rows: for the first `seams` slots, the final states

@@ -92,17 +92,47 @@ constexpr int kSeamCostChunks = 5;    // seam pass, in chunk periods of a slice
 
 __host__ __device__ inline int seam_split_chunk(int chunks) { return (chunks + 1) / 2; }
 
-// Seams the grid has room for (host and device): workgroups beyond the
-// N * HV * slices of the chains, two extra chains (tail, transition) per seam.
-__host__ __device__ inline int seam_room(int N, int HV, int slices, int cus) {
+// XCD of the first seam group: the groups continue the rotation where the
+// chains' last, partial row of units left XCDs idle (an even row fills XCDs
+// 0 .. r-1, an odd one 8-r .. 7).
+__host__ __device__ inline int seam_xcd_offset(int n_units) {
+  const int r = n_units & 7;
+  return (r == 0 || (((n_units - 1) >> 3) & 1)) ? 0 : r;
+}
+
+// Seams the grid has room for (host and device).  Every workgroup of the
+// slice launch holds a CU, and the dispatcher keeps each workgroup on the
+// XCD its id names (id mod 8), so the count is per XCD: each chain unit puts
+// G * slices workgroups on its XCD, each seam 2 HQ groups of G * slices (the
+// tails, the transition chains), and a seam is admitted only while every XCD
+// keeps at most cus / 8 of them: a tail that waited for a CU would run after
+// the head it is meant to run beside.
+__host__ __device__ inline int seam_room(int N, int HQ, int HV, int slices, int cus) {
   const long long chains = (long long)N * HV;
-  if (chains <= 0 || chains > kSeamMaxChains || cus <= 0) return 0;
-  const long long idle = (long long)cus - chains * slices;
-  if (idle <= 0) return 0;
-  long long k = idle / (2LL * HV * slices);
-  if (k > N) k = N;
-  if (k > kMaxSeams) k = kMaxSeams;
-  return int(k);
+  if (HQ <= 0 || chains <= 0 || chains > kSeamMaxChains || cus <= 0) return 0;
+  const int per_xcd = cus / 8, units = N * HQ, group = (HV / HQ) * slices;
+  int load[8] = {};
+  for (int su = 0; su < units; ++su) {
+    const int jx = su >> 3, x = su & 7;
+    load[(jx & 1) ? 7 - x : x] += group;
+  }
+  int worst = 0;
+  for (int x = 0; x < 8; ++x) worst = load[x] > worst ? load[x] : worst;
+  if (worst > per_xcd) return 0;
+  const int off = seam_xcd_offset(units);
+  const int k_max = N < kMaxSeams ? N : kMaxSeams;
+  int k = 0;
+  for (int kk = 1; kk <= k_max; ++kk) {
+    bool fits = true;
+    for (int gi = 2 * (kk - 1) * HQ; gi < 2 * kk * HQ; ++gi) {
+      int& l = load[(gi + off) & 7];
+      l += group;
+      fits = fits && l <= per_xcd;
+    }
+    if (!fits) break;
+    k = kk;
+  }
+  return k;
 }
 
 // The seam region of the split path follows the order[] ints; its slots:
@@ -122,6 +152,27 @@ __host__ __device__ inline size_t seam_bytes(int N, int T, int HV) {
 // their count; the split chunk of seam j is seam_split_chunk of the chunk
 // count of sequence order[j].  Chunk counts are clamped as the chains clamp
 // them.  Wave-uniform.
+// chunks_of(r): chunk count of the r-th longest sequence.  Returns the seam
+// count and sets *span to the modelled finish in chunk periods of a slice
+// (the longest chain's chunks without seams).  Host and device.
+template <typename ChunksOf>
+__host__ __device__ inline int seam_choice(ChunksOf chunks_of, int N, int room, int* span) {
+  const int l0 = N > 0 ? chunks_of(0) : 0;
+  int best = l0, best_k = 0;
+  for (int kk = 1; kk <= room; ++kk) {
+    if (chunks_of(kk - 1) < kSeamMinChunks) break;
+    const int rest = kk < N ? chunks_of(kk) : 0;
+    const int sp = seam_split_chunk(l0);
+    const int span_k = (sp > rest ? sp : rest) + kSeamCostChunks;
+    if (span_k < best) {
+      best = span_k;
+      best_k = kk;
+    }
+  }
+  *span = best;
+  return best_k;
+}
+
 template <typename CuT>
 __device__ int seam_count(const CuT* cu, const int* order, int N, int T, int room) {
   if (room <= 0) return 0;
@@ -131,18 +182,8 @@ __device__ int seam_count(const CuT* cu, const int* order, int N, int T, int roo
     seq_bounds(cu, nn, T, bb, ll);
     return (ll + C - 1) / C;
   };
-  const int l0 = chunks_of(0);
-  int best = l0, best_k = 0;
-  for (int kk = 1; kk <= room; ++kk) {
-    if (chunks_of(kk - 1) < kSeamMinChunks) break;
-    const int rest = kk < N ? chunks_of(kk) : 0;
-    const int span = max(seam_split_chunk(l0), rest) + kSeamCostChunks;
-    if (span < best) {
-      best = span;
-      best_k = kk;
-    }
-  }
-  return best_k;
+  int span;
+  return seam_choice(chunks_of, N, room, &span);
 }
 
 // OX rows of the seams before seam j (their tail tokens).  OX holds
@@ -638,9 +679,11 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   // for a CU land where the shortest of the first units ran.
   //
   // Workgroups past the chains' grid (ids from base_ids on) run the tails of
-  // the seams: for each seam unit (seam j, qk-head hq) 2 G S workgroups, the
-  // zero-state tail chains then the transition chains, ids 8 apart on one
-  // XCD; the seam units continue the XCD rotation after the last chain unit.
+  // the seams in groups of G S workgroups, ids 8 apart on one XCD: group 2 u
+  // of seam unit u = (seam j, qk-head hq) its zero-state tail chains, group
+  // 2 u + 1 its transition chains.  Group gi sits on XCD (gi + off) mod 8,
+  // off = seam_xcd_offset(n_units), and seam_room admits only seams whose
+  // groups leave every XCD at most one workgroup per CU.
   const int G = HV / HQ;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -666,12 +709,14 @@ __global__ __launch_bounds__(SliceCfg<NRG>::kThreads, 1) void gdn_prefill_slice_
   } else {
     const int e = int(blockIdx.x) - base_ids;
     const int xcd = e & 7, w = e >> 3;
-    const int ux = 8 * (w / (2 * G * S)) + xcd - (n_units & 7);
-    if (ux < 0 || ux >= n_seams * HQ) return;
-    const int within = w - (w / (2 * G * S)) * (2 * G * S);
-    role = 2 + within / (G * S);
-    m = (within % (G * S)) / S;
-    s = within % S;
+    const int row = w / (G * S);
+    const int gi = 8 * row + ((xcd - seam_xcd_offset(n_units)) & 7);
+    if (gi >= 2 * n_seams * HQ) return;
+    const int within = w - row * (G * S);
+    role = 2 + (gi & 1);
+    m = within / S;
+    s = within - m * S;
+    const int ux = gi >> 1;
     rank = ux / HQ;
     hq = ux - rank * HQ;
   }
@@ -1300,7 +1345,16 @@ __global__ __launch_bounds__(kSeamThreads) void gdn_prefill_seam_kernel(
 
 namespace gdn {
 
-int prefill_split_seam_room(int N, int HV, int slices, int cus) { return seam_room(N, HV, slices, cus); }
+int prefill_split_seam_room(int N, int HQ, int HV, int slices, int cus) {
+  return seam_room(N, HQ, HV, slices, cus);
+}
+
+int prefill_split_seam_span(const int* chunks_desc, int N, int room, int* seams) {
+  int span = 0;
+  const int k = seam_choice([&](int r) { return chunks_desc[r]; }, N, room, &span);
+  if (seams) *seams = k;
+  return span;
+}
 
 int prefill_seam_pass(char* region, int HV, int k_slots, int ox_rows, int seams, int max_tail_chunks,
                       uint16_t* out, float* final_state, hipStream_t st) {
@@ -1354,10 +1408,10 @@ int launch_split_t(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   // Seams (time splits of the longest chains) use the CUs the slices leave
   // idle; not with the per-chunk states (h), which the tails cannot give.
   const int cus = device_cu_count();
-  const int room = (h == nullptr && !no_seams) ? seam_room(N, HV, slices, cus > 0 ? cus : 256) : 0;
+  const int room = (h == nullptr && !no_seams) ? seam_room(N, HQ, HV, slices, cus > 0 ? cus : 256) : 0;
   const unsigned base = 8u * G * unsigned(slices) * ((units + 7u) / 8u);
-  const unsigned seam_units = unsigned(room) * unsigned(HQ) + (units & 7u);
-  const unsigned extra = room > 0 ? 8u * 2u * G * unsigned(slices) * ((seam_units + 7u) / 8u) : 0u;
+  const unsigned seam_groups = 2u * unsigned(room) * unsigned(HQ);
+  const unsigned extra = 8u * G * unsigned(slices) * ((seam_groups + 7u) / 8u);
   const dim3 grid{base + extra, 1u, 1u};
   switch (slices) {
     case 8:
