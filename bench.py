@@ -16,7 +16,11 @@ Work accounting (per v-head and per step):
 Timing: ``--warmup`` untimed steps, then ``--steps`` timed steps bracketed by
 ``torch.cuda.synchronize()`` and one pair of HIP events on the launch
 stream; a step is one kernel launch, so the mean launch duration (the
-roofline's kernel time) is the elapsed time over the step count.  Decode rotates 4 (state, new_state)
+roofline's kernel time) is the elapsed time over the step count.  Every
+object other than the headline decode also runs untimed launches for at
+least ``WARM_MS`` of GPU time first (``warm_ms`` in the line): the clock
+ramps up under load, and a compute-bound launch such as the 32k prefill
+reaches its steady time only after ~35 ms of it.  Decode rotates 4 (state, new_state)
 buffer sets (1 GiB) so the 256 MB Infinity Cache cannot serve the state.
 """
 
@@ -81,35 +85,60 @@ def _traffic(name: str, path: str = None):
     return None
 
 
-# Untimed prefill launches before the timed ones (~15 ms of work): lets the GPU
-# reach its steady clocks, which the first few launches of a run do not show.
+# Untimed prefill launches before the timed ones.
 PREFILL_WARMUP = 30
+# GPU time of back-to-back untimed launches before a timed region (at least;
+# on top of the warmup count).  Under sustained load the chip's clock ramps up
+# over tens of milliseconds and drops back within a second of idling: the
+# 32 768-token prefill launch takes ~334 us over its first 25 launches, ~278 us
+# at launches 75-99 and a steady 266-272 us from about launch 125 (~35 ms of
+# load) on; after 30 warmup launches the timed mean was 296 us, after 300 it was
+# 267 us (same box, same run).  The operator legs other than the headline
+# decode warm up for this long, so that their kernel times are the steady-state
+# ones.
+WARM_MS = 150.0
 
 
-def timed_launches(launch, n_steps: int, warmup: int):
+def timed_launches(launch, n_steps: int, warmup: int, warm_ms: float = 0.0):
     """Run ``launch(i)`` warmup + n_steps times; return (total_ms, mean_launch_ms).
 
     The timed launches run back to back on the launch stream between one
     pair of HIP events; every launch is one kernel, so the mean launch
     duration is the elapsed time over the launch count (event markers between
-    launches would insert gaps of their own).
+    launches would insert gaps of their own).  With ``warm_ms`` > 0, untimed
+    launches continue after the ``warmup`` ones until that much GPU time has
+    passed since the first of them.
     """
-    for i in range(warmup):
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    i = 0
+    for _ in range(max(warmup, 1 if warm_ms > 0 else 0)):
         launch(i)
+        i += 1
+    e1.record()
+    torch.cuda.synchronize()
+    if warm_ms > 0:
+        done = e0.elapsed_time(e1)
+        if done < warm_ms:
+            for _ in range(math.ceil((warm_ms - done) / max(done / i, 1e-3))):
+                launch(i)
+                i += 1
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record()
-    for i in range(n_steps):
-        launch(warmup + i)
+    for k in range(n_steps):
+        launch(i + k)
     t1.record()
     torch.cuda.synchronize()
     total = t0.elapsed_time(t1)
     return total, total / n_steps
 
 
-def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4, qk_l2norm=False):
+def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4, qk_l2norm=False,
+                 warm_ms=WARM_MS):
     x = ginp.decode_inputs(B, HQ, HV, seed=1001)
     g = _to(x, dev)
     states = [g["state"]] + [g["state"].clone() for _ in range(sets - 1)]
@@ -123,12 +152,12 @@ def bench_decode(dev, steps, warmup, B=256, HQ=4, HV=8, sets=4, qk_l2norm=False)
     def launch(i):
         steps_[i % sets]()
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     nbytes = decode_bytes(B, HQ, HV)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=nbytes)
 
 
-def bench_decode_pool(dev, steps, warmup, B=1024, HQ=16, HV=32):
+def bench_decode_pool(dev, steps, warmup, B=1024, HQ=16, HV=32, warm_ms=WARM_MS):
     """One decode step of batch B against a [B, HV, 128, 128] pool (slot ids a
     random permutation), updated in place."""
     x = ginp.decode_inputs(B, HQ, HV, seed=1004, with_state=False)
@@ -142,7 +171,7 @@ def bench_decode_pool(dev, steps, warmup, B=1024, HQ=16, HV=32):
         gdec.decode_pool_(g["q"], g["k"], g["v"], pool, slots, g["A_log"], g["a"], g["dt_bias"],
                           g["b"], g["scale"], output=o)
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=decode_bytes(B, HQ, HV) + 4 * B)
 
 
@@ -151,7 +180,8 @@ def decode_multi_bytes(B: int, T: int, HQ: int, HV: int) -> int:
     return B * HV * 2 * D * D * 4 + T * B * (HV * (2 * D * 2 + 4) + HQ * 2 * D * 2)
 
 
-def bench_decode_multi(dev, steps, warmup, B=256, T=4, HQ=4, HV=8, sets=4):
+def bench_decode_multi(dev, steps, warmup, B=256, T=4, HQ=4, HV=8, sets=4,
+                       warm_ms=WARM_MS):
     x = ginp.decode_multi_inputs(B, T, HQ, HV, seed=1006)
     g = _to(x, dev)
     states = [g["state"]] + [g["state"].clone() for _ in range(sets - 1)]
@@ -164,12 +194,13 @@ def bench_decode_multi(dev, steps, warmup, B=256, T=4, HQ=4, HV=8, sets=4):
     def launch(i):
         calls[i % sets]()
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, bytes=decode_multi_bytes(B, T, HQ, HV), B=B,
                 T=T)
 
 
-def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk_l2norm=False):
+def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk_l2norm=False,
+                  warm_ms=WARM_MS):
     w = ginp.WORKLOADS[name]
     lens = ginp.workload_lengths(name)
     x = ginp.prefill_inputs(lens, w["HQ"], w["HV"], seed=w["seed"], with_state=w["with_state"],
@@ -187,7 +218,7 @@ def bench_prefill(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", qk
     def launch(i):
         call()
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, T=T, N=N, lens=lens, HQ=w["HQ"],
                 HV=w["HV"], flops=prefill_flops(T, w["HV"]),
                 flops_qk_shared=prefill_flops(T, w["HV"], qk_shared=True),
@@ -200,7 +231,7 @@ OCCUPANCY_WORKLOADS = (("1x5348", [5348]), ("4x5348", [5348] * 4), ("8x5348", [5
                        ("8x64", [64] * 8))
 
 
-def bench_prefill_occupancy(dev, steps, warmup, HQ=16, HV=32):
+def bench_prefill_occupancy(dev, steps, warmup, HQ=16, HV=32, warm_ms=WARM_MS):
     res = {}
     for tag, lens in OCCUPANCY_WORKLOADS:
         x = ginp.prefill_inputs(lens, HQ, HV, seed=1004, with_state=True)
@@ -212,7 +243,7 @@ def bench_prefill_occupancy(dev, steps, warmup, HQ=16, HV=32):
                                "cu_seqlens")]
         _, kern_ms = timed_launches(
             lambda i: gpre.gdn_prefill(*args, g["scale"], output=out, final_state=fs,
-                                       validate=False, path="fused"), steps, warmup)
+                                       validate=False, path="fused"), steps, warmup, warm_ms)
         chunks = max((n + C - 1) // C for n in lens)
         res[tag] = {"chains": N * HV, "chunks_per_chain": chunks,
                     "kernel_us": round(kern_ms * 1e3, 2),
@@ -223,7 +254,7 @@ def bench_prefill_occupancy(dev, steps, warmup, HQ=16, HV=32):
 
 
 def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", path="fused",
-                    slices=8):
+                    slices=8, warm_ms=WARM_MS):
     """The prefill that also writes the state entering every chunk (bf16 h), on
     the given path (the split path with its workspace allocated once)."""
     w = ginp.WORKLOADS[name]
@@ -246,7 +277,7 @@ def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", 
         gpre.gdn_prefill(*args, g["scale"], output=out, final_state=fs, validate=False, h=h,
                          path=path, slices=slices, workspace=ws)
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     return dict(total_ms=total_ms, kernel_ms=kern_ms, chunks=NT, h_bytes=h.numel() * 2)
 
 
@@ -256,7 +287,8 @@ def bench_prefill_h(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32", 
 BWD_MFMA_PER_CHUNK_HEAD = 656 + 256 + 1360
 
 
-def bench_backward(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
+def bench_backward(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32",
+                   warm_ms=WARM_MS):
     """Backward of the prefill (gdn_prefill_bwd: transition, reverse chain,
     per-chunk gradients) from the forward's h, one C call per step."""
     w = ginp.WORKLOADS[name]
@@ -285,7 +317,7 @@ def bench_backward(dev, steps, warmup, name="prefill_varlen8_t32768_qk16_v32"):
     def launch(i):
         lib.gdn_prefill_bwd(*call)
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     flops = h.shape[0] * HV * BWD_MFMA_PER_CHUNK_HEAD * 16384
     return dict(kernel_ms=kern_ms, T=T, N=N, HQ=HQ, HV=HV, chunks=h.shape[0], flops=flops,
                 ws_bytes=need)
@@ -364,7 +396,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def bench_conv(dev, steps, warmup, HQ=16, HV=32, W=4):
+def bench_conv(dev, steps, warmup, HQ=16, HV=32, W=4, warm_ms=WARM_MS):
     """q/k/v causal conv1d + SiLU over the 32 768-token, 8-sequence workload at
     qk16 / v32 (C = 8192 channels), written as GDN's q, k, v.  Algorithmic
     bytes: x read once, q/k/v written once, conv states read and written."""
@@ -390,12 +422,12 @@ def bench_conv(dev, steps, warmup, HQ=16, HV=32, W=4):
     def launch(i):
         lib.gdn_qkv_conv1d_fwd(*args)
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     nbytes = 2 * T * C * 2 + 2 * N * C * (W - 1) * 2
     return dict(kernel_ms=kern_ms, bytes=nbytes, T=T, C=C)
 
 
-def bench_conv_update(dev, steps, warmup, B=1024, HQ=16, HV=32, W=4):
+def bench_conv_update(dev, steps, warmup, B=1024, HQ=16, HV=32, W=4, warm_ms=WARM_MS):
     """Decode conv update at batch 1024, qk16 / v32: one token per sequence,
     the [1024, 8192, 3] bf16 conv state updated in place."""
     C = 256 * HQ + 128 * HV
@@ -414,7 +446,7 @@ def bench_conv_update(dev, steps, warmup, B=1024, HQ=16, HV=32, W=4):
     def launch(i):
         lib.gdn_qkv_conv1d_update(*args)
 
-    total_ms, kern_ms = timed_launches(launch, steps, warmup)
+    total_ms, kern_ms = timed_launches(launch, steps, warmup, warm_ms)
     nbytes = 2 * B * C * 2 + 2 * B * C * (W - 1) * 2
     return dict(kernel_ms=kern_ms, bytes=nbytes, B=B, C=C)
 
@@ -530,14 +562,17 @@ def main():
     torch.cuda.set_device(dev)
 
     line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+            "warmup": args.warmup, "warm_ms": WARM_MS, "ms_per_step": None,
+            "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
             "config": {"workload": "decode_b256_qk4_v8", "batch": 256, "qk_heads": 4,
                        "v_heads": 8, "head_dim": 128, "state": "fp32 [256,8,128,128] k-last",
                        "state_buffer_sets": 4}}
 
     if args.only in ("all", "decode"):
-        r = bench_decode(dev, args.steps, args.warmup)
+        # the headline: exactly --warmup untimed steps (decode is HBM-bound; a
+        # WARM_MS warm-up moves it by under 1%)
+        r = bench_decode(dev, args.steps, args.warmup, warm_ms=0.0)
         ms = r["total_ms"] / args.steps
         gbs = r["bytes"] / (ms * 1e-3) / 1e9
         kgbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
