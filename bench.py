@@ -97,6 +97,9 @@ PREFILL_WARMUP = 30
 # decode warm up for this long, so that their kernel times are the steady-state
 # ones.
 WARM_MS = 150.0
+# at most this many extra untimed launches (short kernels reach WARM_MS only
+# after tens of thousands of launches, which measures the host instead)
+WARM_MAX_LAUNCHES = 4000
 
 
 def timed_launches(launch, n_steps: int, warmup: int, warm_ms: float = 0.0):
@@ -122,7 +125,7 @@ def timed_launches(launch, n_steps: int, warmup: int, warm_ms: float = 0.0):
     if warm_ms > 0:
         done = e0.elapsed_time(e1)
         if done < warm_ms:
-            for _ in range(math.ceil((warm_ms - done) / max(done / i, 1e-3))):
+            for _ in range(min(math.ceil((warm_ms - done) / max(done / i, 1e-3)), WARM_MAX_LAUNCHES)):
                 launch(i)
                 i += 1
     torch.cuda.synchronize()
@@ -751,7 +754,7 @@ def main():
         kus = {"decode_b256_qk4_v8": line.get("roofline", {}).get("kernel_us"),
                "prefill_t4096_n1_qk4_v8": line.get("prefill_t4096_n1_qk4_v8", {}).get("kernel_us"),
                "prefill_varlen16_qk4_v8": line.get("prefill_varlen16_qk4_v8", {}).get("kernel_us")}
-        r1 = bench_decode(dev, 50, 10, B=1, sets=1)
+        r1 = bench_decode(dev, 50, 10, B=1, sets=1, warm_ms=0.0)   # launch-bound: no warm-up
         kus["decode_b1_qk4_v8"] = round(r1["kernel_ms"] * 1e3, 2)
         line["run_latency"] = bench_run_latency(dev, kus)
         print(f"# run latency: {json.dumps(line['run_latency'])}", file=sys.stderr, flush=True)
