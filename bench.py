@@ -377,7 +377,40 @@ def bench_run_latency(dev, kernel_us, reps=50):
         g = _to(x, dev)
         record(name, lambda: gpre.run(g["q"], g["k"], g["v"], g["state"], g["A_log"], g["a"],
                                       g["dt_bias"], g["b"], g["cu_seqlens"], g["scale"]))
+    res["decode_b1_qk4_v8"]["graph_step_us"] = round(graph_decode_step_us(dev), 2)
     return res
+
+
+def graph_decode_step_us(dev, B=1, steps=32, replays=50):
+    """Decode steps at batch B replayed from one HIP graph (a serving loop's
+    way past the host cost of a call): ``steps`` prepared decode calls that
+    alternate two state buffers are captured once; the time per step over
+    ``replays`` back-to-back replays."""
+    g = _to(ginp.decode_inputs(B, 4, 8, seed=1000), dev)
+    states = [g["state"], torch.empty_like(g["state"])]
+    out = torch.empty(B, 1, 8, D, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        calls = [gdec.PreparedDecode(g["q"], g["k"], g["v"], states[i % 2], g["A_log"], g["a"],
+                                     g["dt_bias"], g["b"], g["scale"], out, states[(i + 1) % 2])
+                 for i in range(steps)]
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for c in calls:
+            c()
+    for _ in range(5):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e6 / (replays * steps)
 
 
 def cpu_model() -> str:
