@@ -146,12 +146,14 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 // bytes land at lds_dst + 16 l; lds_dst must be uniform across the wave.
 // Issued from asm so that the compiler does not wait for it at LDS accesses
 // it cannot tell apart from the destination; every consumer of the copied
-// data waits for it explicitly (wait_vm) and then crosses a barrier.
+// data waits for it explicitly (wait_vm) and then crosses a barrier.  The
+// LDS address goes in through a fixed M0 operand ("{m0}"): the compiler
+// writes M0 itself and knows what it holds; the s_nop separates that write
+// from the load that reads it.
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
   const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(lds_addr), "v"(src) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "{m0}"(lds_addr) : "memory");
 }
 
 // The same copy from base + off: base uniform (an SGPR pair), off a 32-bit
@@ -159,8 +161,8 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
 __device__ __forceinline__ void lds_dma16_saddr(const void* base, uint32_t off, void* lds_dst) {
   const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(off), "s"(base) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
 // Round-to-nearest-even fp32 pair -> packed bf16 pair (one v_cvt_pk_bf16_f32).

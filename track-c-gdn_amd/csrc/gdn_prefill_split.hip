@@ -204,10 +204,9 @@ __device__ int seam_rows_before(const CuT* cu, const int* order, int T, int j) {
 // base + off (base uniform, off a 32-bit lane offset) to LDS byte address
 // lds + 16 l for lane l (lds uniform).  Issued from asm so that the compiler
 // places no waits for it; consumers wait with explicit vmcnt counts and a
-// barrier.
+// barrier.  The LDS address is a fixed M0 operand, written by the compiler.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds), "v"(off), "s"(base) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // ---------------------------------------------------------------------------
