@@ -309,7 +309,8 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const float* __restrict__ A_log,
     const uint16_t* __restrict__ a, const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const CuT* __restrict__ cu, int N, int T, int HQ, int HV, float scale,
-    const uint16_t* __restrict__ d_out, int h_chunks, char* __restrict__ mrec, char* __restrict__ rrec) {
+    const uint16_t* __restrict__ d_out, int h_chunks, int slots, char* __restrict__ mrec,
+    char* __restrict__ rrec) {
   __shared__ __align__(16) uint16_t sK[kCB];      // K; then G0 = P^T dO
   __shared__ __align__(16) uint16_t sQ[kCB];      // Q; then W2 = Tm^T Dc K
   __shared__ __align__(16) uint16_t sdO[kCB];
@@ -323,131 +324,172 @@ __global__ __launch_bounds__(kGradThreads, 1) void gdn_bwd_prep_kernel(
   __shared__ __align__(16) float sZ[16 * 17];
   __shared__ __align__(16) float gb[GB_SZ];
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid0 = threadIdx.x, lane0 = tid0 & 63;
+  const int tid = tid0, lane = lane0;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int slot = blockIdx.x, hv = blockIdx.y;
-  if (slot >= h_chunks) return;
-  int n, ci;
-  locate_chunk(cu, N, T, slot, lane, n, ci);
-  if (n < 0) return;
-  int bos, slen;
-  seq_bounds(cu, n, T, bos, slen);
-  const int t0 = bos + C * ci;
-  const int len = min(C, slen - C * ci);
-  const int hq = hv / (HV / HQ);
-
-  {
-    GateIn gi{};
+  // Persistent workgroups (one per CU: the LDS holds one): workgroup w takes
+  // the (chunk slot, v-head) units w, w + gridDim.x, ... (slot fastest, the
+  // order of a (slots, HV) grid) and fetches the next unit's rows and gate
+  // inputs into registers while it works on one, so the HBM latency of a
+  // unit's inputs is spent inside the unit before it.
+  const int units = slots * HV;
+  auto locate = [&](int u, int& t0, int& len) {
+    const int slot = u % slots;
+    if (slot >= h_chunks) return false;
+    int n, ci;
+    locate_chunk(cu, N, T, slot, lane, n, ci);
+    if (n < 0) return false;
+    int bos, slen;
+    seq_bounds(cu, n, T, bos, slen);
+    t0 = bos + C * ci;
+    len = min(C, slen - C * ci);
+    return true;
+  };
+  auto fetch = [&](int u, int t0, int len, uint4 (&wk)[2], uint4 (&wq)[2], uint4 (&wo)[2], GateIn& gi) {
+    const int hv = u / slots, hq = hv / (HV / HQ);
     if (wave == 0) gi = gate_inputs(A_log, a, dt_bias, b, HV, hv, t0, len, lane);
-    uint4 wk[2], wq[2], wo[2];
     rows_fetch(wk, k + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
     rows_fetch(wq, q + size_t(hq) * D, size_t(HQ) * D, t0, len, tid);
     rows_fetch(wo, d_out + size_t(hv) * D, size_t(HV) * D, t0, len, tid);
-    for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
-    for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
-    rows_store(sK, wk, tid);
-    rows_store(sQ, wq, tid);
-    rows_store(sdO, wo, tid);
-    if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
-  }
-  lds_barrier();
+  };
+  uint4 wk[2], wq[2], wo[2];
+  GateIn gi{};
+  int t0 = 0, len = 0;
+  bool ok = int(blockIdx.x) < units && locate(int(blockIdx.x), t0, len);
+  if (ok) fetch(int(blockIdx.x), t0, len, wk, wq, wo, gi);
+  for (int u = int(blockIdx.x); u < units; u += int(gridDim.x)) {
+    // the next unit's inputs, in flight while this one is worked on
+    const int un = u + int(gridDim.x);
+    int t0n = 0, lenn = 0;
+    const bool okn = un < units && locate(un, t0n, lenn);
+    uint4 wkn[2], wqn[2], won[2];
+    GateIn gin{};
+    if (okn) fetch(un, t0n, lenn, wkn, wqn, won, gin);
+    if (ok) {
+      const int slot = u % slots, hv = u / slots;
+      // Lane indices opaque to the compiler at the top of each unit: their
+      // address arithmetic is formed where it is used instead of being
+      // hoisted out of the loop into registers live across every unit.
+      int tid = tid0, lane = lane0;
+      asm volatile("" : "+v"(tid), "+v"(lane));
+      for (int x = tid; x < C * LDA; x += kGradThreads) sAr[x] = 0.f;
+      for (int x = tid; x < kTB; x += kGradThreads) sP[x] = 0;
+      rows_store(sK, wk, tid);
+      rows_store(sQ, wq, tid);
+      rows_store(sdO, wo, tid);
+      if (wave == 0) chunk_gates_calc(gi, len, lane, gb);
+      lds_barrier();
 
-  // Ar, P; the scaled row copies
-  ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
-  for (int x = tid; x < C * 16; x += kGradThreads) {
-    const int r = x >> 4, cc = (x & 15) * 8;
-    const uint4 kw = *reinterpret_cast<const uint4*>(&sK[r * LDK + cc]);
-    const uint4 qw = *reinterpret_cast<const uint4*>(&sQ[r * LDK + cc]);
-    const float fd = gb[GB_DC + r], fb = gb[GB_BETA + r] * gb[GB_E + r], fq = scale * gb[GB_E + r];
-    const uint32_t kk[4] = {kw.x, kw.y, kw.z, kw.w}, qq[4] = {qw.x, qw.y, qw.z, qw.w};
-    uint32_t od[4], ob[4], oq[4];
+      // Ar, P; the scaled row copies
+      ar_p_tiles(sK, sQ, gb, scale, sAr, sP, wave, lane);
+      for (int x = tid; x < C * 16; x += kGradThreads) {
+        const int r = x >> 4, cc = (x & 15) * 8;
+        const uint4 kw = *reinterpret_cast<const uint4*>(&sK[r * LDK + cc]);
+        const uint4 qw = *reinterpret_cast<const uint4*>(&sQ[r * LDK + cc]);
+        const float fd = gb[GB_DC + r], fb = gb[GB_BETA + r] * gb[GB_E + r], fq = scale * gb[GB_E + r];
+        const uint32_t kk[4] = {kw.x, kw.y, kw.z, kw.w}, qq[4] = {qw.x, qw.y, qw.z, qw.w};
+        uint32_t od[4], ob[4], oq[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float k0, k1, q0, q1;
-      unpack_bf16x2(kk[e], k0, k1);
-      unpack_bf16x2(qq[e], q0, q1);
-      od[e] = pack_bf16x2(fd * k0, fd * k1);
-      ob[e] = pack_bf16x2(fb * k0, fb * k1);
-      oq[e] = pack_bf16x2(fq * q0, fq * q1);
-    }
-    *reinterpret_cast<uint4*>(&sDK[r * LDK + cc]) = make_uint4(od[0], od[1], od[2], od[3]);
-    *reinterpret_cast<uint4*>(&sBEK[r * LDK + cc]) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
-    *reinterpret_cast<uint4*>(&sEQ[r * LDK + cc]) = make_uint4(oq[0], oq[1], oq[2], oq[3]);
-  }
-  lds_barrier();
-
-  // Tm (wave 0) while waves 1-7 form G0 = P^T dO [t][v] over sK (K is done)
-  if (wave == 0) {
-    unit_lower_inverse(sAr, gb, sT, sZ, sTm, lane);
-  } else {
-    for (int x = wave - 1; x < 32; x += 7) {
-      const int tb = x & 3, vb = x >> 2;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < C / 32; ++s)
-        acc = mfma16_bf(op_rm(sP, LDC, 16 * tb, 32 * s, lane), op_rm(sdO, LDK, 16 * vb, 32 * s, lane), acc);
-      st_tile(sK, LDK, 16 * tb, 16 * vb, acc, lane);
-    }
-  }
-  lds_barrier();
-
-  // W2 = Tm^T Dc K -> sQ, -G1 = -Tm^T G0 -> sAr (as bf16 [64][LDK])
-  uint16_t* sG1 = reinterpret_cast<uint16_t*>(sAr);
-  {
-    const int tb = wave & 3, d0 = 4 * (wave >> 2);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int db = d0 + u;
-      f32x4 w2 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < C / 32; ++s) {
-        const bf16x8_t tmt = op_rm(sTm, LDC, 16 * tb, 32 * s, lane);
-        w2 = mfma16_bf(tmt, op_rm(sDK, LDK, 16 * db, 32 * s, lane), w2);
-        g1 = mfma16_bf(tmt, op_rm(sK, LDK, 16 * db, 32 * s, lane), g1);
+        for (int e = 0; e < 4; ++e) {
+          float k0, k1, q0, q1;
+          unpack_bf16x2(kk[e], k0, k1);
+          unpack_bf16x2(qq[e], q0, q1);
+          od[e] = pack_bf16x2(fd * k0, fd * k1);
+          ob[e] = pack_bf16x2(fb * k0, fb * k1);
+          oq[e] = pack_bf16x2(fq * q0, fq * q1);
+        }
+        *reinterpret_cast<uint4*>(&sDK[r * LDK + cc]) = make_uint4(od[0], od[1], od[2], od[3]);
+        *reinterpret_cast<uint4*>(&sBEK[r * LDK + cc]) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
+        *reinterpret_cast<uint4*>(&sEQ[r * LDK + cc]) = make_uint4(oq[0], oq[1], oq[2], oq[3]);
       }
-      st_tile(sQ, LDK, 16 * tb, 16 * db, w2, lane);
-      st_tile(sG1, LDK, 16 * tb, 16 * db, -g1, lane);
-    }
-  }
-  lds_barrier();
+      lds_barrier();
 
-  // M = e^{gam_L} I - W2^T (beta E K): tiles (jt, kt); R^T = (scale E Q)^T dO + (beta E K)^T (-G1)
-  const size_t rec = size_t(slot) * HV + hv;
-  char* mr = mrec + rec * kMBytes;
-  char* rr = rrec + rec * kRBytes;
-  const float eL = gb[GB_EL];
-  {
-    const int jt = wave;
+      // Tm (wave 0) while waves 1-7 form G0 = P^T dO [t][v] over sK (K is done)
+      if (wave == 0) {
+        unit_lower_inverse(sAr, gb, sT, sZ, sTm, lane);
+      } else {
+        for (int x = wave - 1; x < 32; x += 7) {
+          const int tb = x & 3, vb = x >> 2;
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < C / 32; ++s)
+            acc = mfma16_bf(op_rm(sP, LDC, 16 * tb, 32 * s, lane), op_rm(sdO, LDK, 16 * vb, 32 * s, lane), acc);
+          st_tile(sK, LDK, 16 * tb, 16 * vb, acc, lane);
+        }
+      }
+      lds_barrier();
+
+      // W2 = Tm^T Dc K -> sQ, -G1 = -Tm^T G0 -> sAr (as bf16 [64][LDK])
+      uint16_t* sG1 = reinterpret_cast<uint16_t*>(sAr);
+      {
+        const int tb = wave & 3, d0 = 4 * (wave >> 2);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int db = d0 + u;
+          f32x4 w2 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < C / 32; ++s) {
+            const bf16x8_t tmt = op_rm(sTm, LDC, 16 * tb, 32 * s, lane);
+            w2 = mfma16_bf(tmt, op_rm(sDK, LDK, 16 * db, 32 * s, lane), w2);
+            g1 = mfma16_bf(tmt, op_rm(sK, LDK, 16 * db, 32 * s, lane), g1);
+          }
+          st_tile(sQ, LDK, 16 * tb, 16 * db, w2, lane);
+          st_tile(sG1, LDK, 16 * tb, 16 * db, -g1, lane);
+        }
+      }
+      lds_barrier();
+
+      // M = e^{gam_L} I - W2^T (beta E K): tiles (jt, kt); R^T = (scale E Q)^T dO + (beta E K)^T (-G1)
+      const size_t rec = size_t(slot) * HV + hv;
+      char* mr = mrec + rec * kMBytes;
+      char* rr = rrec + rec * kRBytes;
+      const float eL = gb[GB_EL];
+      {
+        const int jt = wave;
 #pragma unroll 2
-    for (int kt = 0; kt < 8; ++kt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < 8; ++kt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < C / 32; ++s)
-        acc = mfma16_bf(op_rm(sQ, LDK, 16 * jt, 32 * s, lane), op_rm(sBEK, LDK, 16 * kt, 32 * s, lane), acc);
-      const int kcol = 16 * kt + (lane & 15);
-      float m[4];
+          for (int s = 0; s < C / 32; ++s)
+            acc = mfma16_bf(op_rm(sQ, LDK, 16 * jt, 32 * s, lane), op_rm(sBEK, LDK, 16 * kt, 32 * s, lane), acc);
+          const int kcol = 16 * kt + (lane & 15);
+          float m[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int jrow = 16 * jt + 4 * (lane >> 4) + i;
-        m[i] = (jrow == kcol ? eL : 0.f) - acc[i];
-      }
-      uint2 w;
-      w.x = pack_bf16x2(m[0], m[1]);
-      w.y = pack_bf16x2(m[2], m[3]);
-      *reinterpret_cast<uint2*>(mr + ((kt * 4 + (jt >> 1)) * 64 + lane) * 16 + 8 * (jt & 1)) = w;
-    }
-    const int kt = wave;
+          for (int i = 0; i < 4; ++i) {
+            const int jrow = 16 * jt + 4 * (lane >> 4) + i;
+            m[i] = (jrow == kcol ? eL : 0.f) - acc[i];
+          }
+          uint2 w;
+          w.x = pack_bf16x2(m[0], m[1]);
+          w.y = pack_bf16x2(m[2], m[3]);
+          *reinterpret_cast<uint2*>(mr + ((kt * 4 + (jt >> 1)) * 64 + lane) * 16 + 8 * (jt & 1)) = w;
+        }
+        const int kt = wave;
 #pragma unroll 2
-    for (int vt = 0; vt < 8; ++vt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int vt = 0; vt < 8; ++vt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < C / 32; ++s) {
-        acc = mfma16_bf(op_rm(sEQ, LDK, 16 * kt, 32 * s, lane), op_rm(sdO, LDK, 16 * vt, 32 * s, lane), acc);
-        acc = mfma16_bf(op_rm(sBEK, LDK, 16 * kt, 32 * s, lane), op_rm(sG1, LDK, 16 * vt, 32 * s, lane), acc);
+          for (int s = 0; s < C / 32; ++s) {
+            acc = mfma16_bf(op_rm(sEQ, LDK, 16 * kt, 32 * s, lane), op_rm(sdO, LDK, 16 * vt, 32 * s, lane), acc);
+            acc = mfma16_bf(op_rm(sBEK, LDK, 16 * kt, 32 * s, lane), op_rm(sG1, LDK, 16 * vt, 32 * s, lane), acc);
+          }
+          *reinterpret_cast<uint2*>(rr + ((vt * 8 + kt) * 64 + lane) * 8) =
+              uint2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+        }
       }
-      *reinterpret_cast<uint2*>(rr + ((vt * 8 + kt) * 64 + lane) * 8) =
-          uint2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+      // the next unit overwrites every buffer this one reads last
+      lds_barrier();
     }
+    ok = okn;
+    t0 = t0n;
+    len = lenn;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      wk[i] = wkn[i];
+      wq[i] = wqn[i];
+      wo[i] = won[i];
+    }
+    gi = gin;
   }
 }
 
@@ -1012,13 +1054,18 @@ int launch_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const fl
   char* mrec = ws;
   char* rrec = mrec + slots * HV * kMBytes;
   uint16_t* dhr = reinterpret_cast<uint16_t*>(rrec + slots * HV * kRBytes);
-  const dim3 cgrid{unsigned(slots), unsigned(HV), 1u};
-  hipLaunchKernelGGL((gdn_bwd_prep_kernel<CuT>), cgrid, dim3(kGradThreads), 0, st, q, k, A_log, a,
-                     dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h_chunks, mrec, rrec);
+  // Persistent workgroups, one per CU, when each takes many units (the next
+  // unit's inputs are then fetched during the current one); with few units
+  // per CU, one workgroup per unit, which the dispatcher balances.
+  const int cus = device_cus();
+  const size_t units = slots * size_t(HV);
+  const size_t wgs = size_t(cus > 0 ? cus : 256);
+  const unsigned pgrid = unsigned(units >= 8 * wgs ? wgs : units);
+  hipLaunchKernelGGL((gdn_bwd_prep_kernel<CuT>), dim3(pgrid), dim3(kGradThreads), 0, st, q, k, A_log, a,
+                     dt_bias, b, cu, N, T, HQ, HV, scale, d_out, h_chunks, int(slots), mrec, rrec);
   // The reverse chain: one workgroup of 8 waves per chain, or, when the
   // chains leave most CUs idle, 4 workgroups of 2 waves (32 state rows) each.
   const unsigned chain_ids = 8u * ((unsigned(N) * unsigned(HV) + 7u) / 8u);
-  const int cus = device_cus();
   if (cus > 0 && 4LL * N * HV <= cus)
     hipLaunchKernelGGL((gdn_bwd_chain_kernel<CuT, 2>), dim3(4u * chain_ids), dim3(128), 0, st, cu, N, T,
                        HV, h_chunks, mrec, rrec, d_ht, dhr, dh0);
