@@ -8,9 +8,11 @@ whose reverse chain splits over state rows when the chains are few) and the
 gate backward, each gradient checked against ``oracle.prefill_backward`` /
 ``oracle.gate_backward`` with the bars of the other backward tests:
 relative Frobenius error <= 1e-2 and largest elementwise error <= 3e-2
-max|r|.
+max|r|; the per-head sums dA_log and ddt_bias within 1e-2 of the sum of
+their terms' magnitudes.
 """
 
+import os
 import random
 
 import pytest
@@ -57,7 +59,11 @@ def _check(x, r, name):
     assert mx <= MAX_BAR * float(r.abs().max()), (name, mx, float(r.abs().max()))
 
 
-@pytest.mark.parametrize("seed", list(range(12)))
+# GDN_RANDOM_BACKWARD_SEEDS widens the sweep.
+N_SEEDS = int(os.environ.get("GDN_RANDOM_BACKWARD_SEEDS", "12"))
+
+
+@pytest.mark.parametrize("seed", list(range(N_SEEDS)))
 def test_random_backward(device, seed):
     pre = pkg_module("prefill")
     bwd = pkg_module("backward")
@@ -83,5 +89,16 @@ def test_random_backward(device, seed):
     for name in ("dq", "dk", "dv", "dg", "dbeta", "dh0"):
         _check(r[name], ref[name], name)
     gref = O.gate_backward(x["A_log"], x["a"], x["dt_bias"], x["b"], ref["dg"], ref["dbeta"])
-    for name in ("da", "db", "dA_log", "ddt_bias"):
+    for name in ("da", "db"):
         _check(gg[name], gref[name], name)
+    # dA_log and ddt_bias sum one term per token (dg g, da): the per-token
+    # errors of dg carry into the sum in proportion to the terms' magnitudes,
+    # so the bar applies to the sum of |term| per head, not to the sum, which
+    # cancellation can make much smaller (at 400 seeds, a few per-head sums
+    # came out 1-4% off while dg met its bar).  The gate kernel's own
+    # arithmetic is held to the usual bars in test_backward_gpu.py.
+    gabs = O.gate_backward(x["A_log"], x["a"], x["dt_bias"], x["b"], ref["dg"].abs(), ref["dbeta"])
+    for name in ("dA_log", "ddt_bias"):
+        err = (gg[name].detach().double().cpu() - gref[name]).abs()
+        scale = gabs[name].abs()
+        assert bool((err <= REL_BAR * scale).all()), (name, float((err / scale.clamp_min(1e-300)).max()))
